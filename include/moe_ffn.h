@@ -1,0 +1,147 @@
+/*
+ * moe_ffn.h -- C ABI of the MI355X-native MoE expert-FFN hot path (gfx950, HIP).
+ *
+ * Drop-in for the Vulkan MoE path of herlangga72/moe-680m.  Every entry point below names
+ * the reference interface it replaces (path:line in the reference tree).  The reference
+ * binds that path from Rust (src/inference.rs, src/router.rs); the matching Rust
+ * `extern "C"` block is in INTEGRATION.md.
+ *
+ * Conventions
+ *   - All tensor pointers are DEVICE pointers; the caller owns every buffer.
+ *   - Calls are asynchronous on the given HIP stream (`void*` = hipStream_t, NULL = the
+ *     legacy default stream); nothing in a hot call synchronises the host or allocates.
+ *   - Every function returns a moe_status; on failure moe_last_error() returns a message
+ *     (thread-local).  Nothing throws or aborts across this boundary.
+ *   - One context per stream/thread at a time; contexts hold no locks.
+ *   - Layout: activations f32 row-major [M][hidden]; weights GGML IQ4_XS (136-byte
+ *     super-blocks of 256 weights), row-major [out][in] (rows are outputs, K contiguous).
+ *     Weight bases and strides must be multiples of 16 bytes.
+ *   - Routing: ids u16 [M][9], w f32 [M][9].  Slots 0..7 hold the routed experts in
+ *     descending logit order, slot 8 the shared expert with id = n_experts and weight 1.
+ */
+#ifndef MOE_FFN_H
+#define MOE_FFN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct moe_ctx moe_ctx;
+
+typedef enum {
+    MOE_OK = 0,
+    MOE_EINVAL = 1,       /* bad argument (null pointer, size, alignment, layer index) */
+    MOE_ENOMEM = 2,       /* device allocation failed at create time */
+    MOE_EHIP = 3,         /* a HIP runtime call failed */
+    MOE_EUNSUPPORTED = 4, /* shape not compiled into this library */
+    MOE_EDEVICE = 5       /* a kernel flagged invalid device-side input (see moe_device_flags) */
+} moe_status;
+
+/* Weight convention of the 8 routed slots.
+ *   MOE_W_REF:    w = softmax probability (not renormalised) and every expert's output,
+ *                 the shared one included, is scaled by 1/9 -- src/router.rs:37-48,
+ *                 src/inference.rs:720,750.
+ *   MOE_W_RENORM: w renormalised over the 8 selected experts, scale 1. */
+typedef enum { MOE_W_REF = 0, MOE_W_RENORM = 1 } moe_wmode;
+
+enum { MOE_TOPK = 8, MOE_SLOTS = 9, MOE_DECODE_MAX_M = 8 };
+
+/* moe_ffn flags */
+enum {
+    MOE_FFN_ACCUMULATE = 1, /* y += out (fused residual); otherwise y = out */
+    MOE_FFN_RMSNORM = 2     /* FFN input is x / sqrt(mean(x^2) + 1e-6) (unit gain) */
+};
+
+/* Device-side input flags (sticky per context, read by moe_device_flags). */
+enum {
+    MOE_DEVFLAG_BAD_ID = 1,   /* an expert id > n_experts was seen; its slot was dropped */
+    MOE_DEVFLAG_DUP_ID = 2    /* a token named one expert in two slots; the later was dropped */
+};
+
+typedef struct {
+    int hidden;     /* 2048 for moe-680m (also 512 is compiled, for small tests) */
+    int inter;      /* 512 for moe-680m (also 256 is compiled) */
+    int n_experts;  /* routed experts, 8..1024 (256 for moe-680m); shared id = n_experts */
+    int n_layers;   /* weight tables to hold (40 for moe-680m) */
+    int m_max;      /* largest M any call will pass (<= 65535); sizes the workspaces */
+    moe_wmode wmode;
+} moe_config;
+
+/* One layer's experts.  Routed expert e: W1 at w1 + e*w1_stride, W3 at w3 + e*w3_stride,
+ * W2 at w2 + e*w2_stride.  W1, W3: [inter][hidden]; W2: [hidden][inter].
+ * Replaces LayerWeights::{expert_w1,expert_w3,expert_w2,shared_w1,shared_w3,shared_w2}
+ * (src/memory.rs:201-291, indexed layer*256+e at src/inference.rs:730,759). */
+typedef struct {
+    const void *w1, *w3, *w2;
+    size_t w1_stride, w3_stride, w2_stride;
+    const void *shared_w1, *shared_w3, *shared_w2;
+} moe_layer_weights;
+
+/* Create a context on HIP device `device`: validates the shape, allocates every
+ * workspace for m_max tokens (nothing is allocated later).
+ * Replaces the MoE slice of InferenceEngine::new (src/inference.rs:85-126) and the
+ * scratch / routing regions of ArenaLayout::compute (src/memory.rs:32-96). */
+moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out);
+moe_status moe_destroy(moe_ctx *ctx);
+
+/* Record one layer's weight table (device pointers, not copied).
+ * Replaces LayerWeights::from_registry (src/memory.rs:227-291). */
+moe_status moe_bind_layer(moe_ctx *ctx, int layer, const moe_layer_weights *lw);
+
+/* Softmax + top-8 per token: logits f32 [M][n_experts] -> ids u16 [M][9], w f32 [M][9].
+ * Ties go to the lower index; NaN logits never win and count as -inf in the softmax.
+ * Replaces shaders/router_topk.comp (dispatch src/inference.rs:608-616) and
+ * router::route_single / route_cpu (src/router.rs:13-51) as used by do_route
+ * (src/inference.rs:622-659). */
+moe_status moe_router_topk(moe_ctx *ctx, const float *logits, int M, uint16_t *ids, float *w,
+                           void *stream);
+
+/* Prefix-sum expert bucket fill over n_experts+1 buckets (bucket n_experts = shared):
+ * ranges u32 [n_experts+2], sorted_tok u16 [9M], sorted_w f32 [9M]; tokens ascend inside
+ * a bucket.  Replaces router::build_expert_batches (src/router.rs:55-97) and the upload
+ * of its output (src/inference.rs:684-699). */
+moe_status moe_bucket_fill(moe_ctx *ctx, const uint16_t *ids, const float *w, int M,
+                           uint32_t *ranges, uint16_t *sorted_tok, float *sorted_w, void *stream);
+
+/* The expert FFN of one layer for M tokens and the weighted combine:
+ *   out_t = c * sum_{s<9} w[t][s] * W2_e (silu(W1_e xin_t) * (W3_e xin_t)),  e = ids[t][s]
+ *   y_t   = (flags & ACCUMULATE ? y_t : 0) + out_t
+ * c = 1/9 (MOE_W_REF) or 1 (MOE_W_RENORM).  x and y may be the same buffer.
+ * M <= 8 runs the decode GEMV kernels (f32); larger M runs bucket fill + grouped
+ * bf16-MFMA GEMMs + combine.  Replaces record_and_submit_moe (src/inference.rs:663-766):
+ * shaders w1_w3_fused(_m1).comp, silu_mult.comp, w2(_scatter)(_m1).comp, moe_combine.comp. */
+moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids, const float *w,
+                   int M, float *y, int flags, void *stream);
+
+/* IQ4_XS decode of n_superblocks blocks into f32 [256*n] (test hook for the codec).
+ * Replaces dequant_iq4_xs (shaders/common.glsl:61-86) with the GGML 136-byte format. */
+moe_status moe_dequant_iq4xs(const void *blocks, size_t n_superblocks, float *out, void *stream);
+
+/* Synchronise the context's last stream and return (then clear) the sticky device flags.
+ * No reference counterpart: the reference panics instead (src/router.rs:41). */
+moe_status moe_device_flags(moe_ctx *ctx, void *stream, uint32_t *flags);
+
+/* Last error message of the calling thread ("" when none). */
+const char *moe_last_error(void);
+
+/* ---- seeded input generators (benchmark/test utilities, not part of the drop-in) ----
+ * Counter-based streams: element i of stream `seed` depends only on (seed, i). */
+/* IQ4_XS super-blocks first..first+n-1: uniform nibbles, uniform 6-bit scales,
+ * d = f16(|N(0,1)| * 2e-3). */
+moe_status moe_gen_iq4xs(void *dst, size_t n_superblocks, uint64_t seed, uint64_t first,
+                         void *stream);
+/* dst[i] = mean + std * N(0,1)_(first+i). */
+moe_status moe_gen_normal(float *dst, size_t n, uint64_t seed, uint64_t first, float mean,
+                          float std, void *stream);
+/* Router logits [M][E]: N(0,1) plus kind 0 none | 1 Zipf(param) bias over a seeded
+ * expert permutation | 2 with probability param a token's hot-expert logit = hot_value. */
+moe_status moe_gen_logits(float *dst, int M, int E, uint64_t seed, int kind, double param,
+                          double hot_value, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,265 @@
+"""moe680m_amd -- Python binding of the MI355X-native MoE expert-FFN path.
+
+The compute lives in ``libmoe680m.so`` (hand-written gfx950 HIP kernels behind the C ABI
+declared in ``include/moe_ffn.h``).  This module only marshals torch tensors (device
+memory and the current HIP stream) into that ABI; it has no compute of its own and no
+CPU fallback: if the shared library is missing, importing this package raises.
+
+The package directory is ``moe-680m_amd/`` (not an importable identifier), so callers
+load it by path; see ``load()`` in ``__graft_entry__.py`` and ``tests/conftest.py``.
+
+Reference interfaces mirrored (path:line in the reference tree):
+  ``Context.router_topk``  -- router::route_single / route_cpu (src/router.rs:13-51) and
+                              the GPU top-k read back by do_route (src/inference.rs:622-659)
+  ``Context.bucket_fill``  -- router::build_expert_batches (src/router.rs:55-97)
+  ``Context.ffn``          -- InferenceEngine::record_and_submit_moe (src/inference.rs:663-766)
+"""
+import ctypes
+import os
+
+import torch  # must precede the library load: it brings the process's HIP runtime
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmoe680m.so")
+
+QK = 256
+SB_BYTES = 136
+SLOTS = 9
+TOPK = 8
+DECODE_MAX_M = 8
+
+MOE_OK, MOE_EINVAL, MOE_ENOMEM, MOE_EHIP, MOE_EUNSUPPORTED, MOE_EDEVICE = range(6)
+STATUS_NAMES = {0: "MOE_OK", 1: "MOE_EINVAL", 2: "MOE_ENOMEM", 3: "MOE_EHIP",
+                4: "MOE_EUNSUPPORTED", 5: "MOE_EDEVICE"}
+W_REF, W_RENORM = 0, 1
+FFN_ACCUMULATE, FFN_RMSNORM = 1, 2
+DEVFLAG_BAD_ID, DEVFLAG_DUP_ID = 1, 2
+
+# Every symbol include/moe_ffn.h declares (checked by the CPU test suite).
+EXPORTS = (
+    "moe_create", "moe_destroy", "moe_bind_layer", "moe_router_topk", "moe_bucket_fill",
+    "moe_ffn", "moe_dequant_iq4xs", "moe_device_flags", "moe_last_error",
+    "moe_gen_iq4xs", "moe_gen_normal", "moe_gen_logits",
+)
+
+
+class MoeError(RuntimeError):
+    def __init__(self, status, message):
+        self.status = status
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
+
+
+class _Config(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_int), ("inter", ctypes.c_int), ("n_experts", ctypes.c_int),
+                ("n_layers", ctypes.c_int), ("m_max", ctypes.c_int), ("wmode", ctypes.c_int)]
+
+
+class _LayerWeights(ctypes.Structure):
+    _fields_ = [("w1", ctypes.c_void_p), ("w3", ctypes.c_void_p), ("w2", ctypes.c_void_p),
+                ("w1_stride", ctypes.c_size_t), ("w3_stride", ctypes.c_size_t),
+                ("w2_stride", ctypes.c_size_t), ("shared_w1", ctypes.c_void_p),
+                ("shared_w3", ctypes.c_void_p), ("shared_w2", ctypes.c_void_p)]
+
+
+_lib = None
+
+
+def lib():
+    """Load libmoe680m.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                          "(make -C moe-680m_amd); there is no fallback path")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, i, u64, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64, ctypes.c_size_t
+    sigs = {
+        "moe_create": [i, ctypes.POINTER(_Config), ctypes.POINTER(vp)],
+        "moe_destroy": [vp],
+        "moe_bind_layer": [vp, i, ctypes.POINTER(_LayerWeights)],
+        "moe_router_topk": [vp, vp, i, vp, vp, vp],
+        "moe_bucket_fill": [vp, vp, vp, i, vp, vp, vp, vp],
+        "moe_ffn": [vp, i, vp, vp, vp, i, vp, i, vp],
+        "moe_dequant_iq4xs": [vp, sz, vp, vp],
+        "moe_device_flags": [vp, vp, ctypes.POINTER(ctypes.c_uint32)],
+        "moe_gen_iq4xs": [vp, sz, u64, u64, vp],
+        "moe_gen_normal": [vp, sz, u64, u64, ctypes.c_float, ctypes.c_float, vp],
+        "moe_gen_logits": [vp, i, i, u64, i, ctypes.c_double, ctypes.c_double, vp],
+    }
+    for name, args in sigs.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = ctypes.c_int
+    L.moe_last_error.argtypes = []
+    L.moe_last_error.restype = ctypes.c_char_p
+    _lib = L
+    return L
+
+
+def _check(status):
+    if status != MOE_OK:
+        raise MoeError(status, lib().moe_last_error().decode(errors="replace"))
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(stream=None):
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def matrix_bytes(hidden, inter):
+    """Bytes of one IQ4_XS [inter][hidden] (or [hidden][inter]) matrix."""
+    return hidden * inter // QK * SB_BYTES
+
+
+def expert_bytes(hidden, inter):
+    """Bytes of one expert packed as w1 | w3 | w2."""
+    return 3 * matrix_bytes(hidden, inter)
+
+
+def layer_bytes(hidden, inter, n_experts):
+    """Bytes of one layer packed as experts 0..n_experts-1 then the shared expert."""
+    return (n_experts + 1) * expert_bytes(hidden, inter)
+
+
+class Context:
+    """One moe_ctx: shapes, per-layer weight tables and all workspaces."""
+
+    def __init__(self, hidden=2048, inter=512, n_experts=256, n_layers=1, m_max=512,
+                 wmode=W_REF, device=0):
+        self.hidden, self.inter, self.n_experts = hidden, inter, n_experts
+        self.n_layers, self.m_max, self.wmode, self.device = n_layers, m_max, wmode, device
+        cfg = _Config(hidden, inter, n_experts, n_layers, m_max, wmode)
+        h = ctypes.c_void_p()
+        _check(lib().moe_create(device, ctypes.byref(cfg), ctypes.byref(h)))
+        self._h = h
+        self._keep = {}
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self):
+        if self._h is not None and self._h.value:
+            _check(lib().moe_destroy(self._h))
+        self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def bind_layer(self, layer, w1, w3, w2, w1_stride, w3_stride, w2_stride,
+                   shared_w1, shared_w3, shared_w2, keep=None):
+        lw = _LayerWeights(_ptr(w1), _ptr(w3), _ptr(w2), w1_stride, w3_stride, w2_stride,
+                           _ptr(shared_w1), _ptr(shared_w3), _ptr(shared_w2))
+        _check(lib().moe_bind_layer(self._h, layer, ctypes.byref(lw)))
+        if keep is not None:
+            self._keep[layer] = keep
+
+    def bind_packed(self, layer, buf):
+        """Bind a uint8 device tensor laid out as [n_experts+1][w1|w3|w2]; the shared
+        expert is the last one."""
+        mb = matrix_bytes(self.hidden, self.inter)
+        eb = 3 * mb
+        need = (self.n_experts + 1) * eb
+        if buf.numel() < need:
+            raise ValueError(f"layer buffer has {buf.numel()} bytes, needs {need}")
+        base = buf.data_ptr()
+        sh = base + self.n_experts * eb
+        self.bind_layer(layer, base, base + mb, base + 2 * mb, eb, eb, eb,
+                        sh, sh + mb, sh + 2 * mb, keep=buf)
+
+    def router_topk(self, logits, ids=None, w=None, stream=None):
+        M = logits.shape[0]
+        if logits.shape[-1] != self.n_experts:
+            raise ValueError("logits last dimension must be n_experts")
+        if ids is None:
+            ids = torch.empty((M, SLOTS), dtype=torch.uint16, device=logits.device)
+        if w is None:
+            w = torch.empty((M, SLOTS), dtype=torch.float32, device=logits.device)
+        _check(lib().moe_router_topk(self._h, _ptr(logits), M, _ptr(ids), _ptr(w), _stream(stream)))
+        return ids, w
+
+    def bucket_fill(self, ids, w, stream=None):
+        M = ids.shape[0]
+        dev = ids.device
+        ranges = torch.empty(self.n_experts + 2, dtype=torch.int32, device=dev)
+        stok = torch.empty(max(SLOTS * M, 1), dtype=torch.uint16, device=dev)
+        sw = torch.empty(max(SLOTS * M, 1), dtype=torch.float32, device=dev)
+        _check(lib().moe_bucket_fill(self._h, _ptr(ids), _ptr(w), M, _ptr(ranges), _ptr(stok),
+                                     _ptr(sw), _stream(stream)))
+        return ranges, stok[: SLOTS * M], sw[: SLOTS * M]
+
+    def ffn(self, layer, x, ids, w, y=None, accumulate=False, rmsnorm=False, stream=None):
+        M = x.shape[0]
+        if y is None:
+            y = torch.empty_like(x)
+        flags = (FFN_ACCUMULATE if accumulate else 0) | (FFN_RMSNORM if rmsnorm else 0)
+        _check(lib().moe_ffn(self._h, layer, _ptr(x), _ptr(ids), _ptr(w), M, _ptr(y), flags,
+                             _stream(stream)))
+        return y
+
+    def device_flags(self, stream=None):
+        v = ctypes.c_uint32()
+        _check(lib().moe_device_flags(self._h, _stream(stream), ctypes.byref(v)))
+        return v.value
+
+
+def dequant_iq4xs(blocks, out=None, stream=None):
+    n = blocks.numel() // SB_BYTES
+    if out is None:
+        out = torch.empty(n * QK, dtype=torch.float32, device=blocks.device)
+    _check(lib().moe_dequant_iq4xs(_ptr(blocks), n, _ptr(out), _stream(stream)))
+    return out
+
+
+def gen_iq4xs(n_sb, seed, first=0, out=None, device="cuda", stream=None):
+    if out is None:
+        out = torch.empty(n_sb * SB_BYTES, dtype=torch.uint8, device=device)
+    _check(lib().moe_gen_iq4xs(_ptr(out), n_sb, seed & (2**64 - 1), first, _stream(stream)))
+    return out
+
+
+def gen_normal(n, seed, first=0, mean=0.0, std=1.0, out=None, device="cuda", stream=None):
+    if out is None:
+        out = torch.empty(n, dtype=torch.float32, device=device)
+    _check(lib().moe_gen_normal(_ptr(out), n, seed & (2**64 - 1), first, mean, std,
+                                _stream(stream)))
+    return out
+
+
+def gen_logits(M, E, seed, kind=0, param=0.0, hot_value=0.0, out=None, device="cuda",
+               stream=None):
+    if out is None:
+        out = torch.empty((M, E), dtype=torch.float32, device=device)
+    _check(lib().moe_gen_logits(_ptr(out), M, E, seed & (2**64 - 1), kind, param, hot_value,
+                                _stream(stream)))
+    return out
+
+
+def gen_layer(hidden, inter, n_experts, seed, out=None, device="cuda", stream=None):
+    """One layer's packed weights ([n_experts+1][w1|w3|w2]) from stream `seed`."""
+    nbytes = layer_bytes(hidden, inter, n_experts)
+    return gen_iq4xs(nbytes // SB_BYTES, seed, 0, out=out, device=device, stream=stream)
+
+
+# Seeds: base ^ (config << 48) ^ (layer << 32) ^ tensor tag.
+SEED_BASE = 0x6D6F65363830
+TAG_W, TAG_X, TAG_L = 0x57, 0x58, 0x4C
+
+
+def seed_for(config, layer, tag):
+    return SEED_BASE ^ (config << 48) ^ (layer << 32) ^ tag

@@ -1,0 +1,190 @@
+// k_decode.hip -- decode path (M <= 8): IQ4_XS-dequant GEMV kernels, f32 arithmetic.
+//
+// Replaces the reference's decode dispatches (src/inference.rs:733-762): per expert a
+// w1_w3_fused_m1 GEMV and a w2_scatter_m1 GEMV (shaders/w1_w3_fused_m1.comp,
+// shaders/w2_scatter_m1.comp), 18 dispatches and 18 barriers per layer, with SiLU fused
+// into the down projection and the combine done as an f16 read-modify-write of the
+// hidden state.  Here one layer is two launches:
+//   gate_up: every (expert, W1/W3 row pair) of the 9 selected experts, SiLU*up fused,
+//            RMSNorm of the input fused (each wave holds the whole activation row);
+//   down:    one workgroup per 8 output rows with one wave per slot, the 9 weighted
+//            contributions summed in slot order in LDS (deterministic, no atomics) and
+//            the residual added in the same store.
+// Lane mapping: a lane owns one 32-weight sub-block of a row (8-byte header load +
+// 16-byte qs load), so a 2048-wide W1 row is exactly one wave and the lane's 32
+// activations stay in registers for every row it visits.
+#include "moe_internal.hpp"
+
+namespace moe {
+
+template <int H, int I, int RP>
+__global__ __launch_bounds__(256) void k_decode_gate_up(DecodeArgs a) {
+    constexpr int SBR = H / QK;     // super-blocks per W1/W3 row
+    constexpr int LPR = SBR * 8;    // lanes per row
+    static_assert(LPR <= 64 && 64 % LPR == 0, "row must tile a wave");
+    constexpr int RPS = 64 / LPR;   // rows per wave step
+    constexpr int ROWB = SBR * SB_BYTES;
+    constexpr int RPW = RP * RPS;   // rows per wave
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int item = blockIdx.y;
+    const int e = a.ids[item];
+    if (e > a.E) {
+        if (threadIdx.x == 0 && blockIdx.x == 0) set_flag(a.flags, MOE_DEVFLAG_BAD_ID);
+        return;
+    }
+    // Only the first (token, slot) naming expert e runs; it serves every later slot that
+    // names e, so each selected expert's rows are fetched once for all tokens.
+    {
+        bool seen = false;
+        for (int p = lane; p < item; p += 64) seen |= (a.ids[p] == e);
+        if (__any(seen)) return;
+    }
+    const int gsb = lane % LPR, rr = lane / LPR;
+    const int sb = gsb >> 3, ib = gsb & 7;
+    const uint8_t *W1 = expert_w(a.L.w1, a.L.s1, a.L.sw1, e, a.E);
+    const uint8_t *W3 = expert_w(a.L.w3, a.L.s3, a.L.sw3, e, a.E);
+    const int nbase = (blockIdx.x * 4 + wv) * RPW;
+
+    u32x4 q1[RP], q3[RP];
+    u32x2 h1[RP], h3[RP];
+#pragma unroll
+    for (int r = 0; r < RP; ++r) {
+        const size_t off = (size_t)(nbase + r * RPS + rr) * ROWB + (size_t)sb * SB_BYTES;
+        h1[r] = ldg<u32x2>(W1 + off);
+        q1[r] = ldg<u32x4>(W1 + off + 8 + 16 * ib);
+        h3[r] = ldg<u32x2>(W3 + off);
+        q3[r] = ldg<u32x4>(W3 + off + 8 + 16 * ib);
+    }
+
+    const int pend = a.M * SLOTS;
+    for (int p = item; p < pend; ++p) {
+        if (a.ids[p] != e) continue;
+        // Keep the weight decode inside the token loop: hoisting the decoded floats of
+        // all rows out of it would take ~250 registers and one wave per SIMD.
+#pragma unroll
+        for (int r = 0; r < RP; ++r) asm volatile("" : "+v"(q1[r]), "+v"(q3[r]), "+v"(h1[r]), "+v"(h3[r]));
+        const int t = p / SLOTS;
+        const float *xr = a.x + (size_t)t * H + 32 * gsb;
+        float xv[32];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            f32x4 v = ldg<f32x4>(xr + 4 * i);
+            xv[4 * i + 0] = v[0];
+            xv[4 * i + 1] = v[1];
+            xv[4 * i + 2] = v[2];
+            xv[4 * i + 3] = v[3];
+        }
+        if (a.rmsnorm) {
+            float ss = 0.f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) ss = __builtin_fmaf(xv[i], xv[i], ss);
+            ss = group_sum<LPR>(ss);
+            const float inv = 1.0f / sqrtf(ss * (1.0f / (float)H) + 1e-6f);
+#pragma unroll
+            for (int i = 0; i < 32; ++i) xv[i] *= inv;
+        }
+        float xs = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) xs += xv[i];
+#pragma unroll
+        for (int r = 0; r < RP; ++r) {
+            float g = sub_scale(h1[r], ib) * subblock_dot(q1[r], xv, xs);
+            float u = sub_scale(h3[r], ib) * subblock_dot(q3[r], xv, xs);
+            g = group_sum<LPR>(g);
+            u = group_sum<LPR>(u);
+            if (gsb == 0) a.hbuf[(size_t)p * I + nbase + r * RPS + rr] = silu(g) * u;
+        }
+    }
+}
+
+template <int H, int I, int STEPS>
+__global__ __launch_bounds__(64 * SLOTS) void k_decode_down(DecodeArgs a) {
+    constexpr int SBR = I / QK;
+    constexpr int LPR = SBR * 8;
+    static_assert(LPR <= 64 && 64 % LPR == 0, "row must tile a wave");
+    constexpr int RPS = 64 / LPR;
+    constexpr int ROWB = SBR * SB_BYTES;
+    constexpr int RPW = RPS * STEPS; // output rows per workgroup
+    __shared__ float part[SLOTS][RPW];
+    const int lane = threadIdx.x & 63, s = threadIdx.x >> 6;
+    const int t = blockIdx.y;
+    const int n0 = blockIdx.x * RPW;
+    const int gsb = lane % LPR, rr = lane / LPR;
+    const int sb = gsb >> 3, ib = gsb & 7;
+    const int p = t * SLOTS + s;
+    const int e = a.ids[p];
+    float v[STEPS];
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) v[st] = 0.f;
+    if (e <= a.E) {
+        const uint8_t *W2 = expert_w(a.L.w2, a.L.s2, a.L.sw2, e, a.E);
+        u32x4 q[STEPS];
+        u32x2 hd[STEPS];
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) {
+            const size_t off = (size_t)(n0 + st * RPS + rr) * ROWB + (size_t)sb * SB_BYTES;
+            hd[st] = ldg<u32x2>(W2 + off);
+            q[st] = ldg<u32x4>(W2 + off + 8 + 16 * ib);
+        }
+        const float *hr = a.hbuf + (size_t)p * I + 32 * gsb;
+        float hv[32];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            f32x4 x4 = ldg<f32x4>(hr + 4 * i);
+            hv[4 * i + 0] = x4[0];
+            hv[4 * i + 1] = x4[1];
+            hv[4 * i + 2] = x4[2];
+            hv[4 * i + 3] = x4[3];
+        }
+        float hs = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) hs += hv[i];
+        const float wt = a.c * a.w[p];
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) {
+            float d = sub_scale(hd[st], ib) * subblock_dot(q[st], hv, hs);
+            d = group_sum<LPR>(d);
+            v[st] = wt * d;
+        }
+    } else if (lane == 0 && blockIdx.x == 0) {
+        set_flag(a.flags, MOE_DEVFLAG_BAD_ID);
+    }
+    if (gsb == 0) {
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) part[s][st * RPS + rr] = v[st];
+    }
+    __syncthreads();
+    if (threadIdx.x < RPW) {
+        const int r = threadIdx.x;
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < SLOTS; ++q) sum += part[q][r];
+        float *yp = a.y + (size_t)t * H + n0 + r;
+        *yp = (a.accumulate ? *yp : 0.f) + sum;
+    }
+}
+
+template <int H, int I>
+static hipError_t launch_decode_t(const DecodeArgs &a, hipStream_t st) {
+    constexpr int RP = 4;
+    constexpr int LPR1 = (H / QK) * 8;
+    constexpr int RPW1 = RP * (64 / LPR1);
+    static_assert(I % (4 * RPW1) == 0, "gate_up grid");
+    dim3 g1(I / (4 * RPW1), a.M * SLOTS);
+    hipLaunchKernelGGL((k_decode_gate_up<H, I, RP>), g1, dim3(256), 0, st, a);
+    constexpr int STEPS = 2;
+    constexpr int LPR2 = (I / QK) * 8;
+    constexpr int RPW2 = (64 / LPR2) * STEPS;
+    static_assert(H % RPW2 == 0, "down grid");
+    dim3 g2(H / RPW2, a.M);
+    hipLaunchKernelGGL((k_decode_down<H, I, STEPS>), g2, dim3(64 * SLOTS), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode(int H, int I, const DecodeArgs &a, hipStream_t st) {
+    if (H == 2048 && I == 512) return launch_decode_t<2048, 512>(a, st);
+    if (H == 512 && I == 256) return launch_decode_t<512, 256>(a, st);
+    return hipErrorInvalidValue;
+}
+
+} // namespace moe

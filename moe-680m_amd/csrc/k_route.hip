@@ -1,0 +1,287 @@
+// k_route.hip -- router softmax + top-8 and the prefix-sum expert bucket fill.
+#include "moe_internal.hpp"
+
+namespace moe {
+
+// ---------------------------------------------------------------- router top-8
+// One 64-lane wave per token.  Replaces shaders/router_topk.comp, whose 256-lane workgroup
+// ran two 8-step LDS tree reductions and a serial insertion sort on lane 0
+// (router_topk.comp:37-85).  Here each lane keeps E/64 logits in registers, the eight
+// winners come from eight wave-wide max reductions on a 64-bit key (order-preserving f32
+// bits : inverted index, so the lower index wins ties exactly like the shader's strict
+// '>' insertion at router_topk.comp:76), and the softmax sum is one wave reduction.
+
+__device__ __forceinline__ float router_key(float v) {
+    if (v != v) v = -INFINITY; // NaN never wins and weighs 0 unless every logit is -inf/NaN
+    if (v == 0.0f) v = 0.0f;   // -0 ties with +0
+    return v;
+}
+__device__ __forceinline__ uint32_t ord32(float v) {
+    uint32_t b = __builtin_bit_cast(uint32_t, v);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float unord32(uint32_t o) {
+    uint32_t b = (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o;
+    return __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        uint32_t lo = __shfl_xor((uint32_t)v, off);
+        uint32_t hi = __shfl_xor((uint32_t)(v >> 32), off);
+        uint64_t o = ((uint64_t)hi << 32) | lo;
+        v = o > v ? o : v;
+    }
+    return v;
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+
+constexpr int RT_MAXV = 16; // E <= 1024
+
+__global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ logits, int M, int E,
+                                                     int renorm, uint16_t *__restrict__ ids,
+                                                     float *__restrict__ w) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= M) return; // whole wave leaves together
+    const float *l = logits + (size_t)t * E;
+    float kf[RT_MAXV];
+#pragma unroll
+    for (int j = 0; j < RT_MAXV; ++j) {
+        int i = lane + 64 * j;
+        kf[j] = (i < E) ? router_key(l[i]) : -INFINITY;
+    }
+    uint32_t taken = 0;
+    int sel[TOPK];
+    uint32_t selord[TOPK];
+#pragma unroll
+    for (int r = 0; r < TOPK; ++r) {
+        uint64_t best = 0;
+#pragma unroll
+        for (int j = 0; j < RT_MAXV; ++j) {
+            int i = lane + 64 * j;
+            if (i < E && !((taken >> j) & 1u)) {
+                uint64_t k = ((uint64_t)ord32(kf[j]) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i);
+                best = k > best ? k : best;
+            }
+        }
+        best = wave_max_u64(best);
+        int idx = (int)(0xFFFFFFFFu - (uint32_t)best);
+        if ((idx & 63) == lane) taken |= 1u << (idx >> 6);
+        sel[r] = idx;
+        selord[r] = (uint32_t)(best >> 32);
+    }
+    const float m = unord32(selord[0]);
+    float zs = 0.f;
+#pragma unroll
+    for (int j = 0; j < RT_MAXV; ++j) {
+        int i = lane + 64 * j;
+        if (i < E) zs += (kf[j] == m) ? 1.0f : expf(kf[j] - m);
+    }
+    const float Z = group_sum<64>(zs);
+    float e8[TOPK];
+    float s8 = 0.f;
+#pragma unroll
+    for (int r = 0; r < TOPK; ++r) {
+        float k = unord32(selord[r]);
+        e8[r] = (k == m) ? 1.0f : expf(k - m);
+        s8 += e8[r];
+    }
+    const float den = renorm ? s8 : Z;
+    if (lane < TOPK) {
+        float ev = e8[0];
+        int id = sel[0];
+#pragma unroll
+        for (int r = 1; r < TOPK; ++r)
+            if (lane == r) { ev = e8[r]; id = sel[r]; }
+        ids[(size_t)t * SLOTS + lane] = (uint16_t)id;
+        w[(size_t)t * SLOTS + lane] = ev / den;
+    } else if (lane == TOPK) {
+        ids[(size_t)t * SLOTS + TOPK] = (uint16_t)E;
+        w[(size_t)t * SLOTS + TOPK] = 1.0f;
+    }
+}
+
+hipError_t launch_router_topk(const float *logits, int M, int E, int renorm, uint16_t *ids, float *w,
+                              hipStream_t st) {
+    if (M <= 0) return hipSuccess;
+    dim3 grid((unsigned)((M + 3) / 4));
+    hipLaunchKernelGGL(k_router_topk, grid, dim3(256), 0, st, logits, M, E, renorm, ids, w);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- bucket fill
+// Stable counting sort of the 9M (token, slot) pairs into E+1 buckets, replacing the CPU
+// loop of src/router.rs:55-97 plus its per-layer upload (src/inference.rs:684-699).
+// Tokens are taken 64 at a time (one per lane); inside such a chunk each bucket is a
+// 64-bit LDS bitmap of the lanes that named it, so the stable rank of token t inside its
+// chunk is popcount(bitmap & lanes-below-t).  Chunk counts get an exclusive scan per
+// bucket, the bucket totals a scan over buckets (ranges), and the scatter writes each slot
+// to ranges[e] + chunk offset + in-chunk rank: tokens ascend within a bucket, as in the
+// reference's cursor fill.  One 1024-thread workgroup; no inter-workgroup synchronisation.
+// The same pass writes the grouped-GEMM tile list (tile_bm slots per tile).
+constexpr int BF_THREADS = 1024;
+constexpr int BF_BITMAP_BYTES = 48 * 1024;
+
+__host__ __device__ inline int bucket_cw(int E1) {
+    int cw = BF_BITMAP_BYTES / (E1 * 8);
+    return cw > 16 ? 16 : (cw < 1 ? 1 : cw);
+}
+__host__ inline size_t bucket_smem(int E1) {
+    return (size_t)bucket_cw(E1) * E1 * 8 + 3 * (size_t)(E1 + 1) * 4;
+}
+
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        uint32_t o = __shfl_up(v, off);
+        if (lane >= off) v += o;
+    }
+    return v;
+}
+
+__global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
+    extern __shared__ uint32_t smem[];
+    __shared__ uint32_t s_flags;
+    const int E1 = a.E1, M = a.M;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int nch = (M + 63) / 64;
+    const int CW = bucket_cw(E1);
+    uint32_t *bm_all = smem;
+    uint32_t *tot = smem + (size_t)CW * E1 * 2;
+    uint32_t *rg = tot + (E1 + 1);
+    uint32_t *ts = rg + (E1 + 1);
+    if (tid == 0) s_flags = 0;
+
+    // Phase 1: per-chunk bucket counts.
+    for (int base = 0; base < nch; base += CW) {
+        const int c = base + wv;
+        const bool active = (wv < CW) && (c < nch);
+        uint32_t *bm = bm_all + (size_t)(wv < CW ? wv : 0) * E1 * 2;
+        if (active)
+            for (int i = lane; i < 2 * E1; i += 64) bm[i] = 0;
+        __syncthreads();
+        if (active) {
+            const int t = c * 64 + lane;
+            if (t < M) {
+                uint32_t f = 0;
+                for (int s = 0; s < SLOTS; ++s) {
+                    int e = a.ids[(size_t)t * SLOTS + s];
+                    if (e >= E1) { f |= MOE_DEVFLAG_BAD_ID; continue; }
+                    uint32_t bit = 1u << (lane & 31);
+                    uint32_t old = atomicOr(&bm[2 * e + (lane >> 5)], bit);
+                    if (old & bit) f |= MOE_DEVFLAG_DUP_ID;
+                }
+                if (f) atomicOr(&s_flags, f);
+            }
+        }
+        __syncthreads();
+        if (active)
+            for (int e = lane; e < E1; e += 64)
+                a.chunk_cnt[(size_t)c * E1 + e] = __popc(bm[2 * e]) + __popc(bm[2 * e + 1]);
+        __syncthreads();
+    }
+
+    // Phase 2a: exclusive scan of each bucket's chunk counts (in place), bucket totals.
+    for (int e = tid; e < E1; e += BF_THREADS) {
+        uint32_t run = 0;
+        for (int c = 0; c < nch; ++c) {
+            uint32_t v = a.chunk_cnt[(size_t)c * E1 + e];
+            a.chunk_cnt[(size_t)c * E1 + e] = run;
+            run += v;
+        }
+        tot[e] = run;
+    }
+    __syncthreads();
+
+    // Phase 2b: scan over buckets -> ranges; tile counts -> tile starts (wave 0).
+    if (wv == 0) {
+        uint32_t carry = 0, tcarry = 0;
+        for (int base = 0; base < E1; base += 64) {
+            const int e = base + lane;
+            uint32_t v = (e < E1) ? tot[e] : 0u;
+            uint32_t nt = (v + (uint32_t)a.tile_bm - 1u) / (uint32_t)a.tile_bm;
+            uint32_t inc = wave_incl_scan(v, lane);
+            uint32_t tinc = wave_incl_scan(nt, lane);
+            if (e < E1) {
+                rg[e] = carry + inc - v;
+                ts[e] = tcarry + tinc - nt;
+            }
+            carry += __shfl(inc, 63);
+            tcarry += __shfl(tinc, 63);
+        }
+        if (lane == 0) {
+            rg[E1] = carry;
+            ts[E1] = tcarry;
+        }
+    }
+    __syncthreads();
+
+    for (int e = tid; e <= E1; e += BF_THREADS) a.ranges[e] = rg[e];
+    if (a.tiles) {
+        for (int e = tid; e < E1; e += BF_THREADS) {
+            const int n = (int)tot[e];
+            for (int j = 0; j * a.tile_bm < n; ++j) {
+                Tile tl;
+                tl.expert = e;
+                tl.row0 = (int)rg[e] + j * a.tile_bm;
+                tl.nrows = min(a.tile_bm, n - j * a.tile_bm);
+                tl.pad = 0;
+                a.tiles[ts[e] + j] = tl;
+            }
+        }
+        for (int i = (int)ts[E1] + tid; i < a.tile_max; i += BF_THREADS) a.tiles[i] = Tile{-1, 0, 0, 0};
+    }
+
+    // Phase 3: rebuild each chunk's bitmaps and scatter.
+    for (int base = 0; base < nch; base += CW) {
+        const int c = base + wv;
+        const bool active = (wv < CW) && (c < nch);
+        uint32_t *bm = bm_all + (size_t)(wv < CW ? wv : 0) * E1 * 2;
+        if (active)
+            for (int i = lane; i < 2 * E1; i += 64) bm[i] = 0;
+        __syncthreads();
+        const int t = c * 64 + lane;
+        uint32_t ok = 0;
+        if (active && t < M) {
+            for (int s = 0; s < SLOTS; ++s) {
+                int e = a.ids[(size_t)t * SLOTS + s];
+                if (e >= E1) continue;
+                uint32_t bit = 1u << (lane & 31);
+                uint32_t old = atomicOr(&bm[2 * e + (lane >> 5)], bit);
+                if (!(old & bit)) ok |= 1u << s;
+            }
+        }
+        __syncthreads();
+        if (active && t < M) {
+            const uint32_t below = (1u << (lane & 31)) - 1u;
+            for (int s = 0; s < SLOTS; ++s) {
+                uint32_t p = 0xFFFFFFFFu;
+                if ((ok >> s) & 1u) {
+                    int e = a.ids[(size_t)t * SLOTS + s];
+                    uint32_t rank = __popc(bm[2 * e + (lane >> 5)] & below) +
+                                    ((lane >> 5) ? __popc(bm[2 * e]) : 0u);
+                    p = rg[e] + a.chunk_cnt[(size_t)c * E1 + e] + rank;
+                    a.sorted_tok[p] = (uint16_t)t;
+                    a.sorted_w[p] = a.w[(size_t)t * SLOTS + s];
+                }
+                if (a.pos) a.pos[(size_t)t * SLOTS + s] = p;
+            }
+        }
+        __syncthreads();
+    }
+    if (tid == 0 && s_flags) set_flag(a.flags, s_flags);
+}
+
+hipError_t launch_bucket_fill(const BucketArgs &a, hipStream_t st) {
+    if (a.M < 0) return hipSuccess; // M == 0 still writes all-zero ranges
+    size_t smem = bucket_smem(a.E1);
+    hipLaunchKernelGGL(k_bucket_fill, dim3(1), dim3(BF_THREADS), smem, st, a);
+    return hipGetLastError();
+}
+
+} // namespace moe
