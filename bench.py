@@ -1,0 +1,272 @@
+#!/usr/bin/env python3
+"""bench.py -- the MoE expert-FFN hot path of moe-680m on one MI355X.
+
+Metric: "MoE-FFN decode HBM GB/s (% of peak) @M=1; prefill tok/s @M=512
+(% MFMA)".  One step = one token (M=1) through the 40-layer MoE-FFN stack of config 2:
+per layer router softmax/top-8 over seeded logits, RMSNorm + the 9-expert IQ4_XS FFN +
+weighted combine + residual.  All 40 x 257 experts (17.2 GB) are resident in HBM and
+every step routes differently, so weights stream from HBM.  `value` is algorithmic bytes
+(602,316,800 per token) / wall time.  The prefill leg (config 1: M=512, Zipf(1.1)-biased
+router) is reported in the same line, with tok/s and the bf16 MFMA fraction.
+
+    python bench.py [--steps K] [--warmup W]      # one JSON line on stdout
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+
+H, I, E, LAYERS = 2048, 512, 256, 40
+EXPERT_BYTES = 3 * (H * I // 256 * 136)                     # 1,671,168
+DECODE_BYTES_PER_LAYER = 9 * EXPERT_BYTES + H * 4 + E * 4 + H * 4   # 15,057,920
+DECODE_BYTES_PER_TOKEN = LAYERS * DECODE_BYTES_PER_LAYER     # 602,316,800
+PREFILL_M = 512
+PREFILL_FLOPS = 2 * (9 * PREFILL_M) * 3 * I * H             # 28,991,029,248
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def load_pkg():
+    sys.path.insert(0, ROOT)
+    import __graft_entry__
+    return __graft_entry__.load()
+
+
+def capture(torch, fn):
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+def cpu_baseline(pkg, layer_dev, seconds):
+    """The oracle (C, OpenMP) on the host: decode M=1 token-layers of the same workload,
+    one resident layer, fresh routing per token, for about `seconds`."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    host = oracle.PackedLayer(layer_dev.cpu().numpy(), H, I, E)
+    n_tok = 256
+    x = oracle.gen_normal(pkg.seed_for(0, 0, pkg.TAG_X), 0, n_tok * H).reshape(n_tok, H)
+    logits = oracle.gen_logits(pkg.seed_for(0, 0, pkg.TAG_L), n_tok, E)
+    done, t0 = 0, time.perf_counter()
+    while True:
+        t = done % n_tok
+        lg = oracle.router_topk(logits[t:t + 1], oracle.W_REF)
+        oracle.moe_ffn(host, x[t:t + 1], lg[0], lg[1], 1.0 / 9, oracle.RMSNORM | oracle.ACCUMULATE,
+                       y=x[t:t + 1])
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    gbs = done * DECODE_BYTES_PER_LAYER / el / 1e9
+    threads = min(oracle.num_threads(), 9)  # one OpenMP task per selected expert
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{done} decode token-layers (M=1, router + RMSNorm + 9-expert FFN + "
+                      f"residual) of one resident layer in {el:.1f} s; f64 oracle, OpenMP over "
+                      f"the 9 experts; host {platform.processor() or platform.machine()}, "
+                      f"nproc {os.cpu_count()}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--prefill-steps", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="run a plain device copy of this size first (scales PMC byte counters)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        log("bench.py measures one GPU only: this build has no multi-GPU path "
+            "(the sharding design is in DESIGN.md); run with --gpus 1")
+        sys.exit(2)
+
+    import torch
+    pkg = load_pkg()
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda:0")
+    props = torch.cuda.get_device_properties(0)
+    log(f"device: {props.name}, {props.multi_processor_count} CUs")
+
+    if args.copy_calibration_mib:
+        n = args.copy_calibration_mib << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy: {n} bytes read, {n} bytes written")
+        del src, dst
+
+    K, W = args.steps, args.warmup
+    ctx = pkg.Context(H, I, E, LAYERS, PREFILL_M, pkg.W_REF)
+    t0 = time.perf_counter()
+    layers = []
+    for l in range(LAYERS):
+        buf = pkg.gen_layer(H, I, E, pkg.seed_for(2, l, pkg.TAG_W))
+        ctx.bind_packed(l, buf)
+        layers.append(buf)
+    torch.cuda.synchronize()
+    log(f"generated {LAYERS} layers x {E + 1} experts ({LAYERS * (E + 1) * EXPERT_BYTES / 1e9:.2f} GB) "
+        f"in {time.perf_counter() - t0:.2f} s")
+
+    # ---------------------------------------------------------------- decode (config 2)
+    # One step = one token through the 40 layers in one moe_decode_stack launch (routing
+    # from that token's per-layer logits, RMSNorm + MoE + residual per layer).
+    nsteps = W + K
+    logits = pkg.gen_logits(nsteps * LAYERS, E, pkg.seed_for(2, 0, pkg.TAG_L)).view(nsteps, LAYERS, E)
+    x = pkg.gen_normal(H, pkg.seed_for(2, 0, pkg.TAG_X))
+    ids = torch.empty((LAYERS, 9), dtype=torch.uint16, device=dev)
+    wts = torch.empty((LAYERS, 9), dtype=torch.float32, device=dev)
+
+    def token(s):
+        ctx.decode_stack(0, x, logits[s], y=x, ids=ids, w=wts, rmsnorm=True)
+
+    token(0)  # eager first pass (also checks the call path before capture)
+    torch.cuda.synchronize()
+    assert ctx.device_flags() == 0, "decode stack raised a device flag"
+    graphs = [capture(torch, lambda s=s: token(s)) for s in range(nsteps)]
+    for s in range(W):
+        graphs[s].replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for s in range(W, nsteps):
+        graphs[s].replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / K
+    decode_gbs = DECODE_BYTES_PER_TOKEN / (ms_step * 1e-3) / 1e9
+    log(f"decode: {ms_step * 1e3:.1f} us/token ({ev0.elapsed_time(ev1) * 1e3 / K:.1f} us by events), "
+        f"{decode_gbs:.1f} GB/s = {100 * decode_gbs / HBM_PEAK_GBS:.1f}% of HBM peak")
+    assert torch.isfinite(x).all(), "decode chain produced non-finite values"
+    assert ctx.device_flags() == 0, "decode stack raised a device flag"
+    del graphs
+
+    # per-kernel HIP-event timing of the same token steps, launched eagerly
+    ctx.timing_enable(64)
+    for s in range(W, min(nsteps, W + 8)):
+        token(s)
+    kt = ctx.timing_read()
+    ctx.timing_enable(0)
+    kern = {k: {"launches": n, "avg_us": round(ms * 1e3 / n, 3)} for k, (n, ms) in kt.items()}
+    stack_us = kern["decode_stack"]["avg_us"]
+    stack_gbs = DECODE_BYTES_PER_TOKEN / (stack_us * 1e-6) / 1e9
+    log(f"decode kernels: {kern}")
+
+    # the per-layer entry points (router + moe_ffn), for reference
+    xl = x.clone().view(1, H)
+    ctx.timing_enable(8 * LAYERS * 4)
+    for s in range(W, min(nsteps, W + 2)):
+        for l in range(LAYERS):
+            ctx.router_topk(logits[s, l:l + 1], ids[l:l + 1], wts[l:l + 1])
+            ctx.ffn(l, xl, ids[l:l + 1], wts[l:l + 1], y=xl, accumulate=True, rmsnorm=True)
+    lkt = ctx.timing_read()
+    ctx.timing_enable(0)
+    layer_kern = {k: {"launches": n, "avg_us": round(ms * 1e3 / n, 3)} for k, (n, ms) in lkt.items()}
+    log(f"per-layer path kernels: {layer_kern}")
+
+    # ---------------------------------------------------------------- prefill (config 1)
+    PK = args.prefill_steps
+    pw = 3
+    pn = pw + PK
+    xp = pkg.gen_normal(PREFILL_M * H, pkg.seed_for(1, 0, pkg.TAG_X)).view(PREFILL_M, H)
+    yp = torch.empty_like(xp)
+    plog = pkg.gen_logits(pn * PREFILL_M, E, pkg.seed_for(1, 0, pkg.TAG_L), 1, 1.1).view(pn, PREFILL_M, E)
+    pids = torch.empty((pn, PREFILL_M, 9), dtype=torch.uint16, device=dev)
+    pw_ = torch.empty((pn, PREFILL_M, 9), dtype=torch.float32, device=dev)
+
+    def prefill(s):
+        ctx.router_topk(plog[s], pids[s], pw_[s])
+        ctx.ffn(s % LAYERS, xp, pids[s], pw_[s], y=yp)
+
+    prefill(0)
+    torch.cuda.synchronize()
+    pgraphs = [capture(torch, lambda s=s: prefill(s)) for s in range(pn)]
+    for s in range(pw):
+        pgraphs[s].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(pw, pn):
+        pgraphs[s].replay()
+    torch.cuda.synchronize()
+    pwall = time.perf_counter() - t0
+    p_ms = pwall * 1e3 / PK
+    p_tflops = PREFILL_FLOPS / (p_ms * 1e-3) / 1e12
+    active = [int(torch.unique(pids[s].view(-1).to(torch.int32)).numel()) for s in range(pw, pn)]
+    log(f"prefill M={PREFILL_M}: {p_ms * 1e3:.1f} us/step, {PREFILL_M / (p_ms * 1e-3):.0f} tok/s, "
+        f"{p_tflops:.1f} TFLOP/s = {100 * p_tflops / BF16_PEAK_TFLOPS:.2f}% of bf16 MFMA peak; "
+        f"active experts {min(active)}-{max(active)}")
+    del pgraphs
+    ctx.timing_enable(8 * 64)
+    for s in range(pw, min(pn, pw + 8)):
+        prefill(s)
+    pkt = ctx.timing_read()
+    ctx.timing_enable(0)
+    pkern = {k: {"launches": n, "avg_us": round(ms * 1e3 / n, 3)} for k, (n, ms) in pkt.items()}
+    log(f"prefill kernels: {pkern}")
+    # dominant prefill kernel: gate/up carries 2/3 of the FLOPs
+    pgu_us = pkern["prefill_gate_up"]["avg_us"]
+    pgu_tflops = (PREFILL_FLOPS * 2 / 3) / (pgu_us * 1e-6) / 1e12
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(pkg, layers[0], args.cpu_seconds)
+        log(f"cpu baseline: {cpu}")
+
+    out = {
+        "metric": "MoE-FFN decode HBM GB/s (% of peak) @M=1; prefill tok/s @M=512 (% MFMA)",
+        "value": round(decode_gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded IQ4_XS weights, N(0,1) activations and router logits; "
+                "random-init, no checkpoint)",
+        "config": {"workload": "config 2: 40-layer MoE-FFN decode stack, M=1 token/step, "
+                               "hidden 2048, 256+1 experts (top-8 + shared), inter 512, IQ4_XS, "
+                               "all 10,280 experts resident (17.19 GB)",
+                   "bytes_per_step": DECODE_BYTES_PER_TOKEN, "tokens_per_step": 1},
+        "hbm_peak_frac": round(decode_gbs / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "kernel": "decode_stack", "achieved": round(stack_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(stack_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_per_launch": DECODE_BYTES_PER_TOKEN, "avg_us": stack_us},
+        "kernels": kern,
+        "per_layer_path_kernels": layer_kern,
+        "prefill": {"workload": "config 1: M=512, Zipf(1.1) router bias, one layer per step "
+                                "(cycling the 40 resident layers)",
+                    "dtype": "bf16 MFMA, f32 accumulate", "ms_per_step": round(p_ms, 5),
+                    "tok_per_s": round(PREFILL_M / (p_ms * 1e-3), 1),
+                    "tflops": round(p_tflops, 2), "mfma_frac": round(p_tflops / BF16_PEAK_TFLOPS, 4),
+                    "active_experts": [min(active), max(active)],
+                    "roofline": {"bound": "mfma", "kernel": "prefill_gate_up",
+                                 "achieved": round(pgu_tflops, 2), "peak": BF16_PEAK_TFLOPS,
+                                 "unit": "TFLOP/s", "frac": round(pgu_tflops / BF16_PEAK_TFLOPS, 4),
+                                 "avg_us": pgu_us},
+                    "kernels": pkern},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

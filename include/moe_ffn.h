@@ -58,7 +58,8 @@ enum {
 /* Device-side input flags (sticky per context, read by moe_device_flags). */
 enum {
     MOE_DEVFLAG_BAD_ID = 1,   /* an expert id > n_experts was seen; its slot was dropped */
-    MOE_DEVFLAG_DUP_ID = 2    /* a token named one expert in two slots; the later was dropped */
+    MOE_DEVFLAG_DUP_ID = 2,   /* a token named one expert in two slots; the later was dropped */
+    MOE_DEVFLAG_TIMEOUT = 4   /* moe_decode_stack: a bounded wait expired; its output is invalid */
 };
 
 typedef struct {
@@ -116,6 +117,22 @@ moe_status moe_bucket_fill(moe_ctx *ctx, const uint16_t *ids, const float *w, in
 moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids, const float *w,
                    int M, float *y, int flags, void *stream);
 
+/* One token (M = 1) through n_layers consecutive MoE layers in one persistent launch:
+ *   for l in layer0 .. layer0+n_layers-1:
+ *       (ids_l, w_l) = top8(softmax(logits[l - layer0]))      (as moe_router_topk)
+ *       x = x + c * sum_{s<9} w_l[s] * FFN_{ids_l[s]}(xin),  xin = RMSNorm(x) if asked
+ *   y = x  (y may be the same buffer as x)
+ * logits f32 [n_layers][n_experts]; ids u16 / w f32 [n_layers][9] receive the routing
+ * (both may be NULL).  flags: MOE_FFN_RMSNORM (the residual is always added).
+ * Needs n_experts <= 256 and every workgroup of the launch resident at once (one per CU;
+ * checked at moe_create).  A bounded wait that expires sets MOE_DEVFLAG_TIMEOUT.
+ * Replaces, for the MoE path of one decode token, the per-layer sequence
+ * record_and_submit_layer's RouterTopk dispatch -> do_route -> record_and_submit_moe of
+ * InferenceEngine::forward_single (src/inference.rs:296-301, 608-616, 622-766). */
+moe_status moe_decode_stack(moe_ctx *ctx, int layer0, int n_layers, const float *x,
+                            const float *logits, float *y, uint16_t *ids, float *w, int flags,
+                            void *stream);
+
 /* IQ4_XS decode of n_superblocks blocks into f32 [256*n] (test hook for the codec).
  * Replaces dequant_iq4_xs (shaders/common.glsl:61-86) with the GGML 136-byte format. */
 moe_status moe_dequant_iq4xs(const void *blocks, size_t n_superblocks, float *out, void *stream);
@@ -126,6 +143,28 @@ moe_status moe_device_flags(moe_ctx *ctx, void *stream, uint32_t *flags);
 
 /* Last error message of the calling thread ("" when none). */
 const char *moe_last_error(void);
+
+/* ---- per-kernel timing (profiling hook) ----
+ * No reference counterpart: the reference has no timing code at all (its only figure,
+ * README.md:27, is unmeasured).  While enabled with `capacity` > 0 event pairs, every
+ * kernel the context launches outside stream capture is bracketed by two HIP events on
+ * its own stream.  moe_timing_read waits for them, returns per kernel id the number of
+ * timed launches and their summed milliseconds, and starts a new window.  Events are
+ * created here, never inside a hot call; capacity 0 disables and frees them. */
+enum {
+    MOE_K_ROUTER_TOPK = 0,
+    MOE_K_BUCKET_FILL = 1,
+    MOE_K_DECODE_GATE_UP = 2,
+    MOE_K_DECODE_DOWN = 3,
+    MOE_K_PREFILL_PREP = 4,
+    MOE_K_PREFILL_GATE_UP = 5,
+    MOE_K_PREFILL_DOWN = 6,
+    MOE_K_PREFILL_COMBINE = 7,
+    MOE_K_DECODE_STACK = 8,
+    MOE_K_COUNT = 9
+};
+moe_status moe_timing_enable(moe_ctx *ctx, int capacity);
+moe_status moe_timing_read(moe_ctx *ctx, int counts[MOE_K_COUNT], double total_ms[MOE_K_COUNT]);
 
 /* ---- seeded input generators (benchmark/test utilities, not part of the drop-in) ----
  * Counter-based streams: element i of stream `seed` depends only on (seed, i). */

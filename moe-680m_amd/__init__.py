@@ -33,14 +33,18 @@ STATUS_NAMES = {0: "MOE_OK", 1: "MOE_EINVAL", 2: "MOE_ENOMEM", 3: "MOE_EHIP",
                 4: "MOE_EUNSUPPORTED", 5: "MOE_EDEVICE"}
 W_REF, W_RENORM = 0, 1
 FFN_ACCUMULATE, FFN_RMSNORM = 1, 2
-DEVFLAG_BAD_ID, DEVFLAG_DUP_ID = 1, 2
+DEVFLAG_BAD_ID, DEVFLAG_DUP_ID, DEVFLAG_TIMEOUT = 1, 2, 4
 
 # Every symbol include/moe_ffn.h declares (checked by the CPU test suite).
 EXPORTS = (
     "moe_create", "moe_destroy", "moe_bind_layer", "moe_router_topk", "moe_bucket_fill",
-    "moe_ffn", "moe_dequant_iq4xs", "moe_device_flags", "moe_last_error",
+    "moe_ffn", "moe_decode_stack", "moe_dequant_iq4xs", "moe_device_flags", "moe_last_error",
+    "moe_timing_enable", "moe_timing_read",
     "moe_gen_iq4xs", "moe_gen_normal", "moe_gen_logits",
 )
+
+KERNELS = ("router_topk", "bucket_fill", "decode_gate_up", "decode_down", "prefill_prep",
+           "prefill_gate_up", "prefill_down", "prefill_combine", "decode_stack")
 
 
 class MoeError(RuntimeError):
@@ -81,11 +85,14 @@ def lib():
         "moe_router_topk": [vp, vp, i, vp, vp, vp],
         "moe_bucket_fill": [vp, vp, vp, i, vp, vp, vp, vp],
         "moe_ffn": [vp, i, vp, vp, vp, i, vp, i, vp],
+        "moe_decode_stack": [vp, i, i, vp, vp, vp, vp, vp, i, vp],
         "moe_dequant_iq4xs": [vp, sz, vp, vp],
         "moe_device_flags": [vp, vp, ctypes.POINTER(ctypes.c_uint32)],
         "moe_gen_iq4xs": [vp, sz, u64, u64, vp],
         "moe_gen_normal": [vp, sz, u64, u64, ctypes.c_float, ctypes.c_float, vp],
         "moe_gen_logits": [vp, i, i, u64, i, ctypes.c_double, ctypes.c_double, vp],
+        "moe_timing_enable": [vp, i],
+        "moe_timing_read": [vp, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_double)],
     }
     for name, args in sigs.items():
         fn = getattr(L, name)
@@ -212,10 +219,32 @@ class Context:
                              _stream(stream)))
         return y
 
+    def decode_stack(self, layer0, x, logits, y=None, ids=None, w=None, rmsnorm=True, stream=None):
+        """One token through len(logits) consecutive layers starting at layer0:
+        routing from logits[l], x <- x + MoE_l(RMSNorm(x)).  Returns y (= x if y is x)."""
+        n = logits.shape[0]
+        if y is None:
+            y = torch.empty_like(x)
+        flags = FFN_RMSNORM if rmsnorm else 0
+        _check(lib().moe_decode_stack(self._h, layer0, n, _ptr(x), _ptr(logits), _ptr(y), _ptr(ids),
+                                      _ptr(w), flags, _stream(stream)))
+        return y
+
     def device_flags(self, stream=None):
         v = ctypes.c_uint32()
         _check(lib().moe_device_flags(self._h, _stream(stream), ctypes.byref(v)))
         return v.value
+
+    def timing_enable(self, capacity=4096):
+        _check(lib().moe_timing_enable(self._h, capacity))
+
+    def timing_read(self):
+        """{kernel name: (launches timed, total ms)} since the last read."""
+        n = len(KERNELS)
+        counts = (ctypes.c_int * n)()
+        ms = (ctypes.c_double * n)()
+        _check(lib().moe_timing_read(self._h, counts, ms))
+        return {k: (counts[i], ms[i]) for i, k in enumerate(KERNELS) if counts[i]}
 
 
 def dequant_iq4xs(blocks, out=None, stream=None):

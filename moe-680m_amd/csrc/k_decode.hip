@@ -27,24 +27,22 @@ __global__ __launch_bounds__(256) void k_decode_gate_up(DecodeArgs a) {
     constexpr int RPW = RP * RPS;   // rows per wave
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int item = blockIdx.y;
+    const int t0 = item / SLOTS;
+    const int gsb = lane % LPR, rr = lane / LPR;
+    const int sb = gsb >> 3, ib = gsb & 7;
+    const int nbase = (blockIdx.x * 4 + wv) * RPW;
+
+    // The activation row does not depend on routing: its loads go out first, then the
+    // expert id and, right behind it, the expert's rows.
+    float xv[32];
+    load32(a.x + (size_t)t0 * H + 32 * gsb, xv);
     const int e = a.ids[item];
     if (e > a.E) {
         if (threadIdx.x == 0 && blockIdx.x == 0) set_flag(a.flags, MOE_DEVFLAG_BAD_ID);
         return;
     }
-    // Only the first (token, slot) naming expert e runs; it serves every later slot that
-    // names e, so each selected expert's rows are fetched once for all tokens.
-    {
-        bool seen = false;
-        for (int p = lane; p < item; p += 64) seen |= (a.ids[p] == e);
-        if (__any(seen)) return;
-    }
-    const int gsb = lane % LPR, rr = lane / LPR;
-    const int sb = gsb >> 3, ib = gsb & 7;
     const uint8_t *W1 = expert_w(a.L.w1, a.L.s1, a.L.sw1, e, a.E);
     const uint8_t *W3 = expert_w(a.L.w3, a.L.s3, a.L.sw3, e, a.E);
-    const int nbase = (blockIdx.x * 4 + wv) * RPW;
-
     u32x4 q1[RP], q3[RP];
     u32x2 h1[RP], h3[RP];
 #pragma unroll
@@ -55,45 +53,46 @@ __global__ __launch_bounds__(256) void k_decode_gate_up(DecodeArgs a) {
         h3[r] = ldg<u32x2>(W3 + off);
         q3[r] = ldg<u32x4>(W3 + off + 8 + 16 * ib);
     }
+    // With several tokens, the first token naming expert e serves every later token that
+    // names it, so each selected expert's rows are fetched once for all tokens.
+    if (a.M > 1) {
+        bool seen = false;
+        for (int p = lane; p < t0 * SLOTS; p += 64) seen |= (a.ids[p] == e);
+        if (__any(seen)) return;
+    }
 
-    const int pend = a.M * SLOTS;
-    for (int p = item; p < pend; ++p) {
-        if (a.ids[p] != e) continue;
-        // Keep the weight decode inside the token loop: hoisting the decoded floats of
-        // all rows out of it would take ~250 registers and one wave per SIMD.
-#pragma unroll
-        for (int r = 0; r < RP; ++r) asm volatile("" : "+v"(q1[r]), "+v"(q3[r]), "+v"(h1[r]), "+v"(h3[r]));
-        const int t = p / SLOTS;
-        const float *xr = a.x + (size_t)t * H + 32 * gsb;
-        float xv[32];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            f32x4 v = ldg<f32x4>(xr + 4 * i);
-            xv[4 * i + 0] = v[0];
-            xv[4 * i + 1] = v[1];
-            xv[4 * i + 2] = v[2];
-            xv[4 * i + 3] = v[3];
-        }
+    auto run = [&](float(&xr)[32], int p) {
         if (a.rmsnorm) {
             float ss = 0.f;
 #pragma unroll
-            for (int i = 0; i < 32; ++i) ss = __builtin_fmaf(xv[i], xv[i], ss);
-            ss = group_sum<LPR>(ss);
+            for (int i = 0; i < 32; ++i) ss = __builtin_fmaf(xr[i], xr[i], ss);
+            ss = lanes_total<LPR>(ss);
             const float inv = 1.0f / sqrtf(ss * (1.0f / (float)H) + 1e-6f);
 #pragma unroll
-            for (int i = 0; i < 32; ++i) xv[i] *= inv;
+            for (int i = 0; i < 32; ++i) xr[i] *= inv;
         }
         float xs = 0.f;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) xs += xv[i];
+        for (int i = 0; i < 32; ++i) xs += xr[i];
 #pragma unroll
         for (int r = 0; r < RP; ++r) {
-            float g = sub_scale(h1[r], ib) * subblock_dot(q1[r], xv, xs);
-            float u = sub_scale(h3[r], ib) * subblock_dot(q3[r], xv, xs);
-            g = group_sum<LPR>(g);
-            u = group_sum<LPR>(u);
+            float g = sub_scale(h1[r], ib) * subblock_dot(q1[r], xr, xs);
+            float u = sub_scale(h3[r], ib) * subblock_dot(q3[r], xr, xs);
+            g = lanes_total<LPR>(g);
+            u = lanes_total<LPR>(u);
             if (gsb == 0) a.hbuf[(size_t)p * I + nbase + r * RPS + rr] = silu(g) * u;
         }
+    };
+    run(xv, item);
+    for (int p = (t0 + 1) * SLOTS; p < a.M * SLOTS; ++p) {
+        if (a.ids[p] != e) continue;
+        // Keep the weight decode inside this loop: hoisting the decoded floats of all rows
+        // out of it would take ~250 registers and one wave per SIMD.
+#pragma unroll
+        for (int r = 0; r < RP; ++r) asm volatile("" : "+v"(q1[r]), "+v"(q3[r]), "+v"(h1[r]), "+v"(h3[r]));
+        float xt[32];
+        load32(a.x + (size_t)(p / SLOTS) * H + 32 * gsb, xt);
+        run(xt, p);
     }
 }
 
@@ -112,6 +111,10 @@ __global__ __launch_bounds__(64 * SLOTS) void k_decode_down(DecodeArgs a) {
     const int gsb = lane % LPR, rr = lane / LPR;
     const int sb = gsb >> 3, ib = gsb & 7;
     const int p = t * SLOTS + s;
+    // h and the slot weight do not depend on the expert id: load them first.
+    float hv[32];
+    load32(a.hbuf + (size_t)p * I + 32 * gsb, hv);
+    const float wslot = a.w[p];
     const int e = a.ids[p];
     float v[STEPS];
 #pragma unroll
@@ -126,20 +129,10 @@ __global__ __launch_bounds__(64 * SLOTS) void k_decode_down(DecodeArgs a) {
             hd[st] = ldg<u32x2>(W2 + off);
             q[st] = ldg<u32x4>(W2 + off + 8 + 16 * ib);
         }
-        const float *hr = a.hbuf + (size_t)p * I + 32 * gsb;
-        float hv[32];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            f32x4 x4 = ldg<f32x4>(hr + 4 * i);
-            hv[4 * i + 0] = x4[0];
-            hv[4 * i + 1] = x4[1];
-            hv[4 * i + 2] = x4[2];
-            hv[4 * i + 3] = x4[3];
-        }
         float hs = 0.f;
 #pragma unroll
         for (int i = 0; i < 32; ++i) hs += hv[i];
-        const float wt = a.c * a.w[p];
+        const float wt = a.c * wslot;
 #pragma unroll
         for (int st = 0; st < STEPS; ++st) {
             float d = sub_scale(hd[st], ib) * subblock_dot(q[st], hv, hs);
@@ -165,25 +158,31 @@ __global__ __launch_bounds__(64 * SLOTS) void k_decode_down(DecodeArgs a) {
 }
 
 template <int H, int I>
-static hipError_t launch_decode_t(const DecodeArgs &a, hipStream_t st) {
+static hipError_t launch_decode_t(const DecodeArgs &a, hipStream_t st, KernelTimer *T) {
     constexpr int RP = 4;
     constexpr int LPR1 = (H / QK) * 8;
     constexpr int RPW1 = RP * (64 / LPR1);
     static_assert(I % (4 * RPW1) == 0, "gate_up grid");
     dim3 g1(I / (4 * RPW1), a.M * SLOTS);
-    hipLaunchKernelGGL((k_decode_gate_up<H, I, RP>), g1, dim3(256), 0, st, a);
+    {
+        TimedLaunch tl(T, MOE_K_DECODE_GATE_UP, st);
+        hipLaunchKernelGGL((k_decode_gate_up<H, I, RP>), g1, dim3(256), 0, st, a);
+    }
     constexpr int STEPS = 2;
     constexpr int LPR2 = (I / QK) * 8;
     constexpr int RPW2 = (64 / LPR2) * STEPS;
     static_assert(H % RPW2 == 0, "down grid");
     dim3 g2(H / RPW2, a.M);
-    hipLaunchKernelGGL((k_decode_down<H, I, STEPS>), g2, dim3(64 * SLOTS), 0, st, a);
+    {
+        TimedLaunch tl(T, MOE_K_DECODE_DOWN, st);
+        hipLaunchKernelGGL((k_decode_down<H, I, STEPS>), g2, dim3(64 * SLOTS), 0, st, a);
+    }
     return hipGetLastError();
 }
 
-hipError_t launch_decode(int H, int I, const DecodeArgs &a, hipStream_t st) {
-    if (H == 2048 && I == 512) return launch_decode_t<2048, 512>(a, st);
-    if (H == 512 && I == 256) return launch_decode_t<512, 256>(a, st);
+hipError_t launch_decode(int H, int I, const DecodeArgs &a, hipStream_t st, KernelTimer *T) {
+    if (H == 2048 && I == 512) return launch_decode_t<2048, 512>(a, st, T);
+    if (H == 512 && I == 256) return launch_decode_t<512, 256>(a, st, T);
     return hipErrorInvalidValue;
 }
 

@@ -274,17 +274,29 @@ __global__ __launch_bounds__(256) void k_pf_combine(PrefillArgs a) {
 }
 
 template <int H, int I>
-static hipError_t launch_prefill_t(const PrefillArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL((k_pf_prep<H>), dim3(a.M), dim3(256), 0, st, a);
-    hipLaunchKernelGGL((k_pf_gate_up<H, I>), dim3(a.tile_max, I / 64), dim3(256), 0, st, a);
-    hipLaunchKernelGGL((k_pf_down<H, I>), dim3(a.tile_max, H / 64), dim3(256), 0, st, a);
-    hipLaunchKernelGGL((k_pf_combine<H>), dim3(a.M), dim3(256), 0, st, a);
+static hipError_t launch_prefill_t(const PrefillArgs &a, hipStream_t st, KernelTimer *T) {
+    {
+        TimedLaunch tl(T, MOE_K_PREFILL_PREP, st);
+        hipLaunchKernelGGL((k_pf_prep<H>), dim3(a.M), dim3(256), 0, st, a);
+    }
+    {
+        TimedLaunch tl(T, MOE_K_PREFILL_GATE_UP, st);
+        hipLaunchKernelGGL((k_pf_gate_up<H, I>), dim3(a.tile_max, I / 64), dim3(256), 0, st, a);
+    }
+    {
+        TimedLaunch tl(T, MOE_K_PREFILL_DOWN, st);
+        hipLaunchKernelGGL((k_pf_down<H, I>), dim3(a.tile_max, H / 64), dim3(256), 0, st, a);
+    }
+    {
+        TimedLaunch tl(T, MOE_K_PREFILL_COMBINE, st);
+        hipLaunchKernelGGL((k_pf_combine<H>), dim3(a.M), dim3(256), 0, st, a);
+    }
     return hipGetLastError();
 }
 
-hipError_t launch_prefill(int H, int I, const PrefillArgs &a, hipStream_t st) {
-    if (H == 2048 && I == 512) return launch_prefill_t<2048, 512>(a, st);
-    if (H == 512 && I == 256) return launch_prefill_t<512, 256>(a, st);
+hipError_t launch_prefill(int H, int I, const PrefillArgs &a, hipStream_t st, KernelTimer *T) {
+    if (H == 2048 && I == 512) return launch_prefill_t<2048, 512>(a, st, T);
+    if (H == 512 && I == 256) return launch_prefill_t<512, 256>(a, st, T);
     return hipErrorInvalidValue;
 }
 

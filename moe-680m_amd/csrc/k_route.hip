@@ -6,100 +6,29 @@ namespace moe {
 // ---------------------------------------------------------------- router top-8
 // One 64-lane wave per token.  Replaces shaders/router_topk.comp, whose 256-lane workgroup
 // ran two 8-step LDS tree reductions and a serial insertion sort on lane 0
-// (router_topk.comp:37-85).  Here each lane keeps E/64 logits in registers, the eight
-// winners come from eight wave-wide max reductions on a 64-bit key (order-preserving f32
-// bits : inverted index, so the lower index wins ties exactly like the shader's strict
-// '>' insertion at router_topk.comp:76), and the softmax sum is one wave reduction.
-
-__device__ __forceinline__ float router_key(float v) {
-    if (v != v) v = -INFINITY; // NaN never wins and weighs 0 unless every logit is -inf/NaN
-    if (v == 0.0f) v = 0.0f;   // -0 ties with +0
-    return v;
-}
-__device__ __forceinline__ uint32_t ord32(float v) {
-    uint32_t b = __builtin_bit_cast(uint32_t, v);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-__device__ __forceinline__ float unord32(uint32_t o) {
-    uint32_t b = (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o;
-    return __builtin_bit_cast(float, b);
-}
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        uint32_t lo = __shfl_xor((uint32_t)v, off);
-        uint32_t hi = __shfl_xor((uint32_t)(v >> 32), off);
-        uint64_t o = ((uint64_t)hi << 32) | lo;
-        v = o > v ? o : v;
-    }
-    return v;
-}
-__device__ __forceinline__ float wave_max_f(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
-}
-
-constexpr int RT_MAXV = 16; // E <= 1024
-
+// (router_topk.comp:37-85).  Here each lane keeps E/64 logits in registers; each of the 8
+// rounds is a wave max of the order-preserving key (DPP inside rows of 16, then four
+// v_readlane) followed by a wave min of the index among lanes holding that key, so the
+// lower index wins ties exactly like the shader's strict '>' insertion
+// (router_topk.comp:76).  The softmax sum is one DPP + readlane reduction.
+template <int NV>
 __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ logits, int M, int E,
                                                      int renorm, uint16_t *__restrict__ ids,
                                                      float *__restrict__ w) {
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= M) return; // whole wave leaves together
-    const float *l = logits + (size_t)t * E;
-    float kf[RT_MAXV];
-#pragma unroll
-    for (int j = 0; j < RT_MAXV; ++j) {
-        int i = lane + 64 * j;
-        kf[j] = (i < E) ? router_key(l[i]) : -INFINITY;
-    }
-    uint32_t taken = 0;
     int sel[TOPK];
-    uint32_t selord[TOPK];
-#pragma unroll
-    for (int r = 0; r < TOPK; ++r) {
-        uint64_t best = 0;
-#pragma unroll
-        for (int j = 0; j < RT_MAXV; ++j) {
-            int i = lane + 64 * j;
-            if (i < E && !((taken >> j) & 1u)) {
-                uint64_t k = ((uint64_t)ord32(kf[j]) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i);
-                best = k > best ? k : best;
-            }
-        }
-        best = wave_max_u64(best);
-        int idx = (int)(0xFFFFFFFFu - (uint32_t)best);
-        if ((idx & 63) == lane) taken |= 1u << (idx >> 6);
-        sel[r] = idx;
-        selord[r] = (uint32_t)(best >> 32);
-    }
-    const float m = unord32(selord[0]);
-    float zs = 0.f;
-#pragma unroll
-    for (int j = 0; j < RT_MAXV; ++j) {
-        int i = lane + 64 * j;
-        if (i < E) zs += (kf[j] == m) ? 1.0f : expf(kf[j] - m);
-    }
-    const float Z = group_sum<64>(zs);
-    float e8[TOPK];
-    float s8 = 0.f;
-#pragma unroll
-    for (int r = 0; r < TOPK; ++r) {
-        float k = unord32(selord[r]);
-        e8[r] = (k == m) ? 1.0f : expf(k - m);
-        s8 += e8[r];
-    }
-    const float den = renorm ? s8 : Z;
+    float ws[TOPK];
+    route_wave<NV>(logits + (size_t)t * E, E, renorm, lane, sel, ws);
     if (lane < TOPK) {
-        float ev = e8[0];
+        float wv = ws[0];
         int id = sel[0];
 #pragma unroll
         for (int r = 1; r < TOPK; ++r)
-            if (lane == r) { ev = e8[r]; id = sel[r]; }
+            if (lane == r) { wv = ws[r]; id = sel[r]; }
         ids[(size_t)t * SLOTS + lane] = (uint16_t)id;
-        w[(size_t)t * SLOTS + lane] = ev / den;
+        w[(size_t)t * SLOTS + lane] = wv;
     } else if (lane == TOPK) {
         ids[(size_t)t * SLOTS + TOPK] = (uint16_t)E;
         w[(size_t)t * SLOTS + TOPK] = 1.0f;
@@ -107,10 +36,16 @@ __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ l
 }
 
 hipError_t launch_router_topk(const float *logits, int M, int E, int renorm, uint16_t *ids, float *w,
-                              hipStream_t st) {
+                              hipStream_t st, KernelTimer *T) {
     if (M <= 0) return hipSuccess;
     dim3 grid((unsigned)((M + 3) / 4));
-    hipLaunchKernelGGL(k_router_topk, grid, dim3(256), 0, st, logits, M, E, renorm, ids, w);
+    {
+        TimedLaunch tl(T, MOE_K_ROUTER_TOPK, st);
+        if (E <= 256)
+            hipLaunchKernelGGL(k_router_topk<4>, grid, dim3(256), 0, st, logits, M, E, renorm, ids, w);
+        else
+            hipLaunchKernelGGL(k_router_topk<16>, grid, dim3(256), 0, st, logits, M, E, renorm, ids, w);
+    }
     return hipGetLastError();
 }
 
@@ -277,10 +212,13 @@ __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
     if (tid == 0 && s_flags) set_flag(a.flags, s_flags);
 }
 
-hipError_t launch_bucket_fill(const BucketArgs &a, hipStream_t st) {
+hipError_t launch_bucket_fill(const BucketArgs &a, hipStream_t st, KernelTimer *T) {
     if (a.M < 0) return hipSuccess; // M == 0 still writes all-zero ranges
     size_t smem = bucket_smem(a.E1);
-    hipLaunchKernelGGL(k_bucket_fill, dim3(1), dim3(BF_THREADS), smem, st, a);
+    {
+        TimedLaunch tl(T, MOE_K_BUCKET_FILL, st);
+        hipLaunchKernelGGL(k_bucket_fill, dim3(1), dim3(BF_THREADS), smem, st, a);
+    }
     return hipGetLastError();
 }
 

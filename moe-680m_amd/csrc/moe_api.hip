@@ -34,6 +34,10 @@ struct moe_ctx {
     uint32_t *pos = nullptr;     // [m_max][9]
     uint32_t *chunk = nullptr;   // [ceil(m_max/64)][E+1]
     Tile *tiles = nullptr;       // [tile_max(m_max)]
+    LayerPtrs *dlayers = nullptr; // device copy of the layer table (decode stack)
+    uint32_t *xtag = nullptr;    // decode stack exchange buffers
+    int stack_ok = 0;            // all stack workgroups fit on the device at once
+    KernelTimer timer;
 };
 
 namespace {
@@ -66,6 +70,22 @@ bool shape_compiled(int H, int I) { return (H == 2048 && I == 512) || (H == 512 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+// The context's timer when timing is on and the stream is not being captured into a graph
+// (an event recorded during capture would become a graph dependency, not a timestamp).
+KernelTimer *timer_for(moe_ctx *ctx, hipStream_t st) {
+    if (ctx->timer.cap <= 0) return nullptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+    return &ctx->timer;
+}
+
+void timer_free(KernelTimer &T) {
+    for (int i = 0; i < 2 * T.cap; ++i) (void)hipEventDestroy(T.ev[i]);
+    delete[] T.ev;
+    delete[] T.kid;
+    T = KernelTimer{};
+}
 
 } // namespace
 
@@ -117,6 +137,8 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
         {(void **)&c->pos, mm * SLOTS * 4},
         {(void **)&c->chunk, nchunk * E1 * 4},
         {(void **)&c->tiles, tmax * sizeof(Tile)},
+        {(void **)&c->dlayers, (size_t)cfg->n_layers * sizeof(LayerPtrs)},
+        {(void **)&c->xtag, ((size_t)(cfg->n_layers + 1) * H + (size_t)cfg->n_layers * SLOTS * I) * 4},
     };
     size_t total = 0;
     for (auto &p : parts) total += align_up(p.bytes, 256);
@@ -132,12 +154,18 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
         off += align_up(p.bytes, 256);
     }
     he = hipMemset(c->flags, 0, 256);
+    if (he == hipSuccess) he = hipMemset(c->dlayers, 0, (size_t)cfg->n_layers * sizeof(LayerPtrs));
     if (he == hipSuccess) he = hipDeviceSynchronize();
     if (he != hipSuccess) {
         (void)hipFree(c->arena);
         delete c;
         return hip_fail(he, "moe_create: clearing workspace");
     }
+    // The decode stack needs every one of its workgroups resident at once.
+    int per_cu = 0, ncu = 0;
+    if (stack_occupancy(H, I, &per_cu) == hipSuccess &&
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess)
+        c->stack_ok = (per_cu >= 1 && (long)per_cu * ncu >= stack_blocks(H) && E <= 256) ? 1 : 0;
     *out = c;
     return ok();
 }
@@ -146,6 +174,7 @@ moe_status moe_destroy(moe_ctx *ctx) {
     if (!ctx) return fail(MOE_EINVAL, "moe_destroy: null context");
     (void)hipSetDevice(ctx->device);
     (void)hipDeviceSynchronize();
+    timer_free(ctx->timer);
     hipError_t he = hipFree(ctx->arena);
     delete ctx;
     if (he != hipSuccess) return hip_fail(he, "moe_destroy: hipFree");
@@ -176,6 +205,8 @@ moe_status moe_bind_layer(moe_ctx *ctx, int layer, const moe_layer_weights *lw) 
     L.sw1 = (const uint8_t *)lw->shared_w1;
     L.sw3 = (const uint8_t *)lw->shared_w3;
     L.sw2 = (const uint8_t *)lw->shared_w2;
+    hipError_t he = hipMemcpy(ctx->dlayers + layer, &L, sizeof(LayerPtrs), hipMemcpyHostToDevice);
+    if (he != hipSuccess) return hip_fail(he, "moe_bind_layer: copying the layer table");
     ctx->layers[layer] = L;
     ctx->bound[layer] = 1;
     return ok();
@@ -190,7 +221,7 @@ moe_status moe_router_topk(moe_ctx *ctx, const float *logits, int M, uint16_t *i
     if (((uintptr_t)logits & 3u) || ((uintptr_t)w & 3u) || ((uintptr_t)ids & 1u))
         return fail(MOE_EINVAL, "moe_router_topk: misaligned pointer");
     hipError_t he = launch_router_topk(logits, M, ctx->cfg.n_experts, ctx->cfg.wmode == MOE_W_RENORM, ids,
-                                       w, as_stream(stream));
+                                       w, as_stream(stream), timer_for(ctx, as_stream(stream)));
     if (he != hipSuccess) return hip_fail(he, "moe_router_topk: launch");
     return ok();
 }
@@ -216,7 +247,7 @@ moe_status moe_bucket_fill(moe_ctx *ctx, const uint16_t *ids, const float *w, in
     a.tile_max = 0;
     a.tile_bm = PF_BM;
     a.flags = ctx->flags;
-    hipError_t he = launch_bucket_fill(a, as_stream(stream));
+    hipError_t he = launch_bucket_fill(a, as_stream(stream), timer_for(ctx, as_stream(stream)));
     if (he != hipSuccess) return hip_fail(he, "moe_bucket_fill: launch");
     return ok();
 }
@@ -251,7 +282,7 @@ moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids,
         a.accumulate = (flags & MOE_FFN_ACCUMULATE) ? 1 : 0;
         a.rmsnorm = (flags & MOE_FFN_RMSNORM) ? 1 : 0;
         a.c = c;
-        he = launch_decode(H, I, a, st);
+        he = launch_decode(H, I, a, st, timer_for(ctx, st));
         if (he != hipSuccess) return hip_fail(he, "moe_ffn: decode launch");
         return ok();
     }
@@ -269,7 +300,8 @@ moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids,
     b.tile_max = tile_max_for(M, E + 1);
     b.tile_bm = PF_BM;
     b.flags = ctx->flags;
-    he = launch_bucket_fill(b, st);
+    KernelTimer *T = timer_for(ctx, st);
+    he = launch_bucket_fill(b, st, T);
     if (he != hipSuccess) return hip_fail(he, "moe_ffn: bucket fill launch");
     PrefillArgs p{};
     p.L = ctx->layers[layer];
@@ -288,8 +320,47 @@ moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids,
     p.rmsnorm = (flags & MOE_FFN_RMSNORM) ? 1 : 0;
     p.tile_max = b.tile_max;
     p.c = c;
-    he = launch_prefill(H, I, p, st);
+    he = launch_prefill(H, I, p, st, T);
     if (he != hipSuccess) return hip_fail(he, "moe_ffn: prefill launch");
+    return ok();
+}
+
+moe_status moe_decode_stack(moe_ctx *ctx, int layer0, int n_layers, const float *x, const float *logits,
+                            float *y, uint16_t *ids, float *w, int flags, void *stream) {
+    if (!ctx) return fail(MOE_EINVAL, "moe_decode_stack: null context");
+    if (!x || !logits || !y) return fail(MOE_EINVAL, "moe_decode_stack: null argument");
+    if ((ids == nullptr) != (w == nullptr)) return fail(MOE_EINVAL, "moe_decode_stack: ids and w go together");
+    if (n_layers < 1 || layer0 < 0 || layer0 + n_layers > ctx->cfg.n_layers)
+        return fail(MOE_EINVAL, "moe_decode_stack: layers %d..%d outside 0..%d", layer0, layer0 + n_layers - 1,
+                    ctx->cfg.n_layers - 1);
+    for (int l = layer0; l < layer0 + n_layers; ++l)
+        if (!ctx->bound[l]) return fail(MOE_EINVAL, "moe_decode_stack: layer %d has no bound weights", l);
+    if (flags & ~MOE_FFN_RMSNORM) return fail(MOE_EINVAL, "moe_decode_stack: unknown flags 0x%x", flags);
+    if (!aligned16(x) || !aligned16(y) || ((uintptr_t)logits & 3u) || ((uintptr_t)ids & 1u) || ((uintptr_t)w & 3u))
+        return fail(MOE_EINVAL, "moe_decode_stack: misaligned pointer (x, y need 16 bytes)");
+    if (!ctx->stack_ok)
+        return fail(MOE_EUNSUPPORTED, "moe_decode_stack: needs n_experts <= 256 and %d co-resident workgroups",
+                    stack_blocks(ctx->cfg.hidden));
+    const int H = ctx->cfg.hidden, I = ctx->cfg.inter;
+    StackArgs a{};
+    a.layers = ctx->dlayers;
+    a.layer0 = layer0;
+    a.n_layers = n_layers;
+    a.x = x;
+    a.logits = logits;
+    a.y = y;
+    a.ids_out = ids;
+    a.w_out = w;
+    a.xt = ctx->xtag;
+    a.ht = ctx->xtag + (size_t)(n_layers + 1) * H;
+    a.flags = ctx->flags;
+    a.E = ctx->cfg.n_experts;
+    a.rmsnorm = (flags & MOE_FFN_RMSNORM) ? 1 : 0;
+    a.renorm = ctx->cfg.wmode == MOE_W_RENORM;
+    a.c = ctx->cfg.wmode == MOE_W_REF ? 1.0f / 9.0f : 1.0f;
+    hipStream_t st = as_stream(stream);
+    hipError_t he = launch_stack(H, I, a, st, timer_for(ctx, st));
+    if (he != hipSuccess) return hip_fail(he, "moe_decode_stack: launch");
     return ok();
 }
 
@@ -300,6 +371,60 @@ moe_status moe_dequant_iq4xs(const void *blocks, size_t n_superblocks, float *ou
         return fail(MOE_EINVAL, "moe_dequant_iq4xs: blocks must be 8-byte and out 16-byte aligned");
     hipError_t he = launch_dequant(blocks, n_superblocks, out, as_stream(stream));
     if (he != hipSuccess) return hip_fail(he, "moe_dequant_iq4xs: launch");
+    return ok();
+}
+
+moe_status moe_timing_enable(moe_ctx *ctx, int capacity) {
+    if (!ctx) return fail(MOE_EINVAL, "moe_timing_enable: null context");
+    if (capacity < 0 || capacity > (1 << 20))
+        return fail(MOE_EINVAL, "moe_timing_enable: capacity %d outside 0..2^20", capacity);
+    (void)hipDeviceSynchronize();
+    timer_free(ctx->timer);
+    if (capacity == 0) return ok();
+    KernelTimer T;
+    T.ev = new (std::nothrow) hipEvent_t[2 * (size_t)capacity];
+    T.kid = new (std::nothrow) int[capacity];
+    if (!T.ev || !T.kid) {
+        delete[] T.ev;
+        delete[] T.kid;
+        return fail(MOE_ENOMEM, "moe_timing_enable: host allocation");
+    }
+    for (int i = 0; i < 2 * capacity; ++i) {
+        hipError_t he = hipEventCreate(&T.ev[i]);
+        if (he != hipSuccess) {
+            T.cap = i / 2;
+            for (int j = 0; j < i; ++j) (void)hipEventDestroy(T.ev[j]);
+            delete[] T.ev;
+            delete[] T.kid;
+            return hip_fail(he, "moe_timing_enable: hipEventCreate");
+        }
+    }
+    T.cap = capacity;
+    ctx->timer = T;
+    return ok();
+}
+
+moe_status moe_timing_read(moe_ctx *ctx, int counts[MOE_K_COUNT], double total_ms[MOE_K_COUNT]) {
+    if (!ctx || !counts || !total_ms) return fail(MOE_EINVAL, "moe_timing_read: null argument");
+    for (int k = 0; k < MOE_K_COUNT; ++k) {
+        counts[k] = 0;
+        total_ms[k] = 0.0;
+    }
+    KernelTimer &T = ctx->timer;
+    for (int i = 0; i < T.n; ++i) {
+        hipError_t he = hipEventSynchronize(T.ev[2 * i + 1]);
+        float ms = 0.f;
+        if (he == hipSuccess) he = hipEventElapsedTime(&ms, T.ev[2 * i], T.ev[2 * i + 1]);
+        if (he != hipSuccess) return hip_fail(he, "moe_timing_read: event");
+        if (T.kid[i] >= 0 && T.kid[i] < MOE_K_COUNT) {
+            counts[T.kid[i]]++;
+            total_ms[T.kid[i]] += ms;
+        }
+    }
+    const int dropped = T.dropped;
+    T.n = 0;
+    T.dropped = 0;
+    if (dropped) return fail(MOE_EINVAL, "moe_timing_read: %d launches not timed (capacity %d)", dropped, T.cap);
     return ok();
 }
 

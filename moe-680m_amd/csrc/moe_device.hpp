@@ -28,6 +28,15 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
+// Loads through the global address space: pointers read from memory (the layer table)
+// are otherwise generic, and FLAT instructions also count against lgkmcnt, so every LDS
+// wait would stall on outstanding weight loads.
+#define MOE_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ T ldg(const void *p) {
+    return *(const MOE_GLOBAL T *)p;
+}
+
 // kvalues_iq4nl = {-127,-104,-83,-65,-49,-35,-22,-10,1,13,25,38,53,69,89,113},
 // stored +128 as unsigned bytes (1..241) so v_cvt_f32_ubyte{0..3} converts them in one
 // instruction; callers subtract 128 * sum(x) once per sub-block.
@@ -129,6 +138,44 @@ __device__ __forceinline__ float sum16(float v) {
     return v;
 }
 
+// Whole-wave sum as a wave-uniform value: row sums by DPP, then the four row totals read
+// with v_readlane and added in a fixed order (no LDS round trip).
+__device__ __forceinline__ float wave_sum(float v) {
+    v = sum16(v);
+    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (a + b) + (c + d);
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<0xB1>(v));
+    v = max(v, dpp_u32<0x4E>(v));
+    v = max(v, dpp_u32<0x141>(v));
+    v = max(v, dpp_u32<0x140>(v));
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+    const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(a, b), max(c, d));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    v = min(v, dpp_u32<0xB1>(v));
+    v = min(v, dpp_u32<0x4E>(v));
+    v = min(v, dpp_u32<0x141>(v));
+    v = min(v, dpp_u32<0x140>(v));
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+    const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return min(min(a, b), min(c, d));
+}
+
 // Sum over groups of G lanes (G in 8,16,32,64), result in every lane of the group.
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
@@ -146,7 +193,90 @@ __device__ __forceinline__ float group_sum(float v) {
     }
 }
 
+// Total over each group of G lanes (G = 64: wave-uniform value through readlane).
+template <int G>
+__device__ __forceinline__ float lanes_total(float v) {
+    if constexpr (G == 64) return wave_sum(v);
+    else return group_sum<G>(v);
+}
+
+// 32 consecutive f32 (16-byte aligned) into registers as eight 128-bit loads.
+__device__ __forceinline__ void load32(const float *__restrict__ src, float (&v)[32]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        f32x4 q = ldg<f32x4>(src + 4 * i);
+        v[4 * i + 0] = q[0];
+        v[4 * i + 1] = q[1];
+        v[4 * i + 2] = q[2];
+        v[4 * i + 3] = q[3];
+    }
+}
+
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+// ---------------------------------------------------------------- router (one wave)
+__device__ __forceinline__ float router_key(float v) {
+    if (v != v) v = -INFINITY; // NaN never wins and weighs 0 unless every logit is -inf/NaN
+    if (v == 0.0f) v = 0.0f;   // -0 ties with +0
+    return v;
+}
+__device__ __forceinline__ uint32_t ord32(float v) {
+    uint32_t b = __builtin_bit_cast(uint32_t, v);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float unord32(uint32_t o) {
+    uint32_t b = (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o;
+    return __builtin_bit_cast(float, b);
+}
+
+// Softmax + top-8 of one token's E logits (E <= 64*NV, E >= 8) by the calling wave.
+// sel/wsel come out wave-uniform: the 8 ids by (logit desc, index asc) and their weights
+// (softmax probability, or renormalised over the 8 when renorm).
+template <int NV>
+__device__ __forceinline__ void route_wave(const float *__restrict__ l, int E, int renorm, int lane,
+                                           int sel[TOPK], float wsel[TOPK]) {
+    float kf[NV];
+    uint32_t ord[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int i = lane + 64 * j;
+        kf[j] = (i < E) ? router_key(ldg<float>(l + i)) : -INFINITY;
+        ord[j] = (i < E) ? ord32(kf[j]) : 0u; // 0 sorts below every real key (-inf is 0x007FFFFF)
+    }
+    uint32_t taken = 0, selord[TOPK];
+#pragma unroll
+    for (int r = 0; r < TOPK; ++r) {
+        uint32_t kb = 0;
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            if (!((taken >> j) & 1u)) kb = max(kb, ord[j]);
+        const uint32_t K = wave_max_u32(kb);
+        uint32_t cand = 0xFFFFFFFFu;
+#pragma unroll
+        for (int j = NV - 1; j >= 0; --j)
+            if (!((taken >> j) & 1u) && ord[j] == K) cand = (uint32_t)(lane + 64 * j);
+        const uint32_t idx = wave_min_u32(cand);
+        if ((int)(idx & 63u) == lane) taken |= 1u << (idx >> 6);
+        sel[r] = (int)idx;
+        selord[r] = K;
+    }
+    const float m = unord32(selord[0]);
+    float zs = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+        if (lane + 64 * j < E) zs += (kf[j] == m) ? 1.0f : expf(kf[j] - m);
+    const float Z = wave_sum(zs);
+    float e8[TOPK], s8 = 0.f;
+#pragma unroll
+    for (int r = 0; r < TOPK; ++r) {
+        const float k = unord32(selord[r]);
+        e8[r] = (k == m) ? 1.0f : expf(k - m);
+        s8 += e8[r];
+    }
+    const float den = renorm ? s8 : Z;
+#pragma unroll
+    for (int r = 0; r < TOPK; ++r) wsel[r] = e8[r] / den;
+}
 
 // ---------------------------------------------------------------- expert table
 struct LayerPtrs {
@@ -155,18 +285,31 @@ struct LayerPtrs {
     const uint8_t *sw1, *sw3, *sw2;
 };
 
+// A LayerPtrs entry of a device table, read field by field through global loads.
+__device__ __forceinline__ LayerPtrs load_layer(const LayerPtrs *p) {
+    const uint64_t *q = reinterpret_cast<const uint64_t *>(p);
+    LayerPtrs L;
+    L.w1 = (const uint8_t *)ldg<uint64_t>(q + 0);
+    L.w3 = (const uint8_t *)ldg<uint64_t>(q + 1);
+    L.w2 = (const uint8_t *)ldg<uint64_t>(q + 2);
+    L.s1 = ldg<uint64_t>(q + 3);
+    L.s3 = ldg<uint64_t>(q + 4);
+    L.s2 = ldg<uint64_t>(q + 5);
+    L.sw1 = (const uint8_t *)ldg<uint64_t>(q + 6);
+    L.sw3 = (const uint8_t *)ldg<uint64_t>(q + 7);
+    L.sw2 = (const uint8_t *)ldg<uint64_t>(q + 8);
+    return L;
+}
+static_assert(sizeof(LayerPtrs) == 72, "LayerPtrs is nine 8-byte fields");
+
 __device__ __forceinline__ const uint8_t *expert_w(const uint8_t *base, uint64_t stride,
                                                    const uint8_t *shared, int e, int E) {
     return e == E ? shared : base + (uint64_t)e * stride;
 }
 
-template <typename T>
-__device__ __forceinline__ T ldg(const void *p) {
-    return *reinterpret_cast<const T *>(p);
-}
 
 __device__ __forceinline__ void set_flag(uint32_t *flags, uint32_t f) {
-    if (flags) atomicOr(flags, f);
+    if (flags) __hip_atomic_fetch_or((MOE_GLOBAL uint32_t *)flags, f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 } // namespace moe

@@ -55,6 +55,51 @@ struct PrefillArgs {
     float c;
 };
 
+constexpr int STK_WAVES = SLOTS + 3; // decode stack: 9 compute waves, 1 router wave, 2 poller waves
+
+struct StackArgs {
+    const LayerPtrs *layers; // device table indexed by absolute layer
+    int layer0, n_layers;
+    const float *x;          // [H] input activation
+    const float *logits;     // [n_layers][E]
+    float *y;                // [H] output activation (may alias x)
+    uint16_t *ids_out;       // [n_layers][9] or null
+    float *w_out;            // [n_layers][9] or null
+    uint32_t *xt;            // tagged exchange: x_l at xt + l*H (l = 1..n-1)
+    uint32_t *ht;            // tagged exchange: h_l at ht + l*9*I
+    uint32_t *flags;         // [0] sticky device flags, [1] abort word
+    int E, rmsnorm, renorm;
+    float c;
+};
+
+// Optional per-kernel timing (moe_timing_enable): each launch is bracketed by two HIP
+// events recorded on the launch's own stream.  Events are created when timing is enabled,
+// never inside a hot call.
+struct KernelTimer {
+    hipEvent_t *ev = nullptr; // 2 * cap events
+    int *kid = nullptr;       // kernel id of each pair
+    int cap = 0, n = 0, dropped = 0;
+};
+
+struct TimedLaunch {
+    KernelTimer *T;
+    hipStream_t st;
+    bool on;
+    TimedLaunch(KernelTimer *t, int id, hipStream_t s) : T(t), st(s), on(false) {
+        if (T && T->cap > 0) {
+            if (T->n < T->cap) {
+                T->kid[T->n] = id;
+                on = hipEventRecord(T->ev[2 * T->n], st) == hipSuccess;
+            } else {
+                T->dropped++;
+            }
+        }
+    }
+    ~TimedLaunch() {
+        if (on && hipEventRecord(T->ev[2 * T->n + 1], st) == hipSuccess) T->n++;
+    }
+};
+
 hipError_t launch_dequant(const void *blocks, uint64_t n_sb, float *out, hipStream_t st);
 hipError_t launch_gen_iq4xs(void *dst, uint64_t n, uint64_t seed, uint64_t first, hipStream_t st);
 hipError_t launch_gen_normal(float *dst, uint64_t n, uint64_t seed, uint64_t first, float mean,
@@ -62,10 +107,13 @@ hipError_t launch_gen_normal(float *dst, uint64_t n, uint64_t seed, uint64_t fir
 hipError_t launch_gen_logits(float *dst, int M, int E, uint64_t seed, int kind, double param,
                              double hot_value, hipStream_t st);
 hipError_t launch_router_topk(const float *logits, int M, int E, int renorm, uint16_t *ids,
-                              float *w, hipStream_t st);
-hipError_t launch_bucket_fill(const BucketArgs &a, hipStream_t st);
-hipError_t launch_decode(int H, int I, const DecodeArgs &a, hipStream_t st);
-hipError_t launch_prefill(int H, int I, const PrefillArgs &a, hipStream_t st);
+                              float *w, hipStream_t st, KernelTimer *T);
+hipError_t launch_bucket_fill(const BucketArgs &a, hipStream_t st, KernelTimer *T);
+hipError_t launch_decode(int H, int I, const DecodeArgs &a, hipStream_t st, KernelTimer *T);
+hipError_t launch_prefill(int H, int I, const PrefillArgs &a, hipStream_t st, KernelTimer *T);
+hipError_t launch_stack(int H, int I, const StackArgs &a, hipStream_t st, KernelTimer *T);
+hipError_t stack_occupancy(int H, int I, int *blocks_per_cu);
+int stack_blocks(int H);
 
 inline int tile_max_for(int M, int E1) { return (9 * M + PF_BM - 1) / PF_BM + E1; }
 

@@ -175,3 +175,25 @@ def test_api_errors_on_gpu(gpu, full):
     with pytest.raises(gpu.MoeError):
         ctx.ffn(0, big, ids, w)          # M > m_max
     ctx.ffn(0, x[:0], ids[:0], w[:0])  # M = 0 is a no-op
+
+
+def test_kernel_timing_hook(gpu, full):
+    import torch
+    ctx, _ = full
+    log("timing hook")
+    x = gpu.gen_normal(2 * H, 31).view(2, H)
+    ids, w = ctx.router_topk(gpu.gen_logits(2, E, 32))
+    ctx.timing_enable(64)
+    ctx.router_topk(gpu.gen_logits(2, E, 32), ids, w)
+    ctx.ffn(0, x, ids, w)
+    xp = gpu.gen_normal(40 * H, 33).view(40, H)
+    idp, wp = ctx.router_topk(gpu.gen_logits(40, E, 34))
+    ctx.ffn(0, xp, idp, wp)
+    t = ctx.timing_read()
+    assert t["router_topk"][0] == 2 and t["decode_gate_up"][0] == 1 and t["decode_down"][0] == 1
+    for k in ("bucket_fill", "prefill_prep", "prefill_gate_up", "prefill_down", "prefill_combine"):
+        assert t[k][0] == 1 and t[k][1] > 0
+    assert ctx.timing_read() == {}
+    ctx.timing_enable(0)
+    ctx.ffn(0, x, ids, w)
+    torch.cuda.synchronize()

@@ -1,0 +1,156 @@
+"""GPU: moe_decode_stack (one token through consecutive layers in one persistent launch)
+vs the oracle applied layer by layer: x <- x + MoE_l(RMSNorm(x)), routing from seeded
+per-layer logits.  Decode tolerance: normwise 1e-3."""
+import numpy as np
+import pytest
+
+from gpu_util import E, H, I, log, normwise_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def oracle_chain(orc, pkg, layers_dev, hidden, inter, nexp, x0, logits, rmsnorm=True, mode=0):
+    """Oracle chain on the host; copies only the experts each layer selects."""
+    x = np.array(x0, dtype=np.float32).reshape(1, hidden)
+    eb = 3 * (hidden * inter // 256 * 136)
+    host = np.zeros((nexp + 1) * eb, dtype=np.uint8)
+    all_ids, all_w = [], []
+    for l, dev in enumerate(layers_dev):
+        ids, w = orc.router_topk(logits[l:l + 1], mode)
+        for e in ids[0]:
+            host[int(e) * eb:(int(e) + 1) * eb] = dev[int(e) * eb:(int(e) + 1) * eb].cpu().numpy()
+        L = orc.PackedLayer(host, hidden, inter, nexp)
+        flags = orc.ACCUMULATE | (orc.RMSNORM if rmsnorm else 0)
+        x = orc.moe_ffn(L, x, ids, w, 1.0 / 9 if mode == 0 else 1.0, flags, y=x)
+        all_ids.append(ids[0])
+        all_w.append(w[0])
+    return x.reshape(-1), np.array(all_ids), np.array(all_w)
+
+
+@pytest.fixture(scope="module")
+def small(gpu):
+    hidden, inter, nexp, nl = 512, 256, 16, 6
+    ctx = gpu.Context(hidden, inter, nexp, nl, 16, gpu.W_REF)
+    layers = []
+    for l in range(nl):
+        buf = gpu.gen_layer(hidden, inter, nexp, 500 + l)
+        ctx.bind_packed(l, buf)
+        layers.append(buf)
+    yield ctx, layers, (hidden, inter, nexp)
+    ctx.close()
+
+
+@pytest.mark.parametrize("layer0,n", [(0, 1), (0, 2), (0, 3), (0, 6), (2, 3), (5, 1)])
+def test_small_stack(gpu, orc, small, layer0, n):
+    import torch
+    ctx, layers, (hidden, inter, nexp) = small
+    log(f"stack small H={hidden} layers {layer0}..{layer0 + n - 1}")
+    x = gpu.gen_normal(hidden, 600 + n)
+    logits = gpu.gen_logits(n, nexp, 700 + layer0 + n)
+    ids = torch.empty((n, 9), dtype=torch.uint16, device="cuda")
+    w = torch.empty((n, 9), dtype=torch.float32, device="cuda")
+    y = ctx.decode_stack(layer0, x, logits, ids=ids, w=w)
+    torch.cuda.synchronize()
+    assert ctx.device_flags() == 0
+    ref, rid, rw = oracle_chain(orc, gpu, layers[layer0:layer0 + n], hidden, inter, nexp,
+                                x.cpu().numpy(), logits.cpu().numpy())
+    assert np.array_equal(ids.cpu().numpy(), rid)
+    assert np.allclose(w.cpu().numpy(), rw, rtol=1e-5)
+    err = normwise_err(y.cpu().numpy(), ref)
+    log(f"  normwise err {err:.3e}")
+    assert err <= TOL
+
+
+def test_small_stack_no_norm_and_in_place(gpu, orc, small):
+    import torch
+    ctx, layers, (hidden, inter, nexp) = small
+    n = 2  # without RMSNorm the seeded chain grows ~1e5x per layer and overflows by layer 4
+    x = gpu.gen_normal(hidden, 801)
+    x0 = x.cpu().numpy()
+    logits = gpu.gen_logits(n, nexp, 802)
+    ctx.decode_stack(0, x, logits, y=x, rmsnorm=False)   # in place
+    torch.cuda.synchronize()
+    ref, _, _ = oracle_chain(orc, gpu, layers[:n], hidden, inter, nexp, x0, logits.cpu().numpy(),
+                             rmsnorm=False)
+    assert normwise_err(x.cpu().numpy(), ref) <= TOL
+
+
+@pytest.fixture(scope="module")
+def full(gpu):
+    nl = 40
+    ctx = gpu.Context(H, I, E, nl, 8, gpu.W_REF)
+    layers = []
+    for l in range(nl):
+        buf = gpu.gen_layer(H, I, E, gpu.seed_for(2, l, gpu.TAG_W))
+        ctx.bind_packed(l, buf)
+        layers.append(buf)
+    yield ctx, layers
+    ctx.close()
+
+
+def test_config2_forty_layers(gpu, orc, full):
+    import torch
+    ctx, layers = full
+    log("config 2: 40-layer stack, M=1")
+    x = gpu.gen_normal(H, gpu.seed_for(2, 0, gpu.TAG_X))
+    logits = gpu.gen_logits(40, E, gpu.seed_for(2, 0, gpu.TAG_L))
+    ids = torch.empty((40, 9), dtype=torch.uint16, device="cuda")
+    w = torch.empty((40, 9), dtype=torch.float32, device="cuda")
+    y = ctx.decode_stack(0, x, logits, ids=ids, w=w)
+    torch.cuda.synchronize()
+    assert ctx.device_flags() == 0
+    ref, rid, rw = oracle_chain(orc, gpu, layers, H, I, E, x.cpu().numpy(), logits.cpu().numpy())
+    assert np.array_equal(ids.cpu().numpy(), rid)
+    err = normwise_err(y.cpu().numpy(), ref)
+    log(f"  normwise err {err:.3e}")
+    assert err <= TOL
+
+
+def test_stack_matches_per_layer_path(gpu, full):
+    import torch
+    ctx, _ = full
+    n = 6
+    log("stack vs per-layer router + ffn")
+    x = gpu.gen_normal(H, 901)
+    logits = gpu.gen_logits(n, E, 902)
+    y = ctx.decode_stack(10, x, logits)
+    xr = x.clone().view(1, H)
+    for l in range(n):
+        ids, w = ctx.router_topk(logits[l:l + 1])
+        ctx.ffn(10 + l, xr, ids, w, y=xr, accumulate=True, rmsnorm=True)
+    torch.cuda.synchronize()
+    err = normwise_err(y.cpu().numpy(), xr.view(-1).cpu().numpy())
+    log(f"  stack vs per-layer normwise diff {err:.3e}")
+    assert err <= 1e-5
+
+
+def test_stack_graph_replays(gpu, full):
+    import torch
+    ctx, _ = full
+    log("stack under graph capture, 4 replays")
+    x = gpu.gen_normal(H, 903)
+    logits = gpu.gen_logits(8, E, 904)
+    y = torch.empty_like(x)
+    eager = ctx.decode_stack(0, x, logits).clone()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ctx.decode_stack(0, x, logits, y=y)
+    for _ in range(4):
+        y.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int32), eager.view(torch.int32))
+        assert ctx.device_flags() == 0
+
+
+def test_stack_errors(gpu, full):
+    import torch
+    ctx, _ = full
+    x = torch.zeros(H, device="cuda")
+    lg = torch.zeros((2, E), device="cuda")
+    with pytest.raises(gpu.MoeError):
+        ctx.decode_stack(39, x, lg)          # runs past the last layer
+    with pytest.raises(gpu.MoeError):
+        ctx.decode_stack(0, x[1:], lg)       # misaligned
