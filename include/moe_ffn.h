@@ -161,7 +161,9 @@ enum {
     MOE_K_PREFILL_DOWN = 6,
     MOE_K_PREFILL_COMBINE = 7,
     MOE_K_DECODE_STACK = 8,
-    MOE_K_COUNT = 9
+    MOE_K_PREFILL_GATE_UP_SMALL = 9, /* small-tile variants, run on the context's second stream */
+    MOE_K_PREFILL_DOWN_SMALL = 10,
+    MOE_K_COUNT = 11
 };
 moe_status moe_timing_enable(moe_ctx *ctx, int capacity);
 moe_status moe_timing_read(moe_ctx *ctx, int counts[MOE_K_COUNT], double total_ms[MOE_K_COUNT]);

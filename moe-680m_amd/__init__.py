@@ -44,7 +44,8 @@ EXPORTS = (
 )
 
 KERNELS = ("router_topk", "bucket_fill", "decode_gate_up", "decode_down", "prefill_prep",
-           "prefill_gate_up", "prefill_down", "prefill_combine", "decode_stack")
+           "prefill_gate_up", "prefill_down", "prefill_combine", "decode_stack",
+           "prefill_gate_up_small", "prefill_down_small")
 
 
 class MoeError(RuntimeError):

@@ -58,7 +58,7 @@ hipError_t launch_router_topk(const float *logits, int M, int E, int renorm, uin
 // bucket, the bucket totals a scan over buckets (ranges), and the scatter writes each slot
 // to ranges[e] + chunk offset + in-chunk rank: tokens ascend within a bucket, as in the
 // reference's cursor fill.  One 1024-thread workgroup; no inter-workgroup synchronisation.
-// The same pass writes the grouped-GEMM tile list (tile_bm slots per tile).
+// The same pass writes the grouped-GEMM tile lists (see tile_max_for / stile_max_for).
 constexpr int BF_THREADS = 1024;
 constexpr int BF_BITMAP_BYTES = 48 * 1024;
 
@@ -67,7 +67,7 @@ __host__ __device__ inline int bucket_cw(int E1) {
     return cw > 16 ? 16 : (cw < 1 ? 1 : cw);
 }
 __host__ inline size_t bucket_smem(int E1) {
-    return (size_t)bucket_cw(E1) * E1 * 8 + 3 * (size_t)(E1 + 1) * 4;
+    return (size_t)bucket_cw(E1) * E1 * 8 + 5 * (size_t)(E1 + 1) * 4;
 }
 
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
@@ -88,8 +88,10 @@ __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
     const int CW = bucket_cw(E1);
     uint32_t *bm_all = smem;
     uint32_t *tot = smem + (size_t)CW * E1 * 2;
-    uint32_t *rg = tot + (E1 + 1);
-    uint32_t *ts = rg + (E1 + 1);
+    uint32_t *rg = tot + (E1 + 1);  // bucket starts
+    uint32_t *ts = rg + (E1 + 1);   // first full big tile of each bucket
+    uint32_t *tp = ts + (E1 + 1);   // partial big tile index (after all full ones)
+    uint32_t *tsm = tp + (E1 + 1);  // first small tile
     if (tid == 0) s_flags = 0;
 
     // Phase 1: per-chunk bucket counts.
@@ -133,43 +135,45 @@ __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
     }
     __syncthreads();
 
-    // Phase 2b: scan over buckets -> ranges; tile counts -> tile starts (wave 0).
-    if (wv == 0) {
-        uint32_t carry = 0, tcarry = 0;
+    // Phase 2b: scans over buckets (one wave each): ranges; full big tiles; partial big
+    // tiles; small tiles.  Big tiles are listed full ones first, so the long work items
+    // start first.
+    if (wv < 4) {
+        uint32_t *dst = wv == 0 ? rg : (wv == 1 ? ts : (wv == 2 ? tp : tsm));
+        uint32_t carry = 0;
         for (int base = 0; base < E1; base += 64) {
             const int e = base + lane;
-            uint32_t v = (e < E1) ? tot[e] : 0u;
-            uint32_t nt = (v + (uint32_t)a.tile_bm - 1u) / (uint32_t)a.tile_bm;
-            uint32_t inc = wave_incl_scan(v, lane);
-            uint32_t tinc = wave_incl_scan(nt, lane);
-            if (e < E1) {
-                rg[e] = carry + inc - v;
-                ts[e] = tcarry + tinc - nt;
-            }
+            const uint32_t n = (e < E1) ? tot[e] : 0u;
+            const uint32_t rem = n % PF_BM;
+            uint32_t v = n;
+            if (wv == 1) v = n / PF_BM;
+            else if (wv == 2) v = rem > PF_SMALL_MAX ? 1u : 0u;
+            else if (wv == 3) v = (rem > 0 && rem <= PF_SMALL_MAX) ? (rem + PF_SM - 1) / PF_SM : 0u;
+            const uint32_t inc = wave_incl_scan(v, lane);
+            if (e < E1) dst[e] = carry + inc - v;
             carry += __shfl(inc, 63);
-            tcarry += __shfl(tinc, 63);
         }
-        if (lane == 0) {
-            rg[E1] = carry;
-            ts[E1] = tcarry;
-        }
+        if (lane == 0) dst[E1] = carry;
     }
     __syncthreads();
 
     for (int e = tid; e <= E1; e += BF_THREADS) a.ranges[e] = rg[e];
     if (a.tiles) {
+        const uint32_t nfull = ts[E1];
+        Tile *small = a.tiles + a.tile_max;
         for (int e = tid; e < E1; e += BF_THREADS) {
             const int n = (int)tot[e];
-            for (int j = 0; j * a.tile_bm < n; ++j) {
-                Tile tl;
-                tl.expert = e;
-                tl.row0 = (int)rg[e] + j * a.tile_bm;
-                tl.nrows = min(a.tile_bm, n - j * a.tile_bm);
-                tl.pad = 0;
-                a.tiles[ts[e] + j] = tl;
+            const int nf = n / PF_BM, rem = n % PF_BM;
+            for (int j = 0; j < nf; ++j) a.tiles[ts[e] + j] = Tile{e, (int)rg[e] + j * PF_BM, PF_BM, 0};
+            if (rem > PF_SMALL_MAX) {
+                a.tiles[nfull + tp[e]] = Tile{e, (int)rg[e] + nf * PF_BM, rem, 0};
+            } else {
+                for (int j = 0; j * PF_SM < rem; ++j)
+                    small[tsm[e] + j] = Tile{e, (int)rg[e] + nf * PF_BM + j * PF_SM, min(PF_SM, rem - j * PF_SM), 0};
             }
         }
-        for (int i = (int)ts[E1] + tid; i < a.tile_max; i += BF_THREADS) a.tiles[i] = Tile{-1, 0, 0, 0};
+        for (int i = (int)(nfull + tp[E1]) + tid; i < a.tile_max; i += BF_THREADS) a.tiles[i] = Tile{-1, 0, 0, 0};
+        for (int i = (int)tsm[E1] + tid; i < a.stile_max; i += BF_THREADS) small[i] = Tile{-1, 0, 0, 0};
     }
 
     // Phase 3: rebuild each chunk's bitmaps and scatter.

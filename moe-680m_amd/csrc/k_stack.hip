@@ -41,12 +41,6 @@ __device__ __forceinline__ void tag_store(uint32_t *p, float v) {
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Workgroup barrier for LDS traffic only.  __syncthreads() also waits for every global
-// load the wave has in flight (gfx9 retires loads in order and the barrier's release
-// fence needs vmcnt(0)), which would stall on the weight loads issued two layers ahead.
-// Workgroup-internal exchange here is LDS only; cross-workgroup exchange is tagged.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 // LDS index of word k with 4 pad words after every 32 (conflict-free 128-bit reads of a
 // lane's 32-float chunk).
 __device__ __forceinline__ int padk(int k) { return k + ((k >> 5) << 2); }

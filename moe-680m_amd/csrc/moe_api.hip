@@ -20,23 +20,29 @@ struct moe_ctx {
     int device = 0;
     moe_config cfg{};
     std::vector<LayerPtrs> layers;
+    std::vector<LayerPtrs> rlayers; // R16 repacked copies (prefill)
     std::vector<char> bound;
+    uint8_t *rpk = nullptr;         // [n_layers][E+1][W1|W3|W2] R16, when m_max > MOE_DECODE_MAX_M
     void *arena = nullptr; // one device allocation, carved below
     size_t arena_bytes = 0;
     uint32_t *flags = nullptr;
     float *hbuf = nullptr;       // decode h: [8][9][I] f32
-    __bf16 *xb = nullptr;        // [m_max][H]
-    __bf16 *hs = nullptr;        // [9 m_max][I]
+    _Float16 *xh = nullptr;      // [m_max][H]
+    float *xinv = nullptr;       // [m_max]
+    float *hf = nullptr;         // [9 m_max][I]
+    float *hmax = nullptr;       // [9 m_max][I/128]
     float *part = nullptr;       // [9 m_max][H]
     uint32_t *ranges = nullptr;  // [E+2]
     uint16_t *stok = nullptr;    // [9 m_max]
     float *sw = nullptr;         // [9 m_max]
     uint32_t *pos = nullptr;     // [m_max][9]
     uint32_t *chunk = nullptr;   // [ceil(m_max/64)][E+1]
-    Tile *tiles = nullptr;       // [tile_max(m_max)]
+    Tile *tiles = nullptr;       // [tile_max(m_max) + stile_max]
     LayerPtrs *dlayers = nullptr; // device copy of the layer table (decode stack)
     uint32_t *xtag = nullptr;    // decode stack exchange buffers
     int stack_ok = 0;            // all stack workgroups fit on the device at once
+    hipStream_t aux = nullptr;   // prefill small-tile GEMMs (non-blocking, default priority)
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     KernelTimer timer;
 };
 
@@ -117,6 +123,7 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
     c->device = device;
     c->cfg = *cfg;
     c->layers.resize(cfg->n_layers);
+    c->rlayers.resize(cfg->n_layers);
     c->bound.assign(cfg->n_layers, 0);
 
     const size_t mm = (size_t)cfg->m_max, E1 = (size_t)E + 1;
@@ -128,15 +135,17 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
     } parts[] = {
         {(void **)&c->flags, 256},
         {(void **)&c->hbuf, (size_t)MOE_DECODE_MAX_M * SLOTS * I * sizeof(float)},
-        {(void **)&c->xb, mm * H * 2},
-        {(void **)&c->hs, SLOTS * mm * I * 2},
+        {(void **)&c->xh, mm * H * 2},
+        {(void **)&c->xinv, mm * 4},
+        {(void **)&c->hf, SLOTS * mm * I * 4},
+        {(void **)&c->hmax, SLOTS * mm * (I / 128) * 4},
         {(void **)&c->part, SLOTS * mm * H * sizeof(float)},
         {(void **)&c->ranges, (E1 + 1) * 4},
         {(void **)&c->stok, SLOTS * mm * 2},
         {(void **)&c->sw, SLOTS * mm * 4},
         {(void **)&c->pos, mm * SLOTS * 4},
         {(void **)&c->chunk, nchunk * E1 * 4},
-        {(void **)&c->tiles, tmax * sizeof(Tile)},
+        {(void **)&c->tiles, (tmax + (size_t)stile_max_for((int)E1)) * sizeof(Tile)},
         {(void **)&c->dlayers, (size_t)cfg->n_layers * sizeof(LayerPtrs)},
         {(void **)&c->xtag, ((size_t)(cfg->n_layers + 1) * H + (size_t)cfg->n_layers * SLOTS * I) * 4},
     };
@@ -153,6 +162,18 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
         *p.dst = (char *)c->arena + off;
         off += align_up(p.bytes, 256);
     }
+    if (cfg->m_max > MOE_DECODE_MAX_M) {
+        // the prefill GEMMs read a repacked copy of every bound layer (see k_repack_r16)
+        const size_t mat = (size_t)H * I / QK * SB_BYTES;
+        const size_t rbytes = (size_t)cfg->n_layers * E1 * 3 * mat;
+        he = hipMalloc((void **)&c->rpk, rbytes);
+        if (he != hipSuccess) {
+            (void)hipFree(c->arena);
+            delete c;
+            return fail(MOE_ENOMEM, "moe_create: hipMalloc(%zu) for the prefill weight layout: %s", rbytes,
+                        hipGetErrorString(he));
+        }
+    }
     he = hipMemset(c->flags, 0, 256);
     if (he == hipSuccess) he = hipMemset(c->dlayers, 0, (size_t)cfg->n_layers * sizeof(LayerPtrs));
     if (he == hipSuccess) he = hipDeviceSynchronize();
@@ -160,6 +181,17 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
         (void)hipFree(c->arena);
         delete c;
         return hip_fail(he, "moe_create: clearing workspace");
+    }
+    he = hipStreamCreateWithFlags(&c->aux, hipStreamNonBlocking);
+    if (he == hipSuccess) he = hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming);
+    if (he == hipSuccess) he = hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming);
+    if (he != hipSuccess) {
+        if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
+        if (c->aux) (void)hipStreamDestroy(c->aux);
+        if (c->rpk) (void)hipFree(c->rpk);
+        (void)hipFree(c->arena);
+        delete c;
+        return hip_fail(he, "moe_create: second stream");
     }
     // The decode stack needs every one of its workgroups resident at once.
     int per_cu = 0, ncu = 0;
@@ -175,6 +207,10 @@ moe_status moe_destroy(moe_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipDeviceSynchronize();
     timer_free(ctx->timer);
+    if (ctx->ev_fork) (void)hipEventDestroy(ctx->ev_fork);
+    if (ctx->ev_join) (void)hipEventDestroy(ctx->ev_join);
+    if (ctx->aux) (void)hipStreamDestroy(ctx->aux);
+    if (ctx->rpk) (void)hipFree(ctx->rpk);
     hipError_t he = hipFree(ctx->arena);
     delete ctx;
     if (he != hipSuccess) return hip_fail(he, "moe_destroy: hipFree");
@@ -207,6 +243,25 @@ moe_status moe_bind_layer(moe_ctx *ctx, int layer, const moe_layer_weights *lw) 
     L.sw2 = (const uint8_t *)lw->shared_w2;
     hipError_t he = hipMemcpy(ctx->dlayers + layer, &L, sizeof(LayerPtrs), hipMemcpyHostToDevice);
     if (he != hipSuccess) return hip_fail(he, "moe_bind_layer: copying the layer table");
+    if (ctx->rpk) {
+        const int H = ctx->cfg.hidden, I = ctx->cfg.inter, E = ctx->cfg.n_experts;
+        const size_t es = 3 * mat;
+        uint8_t *base = ctx->rpk + (size_t)layer * (E + 1) * es;
+        he = launch_repack_r16(L.w1, L.s1, L.sw1, base, es, E, I, H, nullptr);
+        if (he == hipSuccess) he = launch_repack_r16(L.w3, L.s3, L.sw3, base + mat, es, E, I, H, nullptr);
+        if (he == hipSuccess) he = launch_repack_r16(L.w2, L.s2, L.sw2, base + 2 * mat, es, E, H, I, nullptr);
+        if (he == hipSuccess) he = hipDeviceSynchronize();
+        if (he != hipSuccess) return hip_fail(he, "moe_bind_layer: repacking for prefill");
+        LayerPtrs R;
+        R.w1 = base;
+        R.w3 = base + mat;
+        R.w2 = base + 2 * mat;
+        R.s1 = R.s3 = R.s2 = es;
+        R.sw1 = base + (size_t)E * es;
+        R.sw3 = R.sw1 + mat;
+        R.sw2 = R.sw1 + 2 * mat;
+        ctx->rlayers[layer] = R;
+    }
     ctx->layers[layer] = L;
     ctx->bound[layer] = 1;
     return ok();
@@ -245,7 +300,7 @@ moe_status moe_bucket_fill(moe_ctx *ctx, const uint16_t *ids, const float *w, in
     a.chunk_cnt = ctx->chunk;
     a.tiles = nullptr;
     a.tile_max = 0;
-    a.tile_bm = PF_BM;
+    a.stile_max = 0;
     a.flags = ctx->flags;
     hipError_t he = launch_bucket_fill(a, as_stream(stream), timer_for(ctx, as_stream(stream)));
     if (he != hipSuccess) return hip_fail(he, "moe_bucket_fill: launch");
@@ -298,20 +353,22 @@ moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids,
     b.chunk_cnt = ctx->chunk;
     b.tiles = ctx->tiles;
     b.tile_max = tile_max_for(M, E + 1);
-    b.tile_bm = PF_BM;
+    b.stile_max = stile_max_for(E + 1);
     b.flags = ctx->flags;
     KernelTimer *T = timer_for(ctx, st);
     he = launch_bucket_fill(b, st, T);
     if (he != hipSuccess) return hip_fail(he, "moe_ffn: bucket fill launch");
     PrefillArgs p{};
-    p.L = ctx->layers[layer];
+    p.L = ctx->rlayers[layer];
     p.x = x;
-    p.xb = ctx->xb;
+    p.xh = ctx->xh;
+    p.xinv = ctx->xinv;
     p.sorted_tok = ctx->stok;
     p.sorted_w = ctx->sw;
     p.pos = ctx->pos;
     p.tiles = ctx->tiles;
-    p.hs = ctx->hs;
+    p.hf = ctx->hf;
+    p.hmax = ctx->hmax;
     p.part = ctx->part;
     p.y = y;
     p.M = M;
@@ -319,8 +376,9 @@ moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids,
     p.accumulate = (flags & MOE_FFN_ACCUMULATE) ? 1 : 0;
     p.rmsnorm = (flags & MOE_FFN_RMSNORM) ? 1 : 0;
     p.tile_max = b.tile_max;
+    p.stile_max = b.stile_max;
     p.c = c;
-    he = launch_prefill(H, I, p, st, T);
+    he = launch_prefill(H, I, p, st, ctx->aux, ctx->ev_fork, ctx->ev_join, T);
     if (he != hipSuccess) return hip_fail(he, "moe_ffn: prefill launch");
     return ok();
 }

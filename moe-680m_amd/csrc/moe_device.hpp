@@ -308,6 +308,12 @@ __device__ __forceinline__ const uint8_t *expert_w(const uint8_t *base, uint64_t
 }
 
 
+// Workgroup barrier for LDS traffic only.  __syncthreads() also waits for every global
+// load the wave has in flight (the barrier's release fence needs vmcnt(0)), which would
+// stall on weight loads issued ahead of use.  Use it where the workgroup exchanges data
+// through LDS only.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ void set_flag(uint32_t *flags, uint32_t f) {
     if (flags) __hip_atomic_fetch_or((MOE_GLOBAL uint32_t *)flags, f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

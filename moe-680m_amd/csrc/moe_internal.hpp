@@ -12,7 +12,9 @@ struct Tile {
     int32_t expert, row0, nrows, pad;
 };
 
-constexpr int PF_BM = 64; // prefill tile rows (token slots)
+constexpr int PF_BM = 128; // prefill big-tile rows (token slots of one expert)
+constexpr int PF_SM = 16;  // prefill small-tile rows
+constexpr int PF_SMALL_MAX = 32; // remainders of at most this many slots become small tiles
 
 struct DecodeArgs {
     LayerPtrs L;
@@ -35,23 +37,27 @@ struct BucketArgs {
     float *sorted_w;      // [9M]
     uint32_t *pos;        // [M][9] or null
     uint32_t *chunk_cnt;  // workspace [ceil(M/64)][E1]
-    Tile *tiles;          // [tile_max] or null
-    int tile_max, tile_bm;
+    Tile *tiles;          // [tile_max] big tiles (full first), then [stile_max] small tiles; or null
+    int tile_max, stile_max;
     uint32_t *flags;
 };
 
+// Prefill reads the R16 repacked copy of a layer (k_repack_r16): same matrix bases and
+// sizes as the natural layout, bytes permuted within every 16-row group.
 struct PrefillArgs {
     LayerPtrs L;
     const float *x;
-    __bf16 *xb;          // [M][H] bf16 (normalised if requested)
+    _Float16 *xh;        // [M][H] f16: x (normalised if requested) * s_t, K permuted in 32-blocks
+    float *xinv;         // [M] 1 / s_t (s_t a power of two)
     const uint16_t *sorted_tok;
     const float *sorted_w;
     const uint32_t *pos; // [M][9]
     const Tile *tiles;
-    __bf16 *hs;          // [9M][I] bf16, sorted slot order
+    float *hf;           // [9M][I] f32 h = silu(g) * u, sorted slot order
+    float *hmax;         // [9M][I/128] max |h| per row and 128-column block
     float *part;         // [9M][H] f32, c*w-scaled expert outputs, sorted slot order
     float *y;
-    int M, E, accumulate, rmsnorm, tile_max;
+    int M, E, accumulate, rmsnorm, tile_max, stile_max;
     float c;
 };
 
@@ -101,6 +107,8 @@ struct TimedLaunch {
 };
 
 hipError_t launch_dequant(const void *blocks, uint64_t n_sb, float *out, hipStream_t st);
+hipError_t launch_repack_r16(const void *src, uint64_t src_stride, const void *shared, void *dst, uint64_t dst_stride,
+                             int E, int rows, int cols, hipStream_t st);
 hipError_t launch_gen_iq4xs(void *dst, uint64_t n, uint64_t seed, uint64_t first, hipStream_t st);
 hipError_t launch_gen_normal(float *dst, uint64_t n, uint64_t seed, uint64_t first, float mean,
                              float stdv, hipStream_t st);
@@ -110,11 +118,17 @@ hipError_t launch_router_topk(const float *logits, int M, int E, int renorm, uin
                               float *w, hipStream_t st, KernelTimer *T);
 hipError_t launch_bucket_fill(const BucketArgs &a, hipStream_t st, KernelTimer *T);
 hipError_t launch_decode(int H, int I, const DecodeArgs &a, hipStream_t st, KernelTimer *T);
-hipError_t launch_prefill(int H, int I, const PrefillArgs &a, hipStream_t st, KernelTimer *T);
+// Big-tile GEMMs run on st, small-tile GEMMs on aux (forked after prep with ev_fork and
+// joined back before the combine with ev_join); both streams see the same timer.
+hipError_t launch_prefill(int H, int I, const PrefillArgs &a, hipStream_t st, hipStream_t aux, hipEvent_t ev_fork,
+                          hipEvent_t ev_join, KernelTimer *T);
 hipError_t launch_stack(int H, int I, const StackArgs &a, hipStream_t st, KernelTimer *T);
 hipError_t stack_occupancy(int H, int I, int *blocks_per_cu);
 int stack_blocks(int H);
 
+// Big tiles: PF_BM-slot tiles of every expert plus remainders above PF_SMALL_MAX slots.
+// Small tiles: remainders of 1..PF_SMALL_MAX slots cut into PF_SM-slot tiles (<= 2 per expert).
 inline int tile_max_for(int M, int E1) { return (9 * M + PF_BM - 1) / PF_BM + E1; }
+inline int stile_max_for(int E1) { return 2 * E1; }
 
 } // namespace moe
