@@ -45,34 +45,33 @@ __device__ __forceinline__ void tag_store(uint32_t *p, float v) {
 // lane's 32-float chunk).
 __device__ __forceinline__ int padk(int k) { return k + ((k >> 5) << 2); }
 
-__device__ __forceinline__ uint64_t aload64(const uint64_t *p) {
-    return __hip_atomic_load((const MOE_GLOBAL uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ bool tagged2(uint64_t v) { return (v & 1u) && ((v >> 32) & 1u); }
+// One 16-byte coherent load (four tagged words).  A volatile access compiles to a
+// system-scope load (sc0 sc1): it misses the CU's L1 and the L2 returns the line as last
+// written by any XCD.
+__device__ __forceinline__ u32x4 qload(const u32x4 *p) { return *(const volatile MOE_GLOBAL u32x4 *)p; }
+__device__ __forceinline__ uint32_t qtag(u32x4 v) { return v[0] & v[1] & v[2] & v[3] & 1u; }
 
-// This thread's share of n tagged words -- word pairs tid, tid+nt, ... (at most MAXP) --
-// polled into LDS.  All its loads are in flight together; only the words still untagged
-// are reloaded.  The wait is bounded (see the file comment).
-template <int MAXP>
-__device__ __forceinline__ void poll_words(const uint32_t *__restrict__ src, float *dst, int n, int tid,
-                                           int nt, uint32_t *flags,
-                                           volatile __attribute__((address_space(3))) int *s_abort) {
-    const uint64_t *src2 = reinterpret_cast<const uint64_t *>(src);
-    const int np = n / 2;
-    uint64_t v[MAXP];
+// This thread's share of n tagged words -- 16-byte quads tid, tid+nt, ... (at most MAXQ) --
+// polled into LDS.  All loads of a round are in flight together; a round ends with one
+// wave-wide test, and only the quads still untagged are reloaded.  The loop is kept short
+// on purpose: the time from a producer's store to the end of the wait is dominated by how
+// often each word is re-read.  Every wait is bounded (see the file comment).
+template <int MAXQ>
+__device__ __forceinline__ void poll_quads(const uint32_t *__restrict__ src, float *dst, int n, int tid, int nt,
+                                           uint32_t *flags, volatile __attribute__((address_space(3))) int *s_abort) {
+    const u32x4 *src4 = reinterpret_cast<const u32x4 *>(src);
+    const int nq = n / 4;
+    u32x4 v[MAXQ];
 #pragma unroll
-    for (int j = 0; j < MAXP; ++j) v[j] = (tid + j * nt < np) ? aload64(src2 + tid + j * nt) : ~0ull;
+    for (int j = 0; j < MAXQ; ++j) v[j] = (tid + j * nt < nq) ? qload(src4 + tid + j * nt) : u32x4{1u, 1u, 1u, 1u};
     uint32_t spins = 0;
     while (true) {
-        bool ok = true;
+        uint32_t t = 1u;
 #pragma unroll
-        for (int j = 0; j < MAXP; ++j)
-            if (!tagged2(v[j])) {
-                ok = false;
-                v[j] = aload64(src2 + tid + j * nt);
-            }
-        if (ok || *s_abort) break;
-        if ((++spins & 63u) == 0) {
+        for (int j = 0; j < MAXQ; ++j) t &= qtag(v[j]);
+        if (__all(t)) break;
+        if ((++spins & 31u) == 0) {
+            if (*s_abort) break;
             if (__hip_atomic_load((const MOE_GLOBAL uint32_t *)(flags + 1), __ATOMIC_RELAXED,
                                   __HIP_MEMORY_SCOPE_AGENT)) {
                 *s_abort = 1;
@@ -85,14 +84,14 @@ __device__ __forceinline__ void poll_words(const uint32_t *__restrict__ src, flo
                 break;
             }
         }
+#pragma unroll
+        for (int j = 0; j < MAXQ; ++j)
+            if (!qtag(v[j])) v[j] = qload(src4 + tid + j * nt);
     }
 #pragma unroll
-    for (int j = 0; j < MAXP; ++j) {
-        const int p = tid + j * nt;
-        if (p < np) {
-            dst[padk(2 * p)] = __builtin_bit_cast(float, (uint32_t)v[j]);
-            dst[padk(2 * p + 1)] = __builtin_bit_cast(float, (uint32_t)(v[j] >> 32));
-        }
+    for (int j = 0; j < MAXQ; ++j) {
+        const int q = tid + j * nt;
+        if (q < nq) *reinterpret_cast<u32x4 *>(dst + padk(4 * q)) = v[j];
     }
 }
 
@@ -113,14 +112,15 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     constexpr int XPAD = H + (H / 32) * 4;
     constexpr int HPAD = I + (I / 32) * 4;
     constexpr int NPOLL = 64 * (STK_WAVES - SLOTS - 1);     // polling threads (poller waves)
-    constexpr int XP = (H / 2 + NPOLL - 1) / NPOLL;         // word pairs per poller: x
-    constexpr int HP = (SLOTS * I / 2 + NPOLL - 1) / NPOLL; // word pairs per poller: h
+    constexpr int XP = (H / 4 + NPOLL - 1) / NPOLL;         // quads per poller: x
+    constexpr int HP = (SLOTS * I / 4 + NPOLL - 1) / NPOLL; // quads per poller: h
 
     __shared__ __attribute__((aligned(16))) float xs[XPAD];
     __shared__ __attribute__((aligned(16))) float hs[SLOTS * HPAD];
     __shared__ float part[SLOTS][8];
     __shared__ int rt_id[3][SLOTS];
     __shared__ float rt_w[3][SLOTS];
+    __shared__ const uint8_t *rt_p[3][SLOTS][3]; // per slot: W1, W3, W2 of the routed expert
     __shared__ int s_abort;
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -146,14 +146,20 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             int sel[TOPK];
             float ws[TOPK];
             route_wave<4>(a.logits + (size_t)li * a.E, a.E, a.renorm, lane, sel, ws);
-            if (lane == 0) {
+            // the layer table entry is read here, two layers ahead, so that the compute
+            // waves' weight prefetches never wait on it
+            const LayerPtrs L = load_layer(a.layers + a.layer0 + li);
+            if (lane < SLOTS) {
+                int id = a.E;
+                float wt = 1.0f;
 #pragma unroll
-                for (int r = 0; r < TOPK; ++r) {
-                    rt_id[li % 3][r] = sel[r];
-                    rt_w[li % 3][r] = ws[r];
-                }
-                rt_id[li % 3][TOPK] = a.E;
-                rt_w[li % 3][TOPK] = 1.0f;
+                for (int r = 0; r < TOPK; ++r)
+                    if (lane == r) { id = sel[r]; wt = ws[r]; }
+                rt_id[li % 3][lane] = id;
+                rt_w[li % 3][lane] = wt;
+                rt_p[li % 3][lane][0] = expert_w(L.w1, L.s1, L.sw1, id, a.E);
+                rt_p[li % 3][lane][1] = expert_w(L.w3, L.s3, L.sw3, id, a.E);
+                rt_p[li % 3][lane][2] = expert_w(L.w2, L.s2, L.sw2, id, a.E);
             }
             if (wg == 0 && a.ids_out && lane < SLOTS) {
                 int id = a.E;
@@ -189,10 +195,10 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                     *reinterpret_cast<f32x4 *>(xs + padk(4 * k)) = v;
                 }
             } else {
-                poll_words<XP>(a.xt + (size_t)li * H, xs, H, ptid, NPOLL, a.flags, abort_lds);
+                poll_quads<XP>(a.xt + (size_t)li * H, xs, H, ptid, NPOLL, a.flags, abort_lds);
             }
             lds_barrier(); // B1
-            poll_words<HP>(a.ht + (size_t)li * SLOTS * I, hs, SLOTS * I, ptid, NPOLL, a.flags, abort_lds);
+            poll_quads<HP>(a.ht + (size_t)li * SLOTS * I, hs, SLOTS * I, ptid, NPOLL, a.flags, abort_lds);
             lds_barrier(); // B2
             lds_barrier(); // B3
             lds_barrier(); // B4
@@ -204,13 +210,14 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     u32x4 aq1[2][STA], aq3[2][STA], bq[2][STB];
     u32x2 ah1[2][STA], ah3[2][STA], bh[2][STB];
 
-    // Loads of local layer li's weights for this wave into register slot SL.
-    auto prefetch = [&](auto SLc, int li) __attribute__((always_inline)) {
+    // Loads of local layer li's phase-A (W1, W3) and phase-B (W2) weights for this wave into
+    // register slot SL.  Phase-A weights of layer li+2 are requested as soon as phase A of
+    // layer li has consumed its slot, phase-B weights after phase B, so the two bursts
+    // land in different exchange waits.
+    auto prefetch_a = [&](auto SLc, int li) __attribute__((always_inline)) {
         constexpr int SL = decltype(SLc)::value;
-        const LayerPtrs L = load_layer(a.layers + a.layer0 + li);
-        const int eA = rt_id[li % 3][sA];
-        const uint8_t *W1 = expert_w(L.w1, L.s1, L.sw1, eA, a.E);
-        const uint8_t *W3 = expert_w(L.w3, L.s3, L.sw3, eA, a.E);
+        const uint8_t *W1 = rt_p[li % 3][sA][0];
+        const uint8_t *W3 = rt_p[li % 3][sA][1];
 #pragma unroll
         for (int st = 0; st < STA; ++st) {
             const size_t off = (size_t)(nA0 + st * RPS1 + rr1) * ROWB1 + (size_t)sb1 * SB_BYTES;
@@ -219,8 +226,10 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             ah3[SL][st] = ldg<u32x2>(W3 + off);
             aq3[SL][st] = ldg<u32x4>(W3 + off + 8 + 16 * ib1);
         }
-        const int eB = rt_id[li % 3][wv];
-        const uint8_t *W2 = expert_w(L.w2, L.s2, L.sw2, eB, a.E);
+    };
+    auto prefetch_b = [&](auto SLc, int li) __attribute__((always_inline)) {
+        constexpr int SL = decltype(SLc)::value;
+        const uint8_t *W2 = rt_p[li % 3][wv][2];
 #pragma unroll
         for (int st = 0; st < STB; ++st) {
             const size_t off = (size_t)(8 * wg + st * RPS2 + rr2) * ROWB2 + (size_t)sb2 * SB_BYTES;
@@ -230,8 +239,12 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     };
 
     lds_barrier(); // B0: routing of layers 0 and 1 is in LDS
-    prefetch(std::integral_constant<int, 0>{}, 0);
-    if (n > 1) prefetch(std::integral_constant<int, 1>{}, 1);
+    prefetch_a(std::integral_constant<int, 0>{}, 0);
+    prefetch_b(std::integral_constant<int, 0>{}, 0);
+    if (n > 1) {
+        prefetch_a(std::integral_constant<int, 1>{}, 1);
+        prefetch_b(std::integral_constant<int, 1>{}, 1);
+    }
 
     auto layer = [&](auto SLc, int li) __attribute__((always_inline)) {
         constexpr int SL = decltype(SLc)::value;
@@ -269,6 +282,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 if (g1 == 0) tag_store(hdst + nA0 + st * RPS1 + rr1, silu(g) * u);
             }
         }
+        if (li + 2 < n) prefetch_a(SLc, li + 2);
         lds_barrier(); // B2: h_l in LDS
         // phase B: slot wv's W2 rows against h_l
         {
@@ -294,7 +308,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             }
         }
         // this slot's registers are free: bring in layer li+2 (its routing arrived by B1)
-        if (li + 2 < n) prefetch(SLc, li + 2);
+        if (li + 2 < n) prefetch_b(SLc, li + 2);
         lds_barrier(); // B3: partials in LDS
         // combine in slot order + residual; publish x_{l+1}
         if (tid < 8) {
