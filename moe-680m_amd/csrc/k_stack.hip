@@ -14,56 +14,87 @@
 //   - the routing of layer l+2 is computed during layer l by a dedicated router wave, and
 //     every wave then issues the loads of its share of layer l+2's weights into registers
 //     (two register slots, even/odd layers), so weights stream from HBM two layers ahead;
-//   - x_l and h_l are exchanged through per-layer buffers cleared to zero before the
-//     launch; producers store each f32 with its mantissa LSB forced to 1 (<= 1 ulp) using
-//     agent-scope stores, consumers poll exactly the words they need with agent-scope loads
-//     until every word carries the tag.  No atomics, no fences, no barrier: a phase
-//     transition costs one cross-XCD store->load round trip (~1.4 us measured).
+//   - activations move between workgroups through per-layer buffers cleared to zero
+//     before the launch; producers store each f32 with its mantissa LSB forced to 1
+//     (<= 1 ulp), consumers poll exactly the words they need until every word carries the
+//     tag.  No atomics, no fences, no grid barrier.
+//
+// Work split, mapped onto the eight XCDs (each with its own L2).  Workgroup (k, j) runs on
+// XCD k (read from the hardware register, so the roles follow where the dispatcher put the
+// workgroup) and is the j-th of the NJ = NB/8 workgroups there.  XCD k owns routed slot k
+// (the k-th ranked expert) and 1/8 of the shared expert:
+//   phase A (x -> h): XCD k computes h for all I rows of slot k and for shared rows
+//       [k*I/8, (k+1)*I/8).  Those 9I/8 values are all XCD k's phase B needs, so they are
+//       exchanged inside the XCD only: plain stores (the L2 is the XCD's point of
+//       coherence) and L1-bypassing agent-scope loads that hit in that L2.
+//   phase B (h -> partial): workgroup (k, j) computes, for output rows [64j, 64j+64),
+//       c*w_k*W2_k h_k + c*w_sh*W2_sh[:, cols of XCD k] h_sh -- a K-split: the eight
+//       XCDs' partials sum to the layer's FFN output.
+//   reduce (partial -> x'): workgroup (k, j) gathers the eight partials of its 64 rows
+//       across XCDs (the only cross-XCD traffic: 2 KB per workgroup, write-through stores
+//       and system-scope loads), adds them to the residual in a fixed order -- every XCD
+//       computes bit-identical rows -- and publishes x' inside its XCD, where all NJ
+//       workgroups gather the full vector for the next layer.
+// One cross-XCD round trip and two L2-local ones per layer, instead of two all-gathers of
+// x (8 KB) and h (18 KB) across all 256 workgroups (5.0 us -> 2.6 us measured for the
+// exchanges alone).
 // Every wait is bounded: a poll that exceeds its limit raises MOE_DEVFLAG_TIMEOUT and a
 // global abort word that makes every other poller stop waiting, so all waves always exit.
-// The launch needs all NB workgroups resident at once (one per CU); the host checks this.
+// The launch needs all NB workgroups resident at once (one per CU) and the dispatcher's
+// round-robin placement over the XCDs (workgroups 8j..8j+7 on eight different XCDs); the
+// host checks residency, and a placement that broke the second rule would leave some rows
+// unproduced and end in the bounded-wait error, never in a silent wrong result.
 //
-// Work split (NB workgroups; per workgroup 9 compute waves, 1 router wave and 2 poller
-// waves, so that no polling load ever queues behind a weight prefetch in a wave's
-// in-order load counter):
-//   phase A: the 9*I (W1,W3) row pairs, RPW_A consecutive pairs per compute wave, a lane
-//            owning one 32-weight sub-block of the row (as in k_decode_gate_up);
-//   phase B: WG w owns output rows [8w, 8w+8); compute wave s takes slot s's W2 rows, the
-//            nine contributions are summed in slot order in LDS, the residual added.
+// Per workgroup: 9 compute waves, 1 router wave and 2 poller waves, so that no polling
+// load ever queues behind a weight prefetch in a wave's in-order load counter.
 #include "moe_internal.hpp"
 
 namespace moe {
 
 constexpr uint32_t STK_SPIN_MAX = 1u << 16;
+constexpr int STK_NX = 8; // XCDs
 
+// Cross-XCD publish: an agent-scope store writes through this XCD's L2.
 __device__ __forceinline__ void tag_store(uint32_t *p, float v) {
     __hip_atomic_store((MOE_GLOBAL uint32_t *)p, __builtin_bit_cast(uint32_t, v) | 1u, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
+}
+// XCD-local publish: a plain store, which stays in this XCD's L2.
+__device__ __forceinline__ void tag_store_local(uint32_t *p, float v) {
+    *(MOE_GLOBAL uint32_t *)p = __builtin_bit_cast(uint32_t, v) | 1u;
 }
 
 // LDS index of word k with 4 pad words after every 32 (conflict-free 128-bit reads of a
 // lane's 32-float chunk).
 __device__ __forceinline__ int padk(int k) { return k + ((k >> 5) << 2); }
 
-// One 16-byte coherent load (four tagged words).  A volatile access compiles to a
-// system-scope load (sc0 sc1): it misses the CU's L1 and the L2 returns the line as last
-// written by any XCD.
-__device__ __forceinline__ u32x4 qload(const u32x4 *p) { return *(const volatile MOE_GLOBAL u32x4 *)p; }
 __device__ __forceinline__ uint32_t qtag(u32x4 v) { return v[0] & v[1] & v[2] & v[3] & 1u; }
 
-// This thread's share of n tagged words -- 16-byte quads tid, tid+nt, ... (at most MAXQ) --
-// polled into LDS.  All loads of a round are in flight together; a round ends with one
-// wave-wide test, and only the quads still untagged are reloaded.  The loop is kept short
-// on purpose: the time from a producer's store to the end of the wait is dominated by how
-// often each word is re-read.  Every wait is bounded (see the file comment).
-template <int MAXQ>
-__device__ __forceinline__ void poll_quads(const uint32_t *__restrict__ src, float *dst, int n, int tid, int nt,
-                                           uint32_t *flags, volatile __attribute__((address_space(3))) int *s_abort) {
-    const u32x4 *src4 = reinterpret_cast<const u32x4 *>(src);
-    const int nq = n / 4;
-    u32x4 v[MAXQ];
-#pragma unroll
-    for (int j = 0; j < MAXQ; ++j) v[j] = (tid + j * nt < nq) ? qload(src4 + tid + j * nt) : u32x4{1u, 1u, 1u, 1u};
+// 16-byte loads that miss the CU's L1.  Remote: system scope (sc0 sc1) -- the line comes
+// from memory as last written through by any XCD.  Local: two agent-scope (sc1) atomic
+// 8-byte loads -- served by this XCD's L2, where the plain stores of its workgroups land.
+// Both are volatile or atomic, so the compiler re-issues them on every poll round.
+struct RemoteQuads {
+    const u32x4 *p;
+    __device__ __forceinline__ u32x4 operator()(int q) const { return *(const volatile MOE_GLOBAL u32x4 *)(p + q); }
+};
+struct LocalQuads {
+    const uint64_t *p;
+    __device__ __forceinline__ u32x4 operator()(int q) const {
+        const MOE_GLOBAL uint64_t *g = (const MOE_GLOBAL uint64_t *)(p + 2 * q);
+        const uint64_t lo = __hip_atomic_load(g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t hi = __hip_atomic_load(g + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return u32x4{(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
+    }
+};
+
+// Bounded wait until every quad in v[] is tagged, reloading only the untagged ones.  All
+// loads of a round are in flight together; a round ends with one wave-wide test.  Returns
+// with the abort word set (and the caller's data invalid) when the wait fails.
+template <int MAXQ, typename LD>
+__device__ __forceinline__ void poll_until_tagged(u32x4 (&v)[MAXQ], const int (&q)[MAXQ], const LD &ld,
+                                                  uint32_t *flags,
+                                                  volatile __attribute__((address_space(3))) int *s_abort) {
     uint32_t spins = 0;
     while (true) {
         uint32_t t = 1u;
@@ -86,165 +117,243 @@ __device__ __forceinline__ void poll_quads(const uint32_t *__restrict__ src, flo
         }
 #pragma unroll
         for (int j = 0; j < MAXQ; ++j)
-            if (!qtag(v[j])) v[j] = qload(src4 + tid + j * nt);
+            if (!qtag(v[j])) v[j] = ld(q[j]);
     }
+}
+
+// n tagged words of an XCD-local buffer (this thread: quads tid, tid+nt, ...) into LDS.
+template <int MAXQ>
+__device__ __forceinline__ void gather_local(const uint32_t *__restrict__ src, float *dst, int n, int tid, int nt,
+                                             uint32_t *flags,
+                                             volatile __attribute__((address_space(3))) int *s_abort) {
+    const LocalQuads ld{reinterpret_cast<const uint64_t *>(src)};
+    const int nq = n / 4;
+    int q[MAXQ];
+    u32x4 v[MAXQ];
 #pragma unroll
     for (int j = 0; j < MAXQ; ++j) {
-        const int q = tid + j * nt;
-        if (q < nq) *reinterpret_cast<u32x4 *>(dst + padk(4 * q)) = v[j];
+        q[j] = tid + j * nt;
+        v[j] = (q[j] < nq) ? ld(q[j]) : u32x4{1u, 1u, 1u, 1u};
     }
+    poll_until_tagged<MAXQ>(v, q, ld, flags, s_abort);
+#pragma unroll
+    for (int j = 0; j < MAXQ; ++j)
+        if (q[j] < nq) *reinterpret_cast<f32x4 *>(dst + padk(4 * q[j])) = __builtin_bit_cast(f32x4, v[j]);
+}
+
+// Sum over aligned groups of G adjacent lanes (G = 1, 2, 4, 8), result in every lane.
+template <int G>
+__device__ __forceinline__ float adjacent_sum(float v) {
+    if constexpr (G == 1) return v;
+    else if constexpr (G == 2) return v + dpp_mov<0xB1>(v);
+    else if constexpr (G == 4) {
+        v += dpp_mov<0xB1>(v);
+        return v + dpp_mov<0x4E>(v);
+    } else return group_sum<G>(v);
 }
 
 template <int H, int I>
 __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
-    constexpr int NB = H / 8;                // workgroups; each owns 8 output rows
+    constexpr int NX = STK_NX;
+    constexpr int NB = H / 8;                // workgroups
+    constexpr int NJ = NB / NX;              // workgroups per XCD
+    constexpr int ROWS = H / NJ;             // output rows per workgroup
+    static_assert(NB % NX == 0 && ROWS == 64, "one 64-row block per workgroup");
+    constexpr int HX = I + I / NX;           // h words per XCD: routed slot + shared share
+    constexpr int CPX = I / (32 * NX);       // shared-expert 32-column chunks per XCD
+    static_assert(CPX >= 1 && CPX <= 8 && 64 % CPX == 0, "shared split");
+    // phase A: RPW_A row pairs per compute wave (waves 0..7: slot k, wave 8: shared)
     constexpr int LPR1 = (H / QK) * 8;       // lanes per W1/W3 row
-    constexpr int RPS1 = 64 / LPR1;          // rows per wave step (phase A)
+    constexpr int RPS1 = 64 / LPR1;          // rows per wave step
     constexpr int ROWB1 = (H / QK) * SB_BYTES;
-    constexpr int RPW_A = I / NB;            // row pairs per compute wave
+    constexpr int RPW_A = I / NB;
     static_assert(RPW_A % RPS1 == 0 && RPW_A >= RPS1, "phase A split");
-    constexpr int STA = RPW_A / RPS1;        // phase A steps
+    static_assert(8 * RPW_A * NJ == I && RPW_A * NJ == I / NX, "phase A covers slot k and the shared share");
+    constexpr int STA = RPW_A / RPS1;
+    // phase B: waves 0..7 take 8 rows of W2_k each; wave 8 the shared chunks of all 64 rows
     constexpr int LPR2 = (I / QK) * 8;       // lanes per W2 row
-    constexpr int RPS2 = 64 / LPR2;          // W2 rows per wave step
+    constexpr int RPS2 = 64 / LPR2;
     constexpr int ROWB2 = (I / QK) * SB_BYTES;
     static_assert(8 % RPS2 == 0, "phase B split");
-    constexpr int STB = 8 / RPS2;            // phase B steps
+    constexpr int STB = 8 / RPS2;
+    static_assert(STB == CPX, "wave 8 takes as many steps as waves 0..7");
     constexpr int XPAD = H + (H / 32) * 4;
-    constexpr int HPAD = I + (I / 32) * 4;
+    constexpr int HPAD = HX + (HX / 32) * 4 + 4;
     constexpr int NPOLL = 64 * (STK_WAVES - SLOTS - 1);     // polling threads (poller waves)
     constexpr int XP = (H / 4 + NPOLL - 1) / NPOLL;         // quads per poller: x
-    constexpr int HP = (SLOTS * I / 4 + NPOLL - 1) / NPOLL; // quads per poller: h
+    constexpr int HP = (HX / 4 + NPOLL - 1) / NPOLL;        // quads per poller: h
+    static_assert(HX % 4 == 0 && 32 * CPX <= HX - I, "h layout");
 
     __shared__ __attribute__((aligned(16))) float xs[XPAD];
-    __shared__ __attribute__((aligned(16))) float hs[SLOTS * HPAD];
-    __shared__ float part[SLOTS][8];
-    __shared__ int rt_id[3][SLOTS];
-    __shared__ float rt_w[3][SLOTS];
-    __shared__ const uint8_t *rt_p[3][SLOTS][3]; // per slot: W1, W3, W2 of the routed expert
+    __shared__ __attribute__((aligned(16))) float hs[HPAD];
+    __shared__ float part[2][ROWS];     // this workgroup's slot-k and shared contributions
+    __shared__ __attribute__((aligned(16))) float ps[NX][ROWS]; // the eight XCD partials of its rows
+    __shared__ float rt_w[3][2];        // per layer (ring of 3): weight of slot k, shared
+    __shared__ const uint8_t *rt_p[3][2][3]; // W1, W3, W2 of the routed expert / shared
     __shared__ int s_abort;
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int wg = blockIdx.x;
+    // HW_REG_XCC_ID (readfirstlane: the compiler then knows the value is wave-uniform)
+    const int k = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & (NX - 1));
+    const int j = blockIdx.x / NX;
     const int n = a.n_layers;
     if (tid == 0) s_abort = 0;
     volatile __attribute__((address_space(3))) int *abort_lds =
         (volatile __attribute__((address_space(3))) int *)&s_abort;
 
-    // phase A assignment of compute wave wv
-    const int rp0 = (wg * SLOTS + wv) * RPW_A;       // first row pair (valid for wv < 9)
-    const int sA = rp0 / I, nA0 = rp0 % I;
-    const int g1 = lane % LPR1, rr1 = lane / LPR1, sb1 = g1 >> 3, ib1 = g1 & 7;
-    // phase B assignment: slot wv, rows 8*wg + step*RPS2 + rr2
-    const int g2 = lane % LPR2, rr2 = lane / LPR2, sb2 = g2 >> 3, ib2 = g2 & 7;
+    // exchange buffers of (layer li, XCD k)
+    auto hbuf = [&](int li) { return a.hx + ((size_t)li * NX + k) * HX; };
+    auto pbuf = [&](int li) { return a.px + (size_t)li * NX * H; };
+    auto xbuf = [&](int li) { return a.xx + ((size_t)li * NX + k) * H; }; // x_{li+1}
 
-    // Each role runs its own loop; all three execute the same sequence of LDS barriers:
-    //   prologue: B0 ; per layer: B1 (x_l in LDS), B2 (h_l in LDS), B3 (partials in LDS),
-    //   B4 (x_{l+1} published).  Separate loops keep each role's registers to itself.
     if (wv == SLOTS) {
-        // ---------------- router wave: routing two layers ahead into the LDS ring
-        auto route = [&](int li) __attribute__((always_inline)) {
-            int sel[TOPK];
-            float ws[TOPK];
-            route_wave<4>(a.logits + (size_t)li * a.E, a.E, a.renorm, lane, sel, ws);
-            // the layer table entry is read here, two layers ahead, so that the compute
-            // waves' weight prefetches never wait on it
-            const LayerPtrs L = load_layer(a.layers + a.layer0 + li);
-            if (lane < SLOTS) {
-                int id = a.E;
-                float wt = 1.0f;
-#pragma unroll
-                for (int r = 0; r < TOPK; ++r)
-                    if (lane == r) { id = sel[r]; wt = ws[r]; }
-                rt_id[li % 3][lane] = id;
-                rt_w[li % 3][lane] = wt;
-                rt_p[li % 3][lane][0] = expert_w(L.w1, L.s1, L.sw1, id, a.E);
-                rt_p[li % 3][lane][1] = expert_w(L.w3, L.s3, L.sw3, id, a.E);
-                rt_p[li % 3][lane][2] = expert_w(L.w2, L.s2, L.sw2, id, a.E);
-            }
-            if (wg == 0 && a.ids_out && lane < SLOTS) {
-                int id = a.E;
-                float wt = 1.0f;
-#pragma unroll
-                for (int r = 0; r < TOPK; ++r)
-                    if (lane == r) { id = sel[r]; wt = ws[r]; }
-                *(MOE_GLOBAL uint16_t *)(a.ids_out + (size_t)li * SLOTS + lane) = (uint16_t)id;
-                *(MOE_GLOBAL float *)(a.w_out + (size_t)li * SLOTS + lane) = wt;
-            }
+        // ---------------- router wave: expert pointers two layers ahead into the LDS ring.
+        // The routing of every layer was computed by k_stack_prep; the id, weight and
+        // layer-table entry of the next layer are loaded one layer ahead, so this wave
+        // never waits on memory.
+        int id;
+        float wt;
+        LayerPtrs L;
+        auto fetch = [&](int li) __attribute__((always_inline)) {
+            id = a.rid[(size_t)li * SLOTS + k];
+            wt = a.rwt[(size_t)li * SLOTS + k];
+            L = load_layer(a.layers + a.layer0 + li);
         };
+        auto route = [&](int li) __attribute__((always_inline)) {
+            if (lane < 2) {
+                const int e = lane == 0 ? id : a.E;
+                rt_w[li % 3][lane] = lane == 0 ? wt : 1.0f;
+                rt_p[li % 3][lane][0] = expert_w(L.w1, L.s1, L.sw1, e, a.E);
+                rt_p[li % 3][lane][1] = expert_w(L.w3, L.s3, L.sw3, e, a.E);
+                rt_p[li % 3][lane][2] = expert_w(L.w2, L.s2, L.sw2, e, a.E);
+            }
+            if (li + 1 < n) fetch(li + 1);
+        };
+        fetch(0);
         route(0);
         if (n > 1) route(1);
+        // ring slots not yet routed hold layer 0's pointers: the compute waves' prefetches
+        // are unconditional (see below) and must always find valid addresses
+        for (int r = n > 1 ? 2 : 1; r < 3; ++r)
+            if (lane < 2) {
+                rt_w[r][lane] = rt_w[0][lane];
+                for (int m = 0; m < 3; ++m) rt_p[r][lane][m] = rt_p[0][lane][m];
+            }
         lds_barrier(); // B0
         for (int li = 0; li < n; ++li) {
-            if (li + 2 < n) route(li + 2); // ring slot (li+2)%3 was last read before B4 of li-1
             lds_barrier();                 // B1
+            // ring slot (li+2)%3 was last read before B3 of li-1, and is next read after B2
+            if (li + 2 < n) route(li + 2);
             lds_barrier();                 // B2
             lds_barrier();                 // B3
-            lds_barrier();                 // B4
         }
         return;
     }
 
     if (wv > SLOTS) {
-        // ---------------- poller waves: x_l and h_l into LDS
+        // ---------------- poller waves: x and h into LDS; wave SLOTS+1 also reduces
         const int ptid = tid - 64 * (SLOTS + 1);
+        const bool reducer = wv == SLOTS + 1;
+        for (int q = ptid; q < H / 4; q += NPOLL)
+            *reinterpret_cast<f32x4 *>(xs + padk(4 * q)) = ldg<f32x4>(a.x + 4 * q);
         lds_barrier(); // B0
         for (int li = 0; li < n; ++li) {
-            if (li == 0) {
-                for (int k = ptid; k < H / 4; k += NPOLL) {
-                    f32x4 v = ldg<f32x4>(a.x + 4 * k);
-                    *reinterpret_cast<f32x4 *>(xs + padk(4 * k)) = v;
-                }
-            } else {
-                poll_quads<XP>(a.xt + (size_t)li * H, xs, H, ptid, NPOLL, a.flags, abort_lds);
+            lds_barrier(); // B1: x_li in LDS
+            gather_local<HP>(hbuf(li), hs, HX, ptid, NPOLL, a.flags, abort_lds);
+            lds_barrier(); // B2: h_li in LDS
+            lds_barrier(); // B3: this workgroup's contributions in LDS
+            if (reducer) {
+                // publish this XCD's partial of rows [64j, 64j+64) ...
+                uint32_t *pb = pbuf(li);
+                tag_store(pb + (size_t)k * H + ROWS * j + lane, part[0][lane] + part[1][lane]);
+                // ... gather all eight (lane: quad lane&15 of XCDs lane>>4 and (lane>>4)+4) ...
+                const RemoteQuads ld{reinterpret_cast<const u32x4 *>(pb + ROWS * j)};
+                const int m = lane >> 4, qq = lane & 15;
+                int q[2] = {m * (H / 4) + qq, (m + 4) * (H / 4) + qq};
+                u32x4 v[2] = {ld(q[0]), ld(q[1])};
+                poll_until_tagged<2>(v, q, ld, a.flags, abort_lds);
+                *reinterpret_cast<f32x4 *>(&ps[m][4 * qq]) = __builtin_bit_cast(f32x4, v[0]);
+                *reinterpret_cast<f32x4 *>(&ps[m + 4][4 * qq]) = __builtin_bit_cast(f32x4, v[1]);
+                // lanes read what other lanes of this wave wrote: LDS keeps a wave's
+                // accesses in order, the compiler must too
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                // ... and add them to the residual in XCD order (the same on every XCD)
+                const int row = ROWS * j + lane;
+                float x1 = xs[padk(row)];
+#pragma unroll
+                for (int s = 0; s < NX; ++s) x1 += ps[s][lane];
+                if (li + 1 < n) tag_store_local(xbuf(li) + row, x1);
+                else if (k == 0) *(MOE_GLOBAL float *)(a.y + row) = x1;
             }
-            lds_barrier(); // B1
-            poll_quads<HP>(a.ht + (size_t)li * SLOTS * I, hs, SLOTS * I, ptid, NPOLL, a.flags, abort_lds);
-            lds_barrier(); // B2
-            lds_barrier(); // B3
-            lds_barrier(); // B4
+            if (li + 1 < n) gather_local<XP>(xbuf(li), xs, H, ptid, NPOLL, a.flags, abort_lds);
         }
         return;
     }
 
-    // ---------------- compute waves (wv = 0..8)
+    // ---------------- compute waves (wv = 0..8; wave 8 takes the shared expert's share)
+    const int es = wv < 8 ? 0 : 1;       // rt_p / rt_w index
+    // phase A rows of this wave and where their h goes in the XCD's h vector
+    const int rowA = wv < 8 ? (8 * j + wv) * RPW_A : k * (I / NX) + j * RPW_A;
+    const int hidx = wv < 8 ? rowA : I + j * RPW_A;
+    const int g1 = lane % LPR1, rr1 = lane / LPR1, sb1 = g1 >> 3, ib1 = g1 & 7;
+    uint32_t offA[STA];
+#pragma unroll
+    for (int st = 0; st < STA; ++st) offA[st] = (uint32_t)((rowA + st * RPS1 + rr1) * ROWB1 + sb1 * SB_BYTES);
+    // phase B: the W2 sub-block of each step and the h chunk it multiplies
+    int ibB, hoff;
+    uint32_t offB[STB];
+    if (wv < 8) {
+        const int g2 = lane % LPR2, rr2 = lane / LPR2;
+        ibB = g2 & 7;
+        hoff = padk(32 * g2);
+#pragma unroll
+        for (int st = 0; st < STB; ++st)
+            offB[st] = (uint32_t)((ROWS * j + 8 * wv + st * RPS2 + rr2) * ROWB2 + (g2 >> 3) * SB_BYTES);
+    } else {
+        const int t = lane % CPX, cc = CPX * k + t;
+        ibB = cc & 7;
+        hoff = padk(I + 32 * t);
+#pragma unroll
+        for (int st = 0; st < STB; ++st)
+            offB[st] = (uint32_t)((ROWS * j + (64 * st + lane) / CPX) * ROWB2 + (cc >> 3) * SB_BYTES);
+    }
+
     u32x4 aq1[2][STA], aq3[2][STA], bq[2][STB];
     u32x2 ah1[2][STA], ah3[2][STA], bh[2][STB];
 
     // Loads of local layer li's phase-A (W1, W3) and phase-B (W2) weights for this wave into
-    // register slot SL.  Phase-A weights of layer li+2 are requested as soon as phase A of
-    // layer li has consumed its slot, phase-B weights after phase B, so the two bursts
-    // land in different exchange waits.
+    // register slot SL.  Phase-A weights of layer li+2 are requested after B2 of layer li
+    // (its routing is computed during phase A), phase-B weights after phase B.  The loads
+    // are issued unconditionally -- past the last layer they re-read layer n-1, which is
+    // still cached -- because a conditional burst would make the compiler's load counter
+    // path-dependent and turn the waits for older slots into waits for everything.
     auto prefetch_a = [&](auto SLc, int li) __attribute__((always_inline)) {
         constexpr int SL = decltype(SLc)::value;
-        const uint8_t *W1 = rt_p[li % 3][sA][0];
-        const uint8_t *W3 = rt_p[li % 3][sA][1];
+        const uint8_t *W1 = rt_p[li % 3][es][0];
+        const uint8_t *W3 = rt_p[li % 3][es][1];
 #pragma unroll
         for (int st = 0; st < STA; ++st) {
-            const size_t off = (size_t)(nA0 + st * RPS1 + rr1) * ROWB1 + (size_t)sb1 * SB_BYTES;
-            ah1[SL][st] = ldg<u32x2>(W1 + off);
-            aq1[SL][st] = ldg<u32x4>(W1 + off + 8 + 16 * ib1);
-            ah3[SL][st] = ldg<u32x2>(W3 + off);
-            aq3[SL][st] = ldg<u32x4>(W3 + off + 8 + 16 * ib1);
+            ah1[SL][st] = ldg<u32x2>(W1 + offA[st]);
+            aq1[SL][st] = ldg<u32x4>(W1 + offA[st] + 8 + 16 * ib1);
+            ah3[SL][st] = ldg<u32x2>(W3 + offA[st]);
+            aq3[SL][st] = ldg<u32x4>(W3 + offA[st] + 8 + 16 * ib1);
         }
     };
     auto prefetch_b = [&](auto SLc, int li) __attribute__((always_inline)) {
         constexpr int SL = decltype(SLc)::value;
-        const uint8_t *W2 = rt_p[li % 3][wv][2];
+        const uint8_t *W2 = rt_p[li % 3][es][2];
 #pragma unroll
         for (int st = 0; st < STB; ++st) {
-            const size_t off = (size_t)(8 * wg + st * RPS2 + rr2) * ROWB2 + (size_t)sb2 * SB_BYTES;
-            bh[SL][st] = ldg<u32x2>(W2 + off);
-            bq[SL][st] = ldg<u32x4>(W2 + off + 8 + 16 * ib2);
+            bh[SL][st] = ldg<u32x2>(W2 + offB[st]);
+            bq[SL][st] = ldg<u32x4>(W2 + offB[st] + 8 + 16 * ibB);
         }
     };
 
     lds_barrier(); // B0: routing of layers 0 and 1 is in LDS
     prefetch_a(std::integral_constant<int, 0>{}, 0);
     prefetch_b(std::integral_constant<int, 0>{}, 0);
-    if (n > 1) {
-        prefetch_a(std::integral_constant<int, 1>{}, 1);
-        prefetch_b(std::integral_constant<int, 1>{}, 1);
-    }
+    prefetch_a(std::integral_constant<int, 1>{}, min(1, n - 1));
+    prefetch_b(std::integral_constant<int, 1>{}, min(1, n - 1));
 
     auto layer = [&](auto SLc, int li) __attribute__((always_inline)) {
         constexpr int SL = decltype(SLc)::value;
@@ -272,25 +381,24 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             float xsum = 0.f;
 #pragma unroll
             for (int i = 0; i < 32; ++i) xsum += xv[i];
-            uint32_t *hdst = a.ht + ((size_t)li * SLOTS + sA) * I;
+            uint32_t *hdst = hbuf(li) + hidx;
 #pragma unroll
             for (int st = 0; st < STA; ++st) {
                 float g = sub_scale(ah1[SL][st], ib1) * subblock_dot(aq1[SL][st], xv, xsum);
                 float u = sub_scale(ah3[SL][st], ib1) * subblock_dot(aq3[SL][st], xv, xsum);
                 g = lanes_total<LPR1>(g);
                 u = lanes_total<LPR1>(u);
-                if (g1 == 0) tag_store(hdst + nA0 + st * RPS1 + rr1, silu(g) * u);
+                if (g1 == 0) tag_store_local(hdst + st * RPS1 + rr1, silu(g) * u);
             }
         }
-        if (li + 2 < n) prefetch_a(SLc, li + 2);
-        lds_barrier(); // B2: h_l in LDS
-        // phase B: slot wv's W2 rows against h_l
+        lds_barrier(); // B2: h_l in LDS; routing of layer li+2 in LDS
+        prefetch_a(SLc, min(li + 2, n - 1));
+        // phase B: W2 rows against h, scaled by c * routing weight
         {
             float hv[32];
-            const float *hsrc = hs + wv * HPAD + padk(32 * g2);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                f32x4 q = *reinterpret_cast<const f32x4 *>(hsrc + 4 * i);
+                f32x4 q = *reinterpret_cast<const f32x4 *>(hs + hoff + 4 * i);
                 hv[4 * i + 0] = q[0];
                 hv[4 * i + 1] = q[1];
                 hv[4 * i + 2] = q[2];
@@ -299,27 +407,22 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             float hsum = 0.f;
 #pragma unroll
             for (int i = 0; i < 32; ++i) hsum += hv[i];
-            const float wt = a.c * rt_w[li % 3][wv];
+            const float wt = a.c * rt_w[li % 3][es];
 #pragma unroll
             for (int st = 0; st < STB; ++st) {
-                float d = sub_scale(bh[SL][st], ib2) * subblock_dot(bq[SL][st], hv, hsum);
-                d = group_sum<LPR2>(d);
-                if (g2 == 0) part[wv][st * RPS2 + rr2] = wt * d;
+                float d = sub_scale(bh[SL][st], ibB) * subblock_dot(bq[SL][st], hv, hsum);
+                if (wv < 8) {
+                    d = group_sum<LPR2>(d);
+                    if (lane % LPR2 == 0) part[0][8 * wv + st * RPS2 + lane / LPR2] = wt * d;
+                } else {
+                    d = adjacent_sum<CPX>(d);
+                    if (lane % CPX == 0) part[1][(64 * st + lane) / CPX] = wt * d;
+                }
             }
         }
-        // this slot's registers are free: bring in layer li+2 (its routing arrived by B1)
-        if (li + 2 < n) prefetch_b(SLc, li + 2);
-        lds_barrier(); // B3: partials in LDS
-        // combine in slot order + residual; publish x_{l+1}
-        if (tid < 8) {
-            const int row = 8 * wg + tid;
-            float v = xs[padk(row)];
-#pragma unroll
-            for (int s = 0; s < SLOTS; ++s) v += part[s][tid];
-            if (li + 1 < n) tag_store(a.xt + (size_t)(li + 1) * H + row, v);
-            else *(MOE_GLOBAL float *)(a.y + row) = v;
-        }
-        lds_barrier(); // B4
+        // this slot's registers are free: bring in layer li+2
+        prefetch_b(SLc, min(li + 2, n - 1));
+        lds_barrier(); // B3: contributions in LDS
     };
 
     for (int li = 0; li < n; li += 2) {
@@ -328,18 +431,45 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     }
 }
 
-// Clears the tagged exchange buffers and the abort word before a stack launch (a kernel,
-// not hipMemsetAsync, so the sequence can be captured into a graph).
-__global__ void k_zero_words(uint32_t *__restrict__ p, uint64_t n, uint32_t *flags) {
-    if (blockIdx.x == 0 && threadIdx.x == 0) flags[1] = 0u;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
-        p[i] = 0u;
+// Before a stack launch: clears the tagged exchange buffers and the abort word (a kernel,
+// not hipMemsetAsync, so the sequence can be captured into a graph), and routes every layer
+// -- the logits are an input, so the top-8 of all layers is computed here in parallel, one
+// wave per layer, instead of on the stack's critical path.
+__global__ void k_stack_prep(StackArgs a, uint64_t words) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) a.flags[1] = 0u;
+    u32x4 *p4 = reinterpret_cast<u32x4 *>(a.hx);
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words / 4;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        p4[i] = u32x4{0u, 0u, 0u, 0u};
+    if ((int)blockIdx.x < a.n_layers && threadIdx.x < 64) {
+        const int li = blockIdx.x, lane = threadIdx.x;
+        int sel[TOPK];
+        float ws[TOPK];
+        route_wave<4>(a.logits + (size_t)li * a.E, a.E, a.renorm, lane, sel, ws);
+        if (lane < SLOTS) {
+            int id = a.E;
+            float wt = 1.0f;
+#pragma unroll
+            for (int r = 0; r < TOPK; ++r)
+                if (lane == r) { id = sel[r]; wt = ws[r]; }
+            a.rid[(size_t)li * SLOTS + lane] = (uint16_t)id;
+            a.rwt[(size_t)li * SLOTS + lane] = wt;
+            if (a.ids_out) {
+                a.ids_out[(size_t)li * SLOTS + lane] = (uint16_t)id;
+                a.w_out[(size_t)li * SLOTS + lane] = wt;
+            }
+        }
+    }
+}
+
+size_t stack_exchange_words(int H, int I, int n_layers) {
+    return (size_t)n_layers * STK_NX * ((size_t)I + I / STK_NX + 2 * (size_t)H);
 }
 
 template <int H, int I>
 static hipError_t launch_stack_t(const StackArgs &a, hipStream_t st, KernelTimer *T) {
-    const uint64_t words = (uint64_t)(a.n_layers + 1) * H + (uint64_t)a.n_layers * SLOTS * I;
-    hipLaunchKernelGGL(k_zero_words, dim3(256), dim3(256), 0, st, a.xt, words, a.flags);
+    const uint64_t words = stack_exchange_words(H, I, a.n_layers);
+    hipLaunchKernelGGL(k_stack_prep, dim3(max(512, a.n_layers)), dim3(256), 0, st, a, words);
     {
         TimedLaunch tl(T, MOE_K_DECODE_STACK, st);
         hipLaunchKernelGGL((k_decode_stack<H, I>), dim3(H / 8), dim3(64 * STK_WAVES), 0, st, a);

@@ -40,6 +40,8 @@ struct moe_ctx {
     Tile *tiles = nullptr;       // [tile_max(m_max) + stile_max]
     LayerPtrs *dlayers = nullptr; // device copy of the layer table (decode stack)
     uint32_t *xtag = nullptr;    // decode stack exchange buffers
+    uint16_t *srid = nullptr;    // decode stack: routing of every layer
+    float *srw = nullptr;
     int stack_ok = 0;            // all stack workgroups fit on the device at once
     hipStream_t aux = nullptr;   // prefill small-tile GEMMs (non-blocking, default priority)
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
@@ -147,7 +149,9 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
         {(void **)&c->chunk, nchunk * E1 * 4},
         {(void **)&c->tiles, (tmax + (size_t)stile_max_for((int)E1)) * sizeof(Tile)},
         {(void **)&c->dlayers, (size_t)cfg->n_layers * sizeof(LayerPtrs)},
-        {(void **)&c->xtag, ((size_t)(cfg->n_layers + 1) * H + (size_t)cfg->n_layers * SLOTS * I) * 4},
+        {(void **)&c->xtag, stack_exchange_words(H, I, cfg->n_layers) * 4},
+        {(void **)&c->srid, (size_t)cfg->n_layers * SLOTS * 2},
+        {(void **)&c->srw, (size_t)cfg->n_layers * SLOTS * 4},
     };
     size_t total = 0;
     for (auto &p : parts) total += align_up(p.bytes, 256);
@@ -409,8 +413,11 @@ moe_status moe_decode_stack(moe_ctx *ctx, int layer0, int n_layers, const float 
     a.y = y;
     a.ids_out = ids;
     a.w_out = w;
-    a.xt = ctx->xtag;
-    a.ht = ctx->xtag + (size_t)(n_layers + 1) * H;
+    a.hx = ctx->xtag;
+    a.px = a.hx + (size_t)n_layers * 8 * (I + I / 8);
+    a.xx = a.px + (size_t)n_layers * 8 * H;
+    a.rid = ctx->srid;
+    a.rwt = ctx->srw;
     a.flags = ctx->flags;
     a.E = ctx->cfg.n_experts;
     a.rmsnorm = (flags & MOE_FFN_RMSNORM) ? 1 : 0;

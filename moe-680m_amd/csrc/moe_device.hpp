@@ -229,18 +229,27 @@ __device__ __forceinline__ float unord32(uint32_t o) {
     return __builtin_bit_cast(float, b);
 }
 
-// Softmax + top-8 of one token's E logits (E <= 64*NV, E >= 8) by the calling wave.
+// A token's E logits, lane + 64j into v[j]: unconditional in-bounds loads (index clamped,
+// the surplus masked later), so all NV are in flight together.
+template <int NV>
+__device__ __forceinline__ void load_logits(const float *__restrict__ l, int E, int lane, float (&v)[NV]) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) v[j] = ldg<float>(l + min(lane + 64 * j, E - 1));
+}
+
+// Softmax + top-8 of one token's E logits (E <= 64*NV, E >= 8) by the calling wave, from
+// the values load_logits returned.
 // sel/wsel come out wave-uniform: the 8 ids by (logit desc, index asc) and their weights
 // (softmax probability, or renormalised over the 8 when renorm).
 template <int NV>
-__device__ __forceinline__ void route_wave(const float *__restrict__ l, int E, int renorm, int lane,
-                                           int sel[TOPK], float wsel[TOPK]) {
+__device__ __forceinline__ void route_values(const float (&raw)[NV], int E, int renorm, int lane, int sel[TOPK],
+                                             float wsel[TOPK]) {
     float kf[NV];
     uint32_t ord[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int i = lane + 64 * j;
-        kf[j] = (i < E) ? router_key(ldg<float>(l + i)) : -INFINITY;
+        kf[j] = (i < E) ? router_key(raw[j]) : -INFINITY;
         ord[j] = (i < E) ? ord32(kf[j]) : 0u; // 0 sorts below every real key (-inf is 0x007FFFFF)
     }
     uint32_t taken = 0, selord[TOPK];
@@ -276,6 +285,14 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ l, int E, i
     const float den = renorm ? s8 : Z;
 #pragma unroll
     for (int r = 0; r < TOPK; ++r) wsel[r] = e8[r] / den;
+}
+
+template <int NV>
+__device__ __forceinline__ void route_wave(const float *__restrict__ l, int E, int renorm, int lane, int sel[TOPK],
+                                           float wsel[TOPK]) {
+    float raw[NV];
+    load_logits<NV>(l, E, lane, raw);
+    route_values<NV>(raw, E, renorm, lane, sel, wsel);
 }
 
 // ---------------------------------------------------------------- expert table

@@ -71,8 +71,12 @@ struct StackArgs {
     float *y;                // [H] output activation (may alias x)
     uint16_t *ids_out;       // [n_layers][9] or null
     float *w_out;            // [n_layers][9] or null
-    uint32_t *xt;            // tagged exchange: x_l at xt + l*H (l = 1..n-1)
-    uint32_t *ht;            // tagged exchange: h_l at ht + l*9*I
+    // tagged exchange buffers (stack_exchange_words words from hx on, cleared per launch)
+    uint32_t *hx;            // [n_layers][8 XCDs][I + I/8] h of each XCD's rows
+    uint32_t *px;            // [n_layers][8 XCDs][H] each XCD's partial of the layer output
+    uint32_t *xx;            // [n_layers][8 XCDs][H] x_{l+1}, one copy per XCD
+    uint16_t *rid;           // [n_layers][9] routing of every layer (k_stack_prep)
+    float *rwt;              // [n_layers][9]
     uint32_t *flags;         // [0] sticky device flags, [1] abort word
     int E, rmsnorm, renorm;
     float c;
@@ -125,6 +129,7 @@ hipError_t launch_prefill(int H, int I, const PrefillArgs &a, hipStream_t st, hi
 hipError_t launch_stack(int H, int I, const StackArgs &a, hipStream_t st, KernelTimer *T);
 hipError_t stack_occupancy(int H, int I, int *blocks_per_cu);
 int stack_blocks(int H);
+size_t stack_exchange_words(int H, int I, int n_layers);
 
 // Big tiles: PF_BM-slot tiles of every expert plus remainders above PF_SMALL_MAX slots.
 // Small tiles: remainders of 1..PF_SMALL_MAX slots cut into PF_SM-slot tiles (<= 2 per expert).
