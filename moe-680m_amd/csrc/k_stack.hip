@@ -52,7 +52,8 @@
 namespace moe {
 
 constexpr uint32_t STK_SPIN_MAX = 1u << 16;
-constexpr int STK_NX = 8; // XCDs
+constexpr int STK_NX = 8;   // XCDs
+constexpr int STK_LEAD = 1; // layers of weights in flight ahead of the one being computed
 
 // Cross-XCD publish: an agent-scope store writes through this XCD's L2.
 __device__ __forceinline__ void tag_store(uint32_t *p, float v) {
@@ -152,37 +153,64 @@ __device__ __forceinline__ float adjacent_sum(float v) {
     } else return group_sum<G>(v);
 }
 
+// 8 weights of one qs dword -- weights 4d..4d+3 (low nibbles) and 16+4d..16+4d+3 (high
+// nibbles) of a sub-block -- against their activations xl[0..3], xh[0..3]; unscaled.
+__device__ __forceinline__ float dword_dot(uint32_t q, const float *xl, const float *xh) {
+    uint32_t lo, hi;
+    kv_biased8(q, lo, hi);
+    float a0 = ubyte(lo, 0) * xl[0], a1 = ubyte(lo, 1) * xl[1];
+    a0 = __builtin_fmaf(ubyte(lo, 2), xl[2], a0);
+    a1 = __builtin_fmaf(ubyte(lo, 3), xl[3], a1);
+    a0 = __builtin_fmaf(ubyte(hi, 0), xh[0], a0);
+    a1 = __builtin_fmaf(ubyte(hi, 1), xh[1], a1);
+    a0 = __builtin_fmaf(ubyte(hi, 2), xh[2], a0);
+    a1 = __builtin_fmaf(ubyte(hi, 3), xh[3], a1);
+    const float xs = ((xl[0] + xl[1]) + (xl[2] + xl[3])) + ((xh[0] + xh[1]) + (xh[2] + xh[3]));
+    return (a0 + a1) - 128.f * xs;
+}
+
 template <int H, int I>
 __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     constexpr int NX = STK_NX;
+    constexpr int NCW = STK_CWAVES;          // compute waves, two per SIMD
     constexpr int NB = H / 8;                // workgroups
     constexpr int NJ = NB / NX;              // workgroups per XCD
     constexpr int ROWS = H / NJ;             // output rows per workgroup
-    static_assert(NB % NX == 0 && ROWS == 64, "one 64-row block per workgroup");
-    constexpr int HX = I + I / NX;           // h words per XCD: routed slot + shared share
+    static_assert(NB % NX == 0 && ROWS == 64 && ROWS == 8 * NCW, "one 64-row block per workgroup");
+    constexpr int SRP = I / NB;              // shared-expert row pairs per workgroup
+    constexpr int HX = I + I / NX;           // h of one XCD in LDS: routed slot, then shared share
+    constexpr int HXG = 3 * I;               // ... in the exchange buffer (see phase A)
     constexpr int CPX = I / (32 * NX);       // shared-expert 32-column chunks per XCD
-    static_assert(CPX >= 1 && CPX <= 8 && 64 % CPX == 0, "shared split");
-    // phase A: RPW_A row pairs per compute wave (waves 0..7: slot k, wave 8: shared)
+    static_assert(CPX == 1 || CPX == 2, "shared split");
+    // phase A, slot k: SRP row pairs per compute wave, a lane owning one sub-block of a row
     constexpr int LPR1 = (H / QK) * 8;       // lanes per W1/W3 row
     constexpr int RPS1 = 64 / LPR1;          // rows per wave step
     constexpr int ROWB1 = (H / QK) * SB_BYTES;
-    constexpr int RPW_A = I / NB;
-    static_assert(RPW_A % RPS1 == 0 && RPW_A >= RPS1, "phase A split");
-    static_assert(8 * RPW_A * NJ == I && RPW_A * NJ == I / NX, "phase A covers slot k and the shared share");
-    constexpr int STA = RPW_A / RPS1;
-    // phase B: waves 0..7 take 8 rows of W2_k each; wave 8 the shared chunks of all 64 rows
+    static_assert(SRP % RPS1 == 0 && SRP >= RPS1, "phase A split");
+    static_assert(8 * SRP * NJ == I && SRP * NJ == I / NX, "phase A covers slot k and the shared share");
+    constexpr int STA = SRP / RPS1;
+    // phase A, shared: the workgroup's 2*SRP shared rows, K split over the compute waves,
+    // a lane owning half a sub-block (16 weights)
+    constexpr int SBW = H / (32 * NCW);      // sub-blocks per wave per row
+    constexpr int LPRS = 2 * SBW;            // lanes per shared row
+    constexpr int NSA = 2 * SRP * LPRS;      // lanes in use
+    static_assert(NSA <= 64 && (LPRS & (LPRS - 1)) == 0, "shared phase A split");
+    // phase B: compute wave w owns rows 8w..8w+7 of the workgroup's block: all I columns of
+    // W2_k (one sub-block per lane), and the XCD's CPX shared chunks (one qs dword per lane)
     constexpr int LPR2 = (I / QK) * 8;       // lanes per W2 row
     constexpr int RPS2 = 64 / LPR2;
     constexpr int ROWB2 = (I / QK) * SB_BYTES;
     static_assert(8 % RPS2 == 0, "phase B split");
     constexpr int STB = 8 / RPS2;
-    static_assert(STB == CPX, "wave 8 takes as many steps as waves 0..7");
+    constexpr int LPRB = 4 * CPX;            // lanes per row, shared part
+    constexpr int NSB = 8 * LPRB;
+    static_assert(NSB <= 64, "shared phase B split");
     constexpr int XPAD = H + (H / 32) * 4;
     constexpr int HPAD = HX + (HX / 32) * 4 + 4;
-    constexpr int NPOLL = 64 * (STK_WAVES - SLOTS - 1);     // polling threads (poller waves)
+    constexpr int NPOLL = 64 * (STK_WAVES - NCW - 1);       // polling threads (poller waves)
+    static_assert(NPOLL == 128, "two poller waves");
     constexpr int XP = (H / 4 + NPOLL - 1) / NPOLL;         // quads per poller: x
-    constexpr int HP = (HX / 4 + NPOLL - 1) / NPOLL;        // quads per poller: h
-    static_assert(HX % 4 == 0 && 32 * CPX <= HX - I, "h layout");
+    static_assert(I / NX <= 64 && I / 4 <= 4 * 64, "h gather split");
 
     __shared__ __attribute__((aligned(16))) float xs[XPAD];
     __shared__ __attribute__((aligned(16))) float hs[HPAD];
@@ -202,11 +230,11 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         (volatile __attribute__((address_space(3))) int *)&s_abort;
 
     // exchange buffers of (layer li, XCD k)
-    auto hbuf = [&](int li) { return a.hx + ((size_t)li * NX + k) * HX; };
+    auto hbuf = [&](int li) { return a.hx + ((size_t)li * NX + k) * HXG; };
     auto pbuf = [&](int li) { return a.px + (size_t)li * NX * H; };
     auto xbuf = [&](int li) { return a.xx + ((size_t)li * NX + k) * H; }; // x_{li+1}
 
-    if (wv == SLOTS) {
+    if (wv == NCW) {
         // ---------------- router wave: expert pointers two layers ahead into the LDS ring.
         // The routing of every layer was computed by k_stack_prep; the id, weight and
         // layer-table entry of the next layer are loaded one layer ahead, so this wave
@@ -250,19 +278,54 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         return;
     }
 
-    if (wv > SLOTS) {
-        // ---------------- poller waves: x and h into LDS; wave SLOTS+1 also reduces
-        const int ptid = tid - 64 * (SLOTS + 1);
-        const bool reducer = wv == SLOTS + 1;
+    if (wv > NCW) {
+        // ---------------- poller waves: x and h into LDS; the first also reduces
+        const int ptid = tid - 64 * (NCW + 1);
+        const bool first = wv == NCW + 1;
         for (int q = ptid; q < H / 4; q += NPOLL)
             *reinterpret_cast<f32x4 *>(xs + padk(4 * q)) = ldg<f32x4>(a.x + 4 * q);
         lds_barrier(); // B0
         for (int li = 0; li < n; ++li) {
             lds_barrier(); // B1: x_li in LDS
-            gather_local<HP>(hbuf(li), hs, HX, ptid, NPOLL, a.flags, abort_lds);
+            {
+                // h of the XCD: the first poller wave takes the shared rows (lane t: the 16
+                // words of shared row t -- eight waves' partial (g, u) -- combined here), the
+                // second the routed slot's I words
+                const LocalQuads ld{reinterpret_cast<const uint64_t *>(hbuf(li))};
+                int q[4];
+                u32x4 v[4];
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const bool ok = first ? lane < I / NX : lane + 64 * m < I / 4;
+                    q[m] = first ? I / 4 + 4 * lane + m : lane + 64 * m;
+                    v[m] = ok ? ld(q[m]) : u32x4{1u, 1u, 1u, 1u};
+                }
+                poll_until_tagged<4>(v, q, ld, a.flags, abort_lds);
+                if (first) {
+                    if (lane < I / NX) {
+                        float g = 0.f, u = 0.f;
+#pragma unroll
+                        for (int m = 0; m < 4; ++m) {
+                            // cast the whole vector: a bit_cast of one element of an
+                            // ext_vector lvalue reads element 0 with this compiler
+                            const f32x4 f = __builtin_bit_cast(f32x4, v[m]);
+                            g += f[0];
+                            u += f[1];
+                            g += f[2];
+                            u += f[3];
+                        }
+                        hs[padk(I + lane)] = silu(g) * u;
+                    }
+                } else {
+#pragma unroll
+                    for (int m = 0; m < 4; ++m)
+                        if (lane + 64 * m < I / 4)
+                            *reinterpret_cast<f32x4 *>(hs + padk(4 * q[m])) = __builtin_bit_cast(f32x4, v[m]);
+                }
+            }
             lds_barrier(); // B2: h_li in LDS
             lds_barrier(); // B3: this workgroup's contributions in LDS
-            if (reducer) {
+            if (first) {
                 // publish this XCD's partial of rows [64j, 64j+64) ...
                 uint32_t *pb = pbuf(li);
                 tag_store(pb + (size_t)k * H + ROWS * j + lane, part[0][lane] + part[1][lane]);
@@ -290,47 +353,51 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         return;
     }
 
-    // ---------------- compute waves (wv = 0..8; wave 8 takes the shared expert's share)
-    const int es = wv < 8 ? 0 : 1;       // rt_p / rt_w index
-    // phase A rows of this wave and where their h goes in the XCD's h vector
-    const int rowA = wv < 8 ? (8 * j + wv) * RPW_A : k * (I / NX) + j * RPW_A;
-    const int hidx = wv < 8 ? rowA : I + j * RPW_A;
+    // ---------------- compute waves (w = wv = 0..7)
+    const int w = wv;
+    // phase A, slot k: rows (8j + w)*SRP .. +SRP (also their h index)
+    const int rowA = (8 * j + w) * SRP;
     const int g1 = lane % LPR1, rr1 = lane / LPR1, sb1 = g1 >> 3, ib1 = g1 & 7;
     uint32_t offA[STA];
 #pragma unroll
     for (int st = 0; st < STA; ++st) offA[st] = (uint32_t)((rowA + st * RPS1 + rr1) * ROWB1 + sb1 * SB_BYTES);
-    // phase B: the W2 sub-block of each step and the h chunk it multiplies
-    int ibB, hoff;
+    // phase A, shared: lane -> row ri (pair ri/2, W1 or W3 by ri&1), sub-block sbg of this
+    // wave's K range, half hh.  Lanes past NSA repeat valid addresses; their sums are dropped.
+    const int ri = (lane / LPRS) % (2 * SRP), pA = ri >> 1, mA = ri & 1;
+    const int sbg = w * SBW + ((lane % LPRS) >> 1), hh = lane & 1;
+    const uint32_t offSA = (uint32_t)((k * (I / NX) + j * SRP + pA) * ROWB1 + (sbg >> 3) * SB_BYTES);
+    const uint32_t qSA = 8 + 16 * (sbg & 7) + 8 * hh;
+    const int xSA = padk(32 * sbg) + 8 * hh;
+    // phase B, slot k: rows 8w + st*RPS2 + rr2 of the block, sub-block g2
+    const int g2 = lane % LPR2, rr2 = lane / LPR2, ibB = g2 & 7;
     uint32_t offB[STB];
-    if (wv < 8) {
-        const int g2 = lane % LPR2, rr2 = lane / LPR2;
-        ibB = g2 & 7;
-        hoff = padk(32 * g2);
 #pragma unroll
-        for (int st = 0; st < STB; ++st)
-            offB[st] = (uint32_t)((ROWS * j + 8 * wv + st * RPS2 + rr2) * ROWB2 + (g2 >> 3) * SB_BYTES);
-    } else {
-        const int t = lane % CPX, cc = CPX * k + t;
-        ibB = cc & 7;
-        hoff = padk(I + 32 * t);
-#pragma unroll
-        for (int st = 0; st < STB; ++st)
-            offB[st] = (uint32_t)((ROWS * j + (64 * st + lane) / CPX) * ROWB2 + (cc >> 3) * SB_BYTES);
-    }
+    for (int st = 0; st < STB; ++st)
+        offB[st] = (uint32_t)((ROWS * j + 8 * w + st * RPS2 + rr2) * ROWB2 + (g2 >> 3) * SB_BYTES);
+    // phase B, shared: lane -> row rB of the wave's 8, chunk tB of the XCD's CPX, dword dB
+    const int rB = (lane / LPRB) & 7, tB = (lane >> 2) % CPX, dB = lane & 3, ccB = CPX * k + tB;
+    const uint32_t offSB = (uint32_t)((ROWS * j + 8 * w + rB) * ROWB2 + (ccB >> 3) * SB_BYTES);
+    const uint32_t qSB = 8 + 16 * (ccB & 7) + 4 * dB;
+    const int hSB = padk(I + 32 * tB) + 4 * dB;
 
-    u32x4 aq1[2][STA], aq3[2][STA], bq[2][STB];
-    u32x2 ah1[2][STA], ah3[2][STA], bh[2][STB];
+    // Register slots of weights in flight: layer li's weights sit in slot li % LEAD; the
+    // slot is refilled with layer li+LEAD's as soon as the phase that reads it is done.
+    constexpr int LEAD = STK_LEAD;
+    u32x4 aq1[LEAD][STA], aq3[LEAD][STA], bq[LEAD][STB];
+    u32x2 ah1[LEAD][STA], ah3[LEAD][STA], bh[LEAD][STB], sah[LEAD], saq[LEAD], sbh[LEAD];
+    uint32_t sbq[LEAD];
 
     // Loads of local layer li's phase-A (W1, W3) and phase-B (W2) weights for this wave into
-    // register slot SL.  Phase-A weights of layer li+2 are requested after B2 of layer li
-    // (its routing is computed during phase A), phase-B weights after phase B.  The loads
-    // are issued unconditionally -- past the last layer they re-read layer n-1, which is
-    // still cached -- because a conditional burst would make the compiler's load counter
-    // path-dependent and turn the waits for older slots into waits for everything.
+    // register slot SL: phase-A weights of layer li+LEAD right after phase A of layer li
+    // (after B2, so that the routing computed during phase A is visible), phase-B weights
+    // after phase B.  The loads are issued unconditionally -- past the last layer they
+    // re-read layer n-1, which is still cached -- because a conditional burst would make the
+    // compiler's load counter path-dependent and turn the waits for older slots into waits
+    // for everything.
     auto prefetch_a = [&](auto SLc, int li) __attribute__((always_inline)) {
         constexpr int SL = decltype(SLc)::value;
-        const uint8_t *W1 = rt_p[li % 3][es][0];
-        const uint8_t *W3 = rt_p[li % 3][es][1];
+        const uint8_t *W1 = rt_p[li % 3][0][0];
+        const uint8_t *W3 = rt_p[li % 3][0][1];
 #pragma unroll
         for (int st = 0; st < STA; ++st) {
             ah1[SL][st] = ldg<u32x2>(W1 + offA[st]);
@@ -338,27 +405,37 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             ah3[SL][st] = ldg<u32x2>(W3 + offA[st]);
             aq3[SL][st] = ldg<u32x4>(W3 + offA[st] + 8 + 16 * ib1);
         }
+        const uint8_t *WS = rt_p[li % 3][1][mA];
+        sah[SL] = ldg<u32x2>(WS + offSA);
+        saq[SL] = ldg<u32x2>(WS + offSA + qSA);
     };
     auto prefetch_b = [&](auto SLc, int li) __attribute__((always_inline)) {
         constexpr int SL = decltype(SLc)::value;
-        const uint8_t *W2 = rt_p[li % 3][es][2];
+        const uint8_t *W2 = rt_p[li % 3][0][2];
 #pragma unroll
         for (int st = 0; st < STB; ++st) {
             bh[SL][st] = ldg<u32x2>(W2 + offB[st]);
             bq[SL][st] = ldg<u32x4>(W2 + offB[st] + 8 + 16 * ibB);
         }
+        const uint8_t *WS = rt_p[li % 3][1][2];
+        sbh[SL] = ldg<u32x2>(WS + offSB);
+        sbq[SL] = ldg<uint32_t>(WS + offSB + qSB);
     };
 
     lds_barrier(); // B0: routing of layers 0 and 1 is in LDS
     prefetch_a(std::integral_constant<int, 0>{}, 0);
     prefetch_b(std::integral_constant<int, 0>{}, 0);
-    prefetch_a(std::integral_constant<int, 1>{}, min(1, n - 1));
-    prefetch_b(std::integral_constant<int, 1>{}, min(1, n - 1));
+    if constexpr (LEAD == 2) {
+        prefetch_a(std::integral_constant<int, LEAD - 1>{}, min(1, n - 1));
+        prefetch_b(std::integral_constant<int, LEAD - 1>{}, min(1, n - 1));
+    }
 
     auto layer = [&](auto SLc, int li) __attribute__((always_inline)) {
         constexpr int SL = decltype(SLc)::value;
         lds_barrier(); // B1: x_l in LDS
-        // phase A: h = silu(W1 xin) * (W3 xin) for this wave's row pairs
+        // phase A: h = silu(W1 xin) * (W3 xin) for this wave's slot-k row pairs, and this
+        // wave's K share of the workgroup's shared rows (partial g, u: combined by the
+        // pollers of every workgroup of the XCD)
         {
             float xv[32];
 #pragma unroll
@@ -369,6 +446,17 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 xv[4 * i + 2] = q[2];
                 xv[4 * i + 3] = q[3];
             }
+            float xa[8], xb[8];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const f32x4 qa = *reinterpret_cast<const f32x4 *>(xs + xSA + 4 * i);
+                const f32x4 qb = *reinterpret_cast<const f32x4 *>(xs + xSA + 16 + 4 * i);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    xa[4 * i + e] = qa[e];
+                    xb[4 * i + e] = qb[e];
+                }
+            }
             if (a.rmsnorm) {
                 float ss = 0.f;
 #pragma unroll
@@ -377,28 +465,38 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 const float inv = 1.0f / sqrtf(ss * (1.0f / (float)H) + 1e-6f);
 #pragma unroll
                 for (int i = 0; i < 32; ++i) xv[i] *= inv;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    xa[i] *= inv;
+                    xb[i] *= inv;
+                }
             }
             float xsum = 0.f;
 #pragma unroll
             for (int i = 0; i < 32; ++i) xsum += xv[i];
-            uint32_t *hdst = hbuf(li) + hidx;
+            uint32_t *hb = hbuf(li);
 #pragma unroll
             for (int st = 0; st < STA; ++st) {
                 float g = sub_scale(ah1[SL][st], ib1) * subblock_dot(aq1[SL][st], xv, xsum);
                 float u = sub_scale(ah3[SL][st], ib1) * subblock_dot(aq3[SL][st], xv, xsum);
                 g = lanes_total<LPR1>(g);
                 u = lanes_total<LPR1>(u);
-                if (g1 == 0) tag_store_local(hdst + st * RPS1 + rr1, silu(g) * u);
+                if (g1 == 0) tag_store_local(hb + rowA + st * RPS1 + rr1, silu(g) * u);
             }
+            float sp = sub_scale(sah[SL], sbg & 7) *
+                       (dword_dot(saq[SL][0], xa, xb) + dword_dot(saq[SL][1], xa + 4, xb + 4));
+            sp = adjacent_sum<LPRS>(sp);
+            if (lane % LPRS == 0 && lane < NSA)
+                tag_store_local(hb + I + ((j * SRP + pA) * NCW + w) * 2 + mA, sp);
         }
         lds_barrier(); // B2: h_l in LDS; routing of layer li+2 in LDS
-        prefetch_a(SLc, min(li + 2, n - 1));
+        prefetch_a(SLc, min(li + LEAD, n - 1));
         // phase B: W2 rows against h, scaled by c * routing weight
         {
             float hv[32];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                f32x4 q = *reinterpret_cast<const f32x4 *>(hs + hoff + 4 * i);
+                f32x4 q = *reinterpret_cast<const f32x4 *>(hs + padk(32 * g2) + 4 * i);
                 hv[4 * i + 0] = q[0];
                 hv[4 * i + 1] = q[1];
                 hv[4 * i + 2] = q[2];
@@ -407,27 +505,36 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             float hsum = 0.f;
 #pragma unroll
             for (int i = 0; i < 32; ++i) hsum += hv[i];
-            const float wt = a.c * rt_w[li % 3][es];
+            const float wk = a.c * rt_w[li % 3][0], wsh = a.c * rt_w[li % 3][1];
 #pragma unroll
             for (int st = 0; st < STB; ++st) {
                 float d = sub_scale(bh[SL][st], ibB) * subblock_dot(bq[SL][st], hv, hsum);
-                if (wv < 8) {
-                    d = group_sum<LPR2>(d);
-                    if (lane % LPR2 == 0) part[0][8 * wv + st * RPS2 + lane / LPR2] = wt * d;
-                } else {
-                    d = adjacent_sum<CPX>(d);
-                    if (lane % CPX == 0) part[1][(64 * st + lane) / CPX] = wt * d;
+                d = group_sum<LPR2>(d);
+                if (g2 == 0) part[0][8 * w + st * RPS2 + rr2] = wk * d;
+            }
+            float hl[4], hh4[4];
+            {
+                const f32x4 ql = *reinterpret_cast<const f32x4 *>(hs + hSB);
+                const f32x4 qh = *reinterpret_cast<const f32x4 *>(hs + hSB + 16);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    hl[e] = ql[e];
+                    hh4[e] = qh[e];
                 }
             }
+            float ds = sub_scale(sbh[SL], ccB & 7) * dword_dot(sbq[SL], hl, hh4);
+            ds = adjacent_sum<LPRB>(ds);
+            if (lane % LPRB == 0 && lane < NSB) part[1][8 * w + rB] = wsh * ds;
         }
-        // this slot's registers are free: bring in layer li+2
-        prefetch_b(SLc, min(li + 2, n - 1));
+        // this slot's registers are free: bring in layer li+LEAD
+        prefetch_b(SLc, min(li + LEAD, n - 1));
         lds_barrier(); // B3: contributions in LDS
     };
 
-    for (int li = 0; li < n; li += 2) {
+    for (int li = 0; li < n; li += LEAD) {
         layer(std::integral_constant<int, 0>{}, li);
-        if (li + 1 < n) layer(std::integral_constant<int, 1>{}, li + 1);
+        if constexpr (LEAD == 2)
+            if (li + 1 < n) layer(std::integral_constant<int, LEAD - 1>{}, li + 1);
     }
 }
 
@@ -463,7 +570,7 @@ __global__ void k_stack_prep(StackArgs a, uint64_t words) {
 }
 
 size_t stack_exchange_words(int H, int I, int n_layers) {
-    return (size_t)n_layers * STK_NX * ((size_t)I + I / STK_NX + 2 * (size_t)H);
+    return (size_t)n_layers * STK_NX * (3 * (size_t)I + 2 * (size_t)H);
 }
 
 template <int H, int I>

@@ -414,7 +414,7 @@ moe_status moe_decode_stack(moe_ctx *ctx, int layer0, int n_layers, const float 
     a.ids_out = ids;
     a.w_out = w;
     a.hx = ctx->xtag;
-    a.px = a.hx + (size_t)n_layers * 8 * (I + I / 8);
+    a.px = a.hx + (size_t)n_layers * 8 * 3 * I;
     a.xx = a.px + (size_t)n_layers * 8 * H;
     a.rid = ctx->srid;
     a.rwt = ctx->srw;

@@ -61,7 +61,8 @@ struct PrefillArgs {
     float c;
 };
 
-constexpr int STK_WAVES = SLOTS + 3; // decode stack: 9 compute waves, 1 router wave, 2 poller waves
+constexpr int STK_CWAVES = 8;             // decode stack: 8 compute waves (two per SIMD),
+constexpr int STK_WAVES = STK_CWAVES + 3; // 1 router wave, 2 poller waves
 
 struct StackArgs {
     const LayerPtrs *layers; // device table indexed by absolute layer
@@ -72,7 +73,7 @@ struct StackArgs {
     uint16_t *ids_out;       // [n_layers][9] or null
     float *w_out;            // [n_layers][9] or null
     // tagged exchange buffers (stack_exchange_words words from hx on, cleared per launch)
-    uint32_t *hx;            // [n_layers][8 XCDs][I + I/8] h of each XCD's rows
+    uint32_t *hx;            // [n_layers][8 XCDs][3I] h of each XCD's rows (shared rows as partials)
     uint32_t *px;            // [n_layers][8 XCDs][H] each XCD's partial of the layer output
     uint32_t *xx;            // [n_layers][8 XCDs][H] x_{l+1}, one copy per XCD
     uint16_t *rid;           // [n_layers][9] routing of every layer (k_stack_prep)
