@@ -457,19 +457,15 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                     xb[4 * i + e] = qb[e];
                 }
             }
+            // RMSNorm scales every activation by one factor, applied to each row's result
+            // (after the sums) rather than to the 48 activations of every lane
+            float inv = 1.0f;
             if (a.rmsnorm) {
                 float ss = 0.f;
 #pragma unroll
                 for (int i = 0; i < 32; ++i) ss = __builtin_fmaf(xv[i], xv[i], ss);
                 ss = lanes_total<LPR1>(ss);
-                const float inv = 1.0f / sqrtf(ss * (1.0f / (float)H) + 1e-6f);
-#pragma unroll
-                for (int i = 0; i < 32; ++i) xv[i] *= inv;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    xa[i] *= inv;
-                    xb[i] *= inv;
-                }
+                inv = 1.0f / sqrtf(ss * (1.0f / (float)H) + 1e-6f);
             }
             float xsum = 0.f;
 #pragma unroll
@@ -479,13 +475,13 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             for (int st = 0; st < STA; ++st) {
                 float g = sub_scale(ah1[SL][st], ib1) * subblock_dot(aq1[SL][st], xv, xsum);
                 float u = sub_scale(ah3[SL][st], ib1) * subblock_dot(aq3[SL][st], xv, xsum);
-                g = lanes_total<LPR1>(g);
-                u = lanes_total<LPR1>(u);
+                g = inv * lanes_total<LPR1>(g);
+                u = inv * lanes_total<LPR1>(u);
                 if (g1 == 0) tag_store_local(hb + rowA + st * RPS1 + rr1, silu(g) * u);
             }
             float sp = sub_scale(sah[SL], sbg & 7) *
                        (dword_dot(saq[SL][0], xa, xb) + dword_dot(saq[SL][1], xa + 4, xb + 4));
-            sp = adjacent_sum<LPRS>(sp);
+            sp = inv * adjacent_sum<LPRS>(sp);
             if (lane % LPRS == 0 && lane < NSA)
                 tag_store_local(hb + I + ((j * SRP + pA) * NCW + w) * 2 + mA, sp);
         }

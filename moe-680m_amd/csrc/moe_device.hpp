@@ -62,20 +62,25 @@ __device__ __forceinline__ uint32_t lookup16(uint32_t idx_lo3, uint32_t sel_bit3
 
 // qs dword q (4 bytes = weights j..j+3 low nibbles, j+16..j+19 high nibbles).
 // Returns biased codebook bytes for the low nibbles (lo) and the high nibbles (hi).
+// (x & 0x04040404) | 0x03020100 in one v_bitop3_b32 (truth table 0xEA = (a & b) | c).
+__device__ __forceinline__ uint32_t sel_bit3(uint32_t x) {
+    return __builtin_amdgcn_bitop3_b32(x, 0x04040404u, 0x03020100u, 0xEA);
+}
+
 __device__ __forceinline__ void kv_biased8(uint32_t q, uint32_t &lo, uint32_t &hi) {
     uint32_t a_lo = q & 0x07070707u;
-    uint32_t s_lo = ((q >> 1) & 0x04040404u) | 0x03020100u;
+    uint32_t s_lo = sel_bit3(q >> 1);
     uint32_t a_hi = (q >> 4) & 0x07070707u;
-    uint32_t s_hi = ((q >> 5) & 0x04040404u) | 0x03020100u;
+    uint32_t s_hi = sel_bit3(q >> 5);
     lo = lookup16<KVB0, KVB1, KVB2, KVB3>(a_lo, s_lo);
     hi = lookup16<KVB0, KVB1, KVB2, KVB3>(a_hi, s_hi);
 }
 
 __device__ __forceinline__ void kv_signed8(uint32_t q, uint32_t &lo, uint32_t &hi) {
     uint32_t a_lo = q & 0x07070707u;
-    uint32_t s_lo = ((q >> 1) & 0x04040404u) | 0x03020100u;
+    uint32_t s_lo = sel_bit3(q >> 1);
     uint32_t a_hi = (q >> 4) & 0x07070707u;
-    uint32_t s_hi = ((q >> 5) & 0x04040404u) | 0x03020100u;
+    uint32_t s_hi = sel_bit3(q >> 5);
     lo = lookup16<KVS0, KVS1, KVS2, KVS3>(a_lo, s_lo);
     hi = lookup16<KVS0, KVS1, KVS2, KVS3>(a_hi, s_hi);
 }
