@@ -7,7 +7,8 @@ per layer router softmax/top-8 over seeded logits, RMSNorm + the 9-expert IQ4_XS
 weighted combine + residual.  All 40 x 257 experts (17.2 GB) are resident in HBM and
 every step routes differently, so weights stream from HBM.  `value` is algorithmic bytes
 (602,316,800 per token) / wall time.  The prefill leg (config 1: M=512, Zipf(1.1)-biased
-router) is reported in the same line, with tok/s and the bf16 MFMA fraction.
+router) is reported in the same line, with tok/s and the MFMA fraction (f16 operands; the f16
+and bf16 dense peaks are the same 2.5 PFLOP/s).
 
     python bench.py [--steps K] [--warmup W]      # one JSON line on stdout
 """
@@ -27,7 +28,10 @@ DECODE_BYTES_PER_TOKEN = LAYERS * DECODE_BYTES_PER_LAYER     # 602,316,800
 PREFILL_M = 512
 PREFILL_FLOPS = 2 * (9 * PREFILL_M) * 3 * I * H             # 28,991,029,248
 HBM_PEAK_GBS = 8000.0
-BF16_PEAK_TFLOPS = 2500.0
+BF16_PEAK_TFLOPS = 2500.0  # dense bf16 and f16 MFMA peak
+# HBM bytes per decode-stack launch measured by rocprofv3 (FETCH_SIZE and WRITE_SIZE runs,
+# calibrated on a plain copy); the summary and its commands are in this file:
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_stack_config2.md")
 
 
 def log(*a):
@@ -74,6 +78,18 @@ def cpu_baseline(pkg, layer_dev, seconds):
                       f"residual) of one resident layer in {el:.1f} s; f64 oracle, OpenMP over "
                       f"the 9 experts; host {platform.processor() or platform.machine()}, "
                       f"nproc {os.cpu_count()}"}
+
+
+def profiled_traffic():
+    """traffic_bytes_per_launch from the committed rocprofv3 summary, or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as fh:
+            for line in fh:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def main():
@@ -208,7 +224,7 @@ def main():
     p_tflops = PREFILL_FLOPS / (p_ms * 1e-3) / 1e12
     active = [int(torch.unique(pids[s].view(-1).to(torch.int32)).numel()) for s in range(pw, pn)]
     log(f"prefill M={PREFILL_M}: {p_ms * 1e3:.1f} us/step, {PREFILL_M / (p_ms * 1e-3):.0f} tok/s, "
-        f"{p_tflops:.1f} TFLOP/s = {100 * p_tflops / BF16_PEAK_TFLOPS:.2f}% of bf16 MFMA peak; "
+        f"{p_tflops:.1f} TFLOP/s = {100 * p_tflops / BF16_PEAK_TFLOPS:.2f}% of the f16/bf16 MFMA peak; "
         f"active experts {min(active)}-{max(active)}")
     del pgraphs
     ctx.timing_enable(8 * 64)
@@ -248,12 +264,16 @@ def main():
         "hbm_peak_frac": round(decode_gbs / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "kernel": "decode_stack", "achieved": round(stack_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(stack_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "bytes_per_launch": DECODE_BYTES_PER_TOKEN, "avg_us": stack_us},
+                     "traffic": profiled_traffic(),
+                     "traffic_source": "rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1 per launch, "
+                                       "profiles/decode_stack_config2.md",
+                     "bytes_per_launch": DECODE_BYTES_PER_TOKEN, "avg_us": stack_us},
         "kernels": kern,
         "per_layer_path_kernels": layer_kern,
         "prefill": {"workload": "config 1: M=512, Zipf(1.1) router bias, one layer per step "
                                 "(cycling the 40 resident layers)",
-                    "dtype": "bf16 MFMA, f32 accumulate", "ms_per_step": round(p_ms, 5),
+                    "dtype": "f16 MFMA (operands scaled by exact powers of two), f32 accumulate",
+                    "ms_per_step": round(p_ms, 5),
                     "tok_per_s": round(PREFILL_M / (p_ms * 1e-3), 1),
                     "tflops": round(p_tflops, 2), "mfma_frac": round(p_tflops / BF16_PEAK_TFLOPS, 4),
                     "active_experts": [min(active), max(active)],

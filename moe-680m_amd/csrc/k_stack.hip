@@ -11,9 +11,11 @@
 // and its two data dependencies (x -> h -> next x) are global.  On MI355X a kernel boundary
 // costs ~1.6 us and an atomic grid barrier over 256 workgroups ~8 us, so both the HBM
 // latency and the synchronisation must come off the critical path:
-//   - the routing of layer l+2 is computed during layer l by a dedicated router wave, and
-//     every wave then issues the loads of its share of layer l+2's weights into registers
-//     (two register slots, even/odd layers), so weights stream from HBM two layers ahead;
+//   - the routing of every layer is computed before the launch (k_stack_prep: the logits
+//     are inputs); during layer l a router wave turns layer l+2's expert id into weight
+//     pointers, and every compute wave keeps one layer of its weights in flight in
+//     registers (layer l+1's phase-A weights are requested when phase A of l is done,
+//     phase-B weights when phase B is done);
 //   - activations move between workgroups through per-layer buffers cleared to zero
 //     before the launch; producers store each f32 with its mantissa LSB forced to 1
 //     (<= 1 ulp), consumers poll exactly the words they need until every word carries the
@@ -45,8 +47,9 @@
 // host checks residency, and a placement that broke the second rule would leave some rows
 // unproduced and end in the bounded-wait error, never in a silent wrong result.
 //
-// Per workgroup: 9 compute waves, 1 router wave and 2 poller waves, so that no polling
-// load ever queues behind a weight prefetch in a wave's in-order load counter.
+// Per workgroup: 8 compute waves (two per SIMD, identical work: the shared expert's share is
+// split by K over all of them), 1 router wave and 2 poller waves, so that no polling load
+// ever queues behind a weight prefetch in a wave's in-order load counter.
 #include "moe_internal.hpp"
 
 namespace moe {
