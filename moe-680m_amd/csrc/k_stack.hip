@@ -73,6 +73,15 @@ __device__ __forceinline__ void tag_store_local(uint32_t *p, float v) {
 __device__ __forceinline__ int padk(int k) { return k + ((k >> 5) << 2); }
 
 __device__ __forceinline__ uint32_t qtag(u32x4 v) { return v[0] & v[1] & v[2] & v[3] & 1u; }
+// Tag tests: LSB-tagged f32 words, or words that are never zero once published.
+struct LsbTag {
+    __device__ __forceinline__ uint32_t operator()(u32x4 v) const { return qtag(v); }
+};
+struct NonzeroTag {
+    __device__ __forceinline__ uint32_t operator()(u32x4 v) const {
+        return (uint32_t)((v[0] != 0u) & (v[1] != 0u) & (v[2] != 0u) & (v[3] != 0u));
+    }
+};
 
 // 16-byte loads that miss the CU's L1.  Remote: system scope (sc0 sc1) -- the line comes
 // from memory as last written through by any XCD.  Local: two agent-scope (sc1) atomic
@@ -95,15 +104,16 @@ struct LocalQuads {
 // Bounded wait until every quad in v[] is tagged, reloading only the untagged ones.  All
 // loads of a round are in flight together; a round ends with one wave-wide test.  Returns
 // with the abort word set (and the caller's data invalid) when the wait fails.
-template <int MAXQ, typename LD>
+template <int MAXQ, typename LD, typename TAG = LsbTag>
 __device__ __forceinline__ void poll_until_tagged(u32x4 (&v)[MAXQ], const int (&q)[MAXQ], const LD &ld,
                                                   uint32_t *flags,
-                                                  volatile __attribute__((address_space(3))) int *s_abort) {
+                                                  volatile __attribute__((address_space(3))) int *s_abort,
+                                                  TAG tag = TAG{}) {
     uint32_t spins = 0;
     while (true) {
         uint32_t t = 1u;
 #pragma unroll
-        for (int j = 0; j < MAXQ; ++j) t &= qtag(v[j]);
+        for (int j = 0; j < MAXQ; ++j) t &= tag(v[j]);
         if (__all(t)) break;
         if ((++spins & 31u) == 0) {
             if (*s_abort) break;
@@ -121,28 +131,8 @@ __device__ __forceinline__ void poll_until_tagged(u32x4 (&v)[MAXQ], const int (&
         }
 #pragma unroll
         for (int j = 0; j < MAXQ; ++j)
-            if (!qtag(v[j])) v[j] = ld(q[j]);
+            if (!tag(v[j])) v[j] = ld(q[j]);
     }
-}
-
-// n tagged words of an XCD-local buffer (this thread: quads tid, tid+nt, ...) into LDS.
-template <int MAXQ>
-__device__ __forceinline__ void gather_local(const uint32_t *__restrict__ src, float *dst, int n, int tid, int nt,
-                                             uint32_t *flags,
-                                             volatile __attribute__((address_space(3))) int *s_abort) {
-    const LocalQuads ld{reinterpret_cast<const uint64_t *>(src)};
-    const int nq = n / 4;
-    int q[MAXQ];
-    u32x4 v[MAXQ];
-#pragma unroll
-    for (int j = 0; j < MAXQ; ++j) {
-        q[j] = tid + j * nt;
-        v[j] = (q[j] < nq) ? ld(q[j]) : u32x4{1u, 1u, 1u, 1u};
-    }
-    poll_until_tagged<MAXQ>(v, q, ld, flags, s_abort);
-#pragma unroll
-    for (int j = 0; j < MAXQ; ++j)
-        if (q[j] < nq) *reinterpret_cast<f32x4 *>(dst + padk(4 * q[j])) = __builtin_bit_cast(f32x4, v[j]);
 }
 
 // Sum over aligned groups of G adjacent lanes (G = 1, 2, 4, 8), result in every lane.
@@ -154,6 +144,61 @@ __device__ __forceinline__ float adjacent_sum(float v) {
         v += dpp_mov<0xB1>(v);
         return v + dpp_mov<0x4E>(v);
     } else return group_sum<G>(v);
+}
+
+// ---------------------------------------------------------------- int8 activations
+// Phase A reads x as two int8 planes per 32-element chunk c (one IQ4_XS sub-block of K):
+//     x_i ~= s_c * (xh_i + xl_i / 256),  s_c = max_c |x| / 127,  xh = rint(x / s_c),
+//     xl = rint(256 * (x / s_c - xh)),
+// so a sub-block dot is two integer dot products of the signed codebook bytes
+// (v_dot4_i32_i8) with f32 scaling once per sub-block.  Error per element <= s_c / 256,
+// i.e. <= 1.6e-5 of the chunk's largest |x|.  In the exchange, element pair (2w, 2w+1) is
+// one word [xl_2w, xh_2w ^ 0x80, xl_2w+1, xh_2w+1 ^ 0x80]: xh is never -128, so byte 1 is
+// never zero and a published word is never zero -- the exchange tag is "word != 0"
+// (the zero-cleared buffer), which costs no bit of precision.
+__device__ __forceinline__ float quant_ratio(float am) { return am > 1e-30f ? 127.0f / am : 0.0f; }
+
+__device__ __forceinline__ uint32_t pack_pair(float xe, float xo, float r) {
+    const float ue = xe * r, uo = xo * r;
+    // the clamps also map a non-finite input to a finite byte, so the tag always holds
+    const float he = fminf(fmaxf(rintf(ue), -127.0f), 127.0f), ho = fminf(fmaxf(rintf(uo), -127.0f), 127.0f);
+    const float le = fminf(fmaxf(rintf((ue - he) * 256.0f), -127.0f), 127.0f);
+    const float lo = fminf(fmaxf(rintf((uo - ho) * 256.0f), -127.0f), 127.0f);
+    return (((uint32_t)(int)le & 0xFFu) | (((uint32_t)(int)he & 0xFFu) << 8) | (((uint32_t)(int)lo & 0xFFu) << 16) |
+            (((uint32_t)(int)ho & 0xFFu) << 24)) ^ 0x80008000u;
+}
+
+// LDS planes: chunk c at XQS * c: xh dwords 0..7 (elements 4d..4d+3), xl dwords 8..15,
+// 4 pad dwords (a lane's 128-bit reads of its chunk are conflict-free across lanes).
+constexpr int XQS = 20;
+
+// Exchange quad q (elements 8q..8q+7, four pair words) into the planes.
+__device__ __forceinline__ void store_quad(uint32_t *xq, int q, u32x4 v) {
+    uint32_t *c = xq + XQS * (q >> 2) + 2 * (q & 3);
+    *reinterpret_cast<u32x2 *>(c) = u32x2{__builtin_amdgcn_perm(v[1], v[0], 0x07050301u) ^ 0x80808080u,
+                                          __builtin_amdgcn_perm(v[3], v[2], 0x07050301u) ^ 0x80808080u};
+    *reinterpret_cast<u32x2 *>(c + 8) =
+        u32x2{__builtin_amdgcn_perm(v[1], v[0], 0x06040200u), __builtin_amdgcn_perm(v[3], v[2], 0x06040200u)};
+}
+
+// One qs dword (weights 4d..4d+3 low nibbles, 16+4d.. high nibbles) against the planes'
+// dwords of those elements: xh_lo = dword d, xh_hi = dword 4+d (and the same for xl).
+__device__ __forceinline__ void dword_idot(uint32_t q, uint32_t xh_lo, uint32_t xh_hi, uint32_t xl_lo,
+                                           uint32_t xl_hi, int &ah, int &al) {
+    uint32_t lo, hi;
+    kv_signed8(q, lo, hi);
+    ah = __builtin_amdgcn_sdot4((int)lo, (int)xh_lo, ah, false);
+    ah = __builtin_amdgcn_sdot4((int)hi, (int)xh_hi, ah, false);
+    al = __builtin_amdgcn_sdot4((int)lo, (int)xl_lo, al, false);
+    al = __builtin_amdgcn_sdot4((int)hi, (int)xl_hi, al, false);
+}
+
+// Whole sub-block against chunk planes xh[8], xl[8]: sum kv * (xh + xl/256), unscaled.
+__device__ __forceinline__ float subblock_idot(u32x4 qs, const uint32_t (&xh)[8], const uint32_t (&xl)[8]) {
+    int ah = 0, al = 0;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) dword_idot(qs[d], xh[d], xh[4 + d], xl[d], xl[4 + d], ah, al);
+    return __builtin_fmaf((float)al, 1.0f / 256.0f, (float)ah);
 }
 
 // 8 weights of one qs dword -- weights 4d..4d+3 (low nibbles) and 16+4d..16+4d+3 (high
@@ -208,14 +253,20 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     constexpr int LPRB = 4 * CPX;            // lanes per row, shared part
     constexpr int NSB = 8 * LPRB;
     static_assert(NSB <= 64, "shared phase B split");
-    constexpr int XPAD = H + (H / 32) * 4;
+    constexpr int NCH = H / 32;              // x chunks (= sub-blocks along K)
     constexpr int HPAD = HX + (HX / 32) * 4 + 4;
     constexpr int NPOLL = 64 * (STK_WAVES - NCW - 1);       // polling threads (poller waves)
     static_assert(NPOLL == 128, "two poller waves");
-    constexpr int XP = (H / 4 + NPOLL - 1) / NPOLL;         // quads per poller: x
+    // x exchange of one (layer, XCD): H/2 pair words, H/32 chunk scales, NJ per-workgroup
+    // sums of squares -- XQ quads
+    constexpr int XD = H / 8, XS = H / 128, NSS = NJ / 4, XQ = XD + XS + NSS;
+    static_assert(NSS >= 2 && 4 * XQ == H / 2 + H / 32 + NJ, "x exchange layout");
+    constexpr int XP = (XQ + NPOLL - 1) / NPOLL;            // quads per poller: x
     static_assert(I / NX <= 64 && I / 4 <= 4 * 64, "h gather split");
 
-    __shared__ __attribute__((aligned(16))) float xs[XPAD];
+    __shared__ __attribute__((aligned(16))) uint32_t xq[NCH * XQS]; // x as int8 planes
+    __shared__ __attribute__((aligned(16))) float xsc[NCH];         // ... and chunk scales
+    __shared__ __attribute__((aligned(16))) float ssq[NSS];         // partial sums of x^2
     __shared__ __attribute__((aligned(16))) float hs[HPAD];
     __shared__ float part[2][ROWS];     // this workgroup's slot-k and shared contributions
     __shared__ __attribute__((aligned(16))) float ps[NX][ROWS]; // the eight XCD partials of its rows
@@ -235,7 +286,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     // exchange buffers of (layer li, XCD k)
     auto hbuf = [&](int li) { return a.hx + ((size_t)li * NX + k) * HXG; };
     auto pbuf = [&](int li) { return a.px + (size_t)li * NX * H; };
-    auto xbuf = [&](int li) { return a.xx + ((size_t)li * NX + k) * H; }; // x_{li+1}
+    auto xbuf = [&](int li) { return a.xx + ((size_t)li * NX + k) * (4 * XQ); }; // x_{li+1}
 
     if (wv == NCW) {
         // ---------------- router wave: expert pointers two layers ahead into the LDS ring.
@@ -285,8 +336,32 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         // ---------------- poller waves: x and h into LDS; the first also reduces
         const int ptid = tid - 64 * (NCW + 1);
         const bool first = wv == NCW + 1;
-        for (int q = ptid; q < H / 4; q += NPOLL)
-            *reinterpret_cast<f32x4 *>(xs + padk(4 * q)) = ldg<f32x4>(a.x + 4 * q);
+        // x_0 from the input: quad q (8 elements) per thread, a chunk on four adjacent lanes
+        {
+            float ss = 0.f;
+            for (int q = ptid; q < XD; q += NPOLL) {
+                const f32x4 x0 = ldg<f32x4>(a.x + 8 * q), x1 = ldg<f32x4>(a.x + 8 * q + 4);
+                float am = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    am = fmaxf(am, fmaxf(fabsf(x0[e]), fabsf(x1[e])));
+                    ss = __builtin_fmaf(x0[e], x0[e], ss);
+                    ss = __builtin_fmaf(x1[e], x1[e], ss);
+                }
+                am = fmaxf(am, dpp_mov<0xB1>(am));
+                am = fmaxf(am, dpp_mov<0x4E>(am));
+                const float r = quant_ratio(am);
+                store_quad(xq, q,
+                           u32x4{pack_pair(x0[0], x0[1], r), pack_pair(x0[2], x0[3], r),
+                                 pack_pair(x1[0], x1[1], r), pack_pair(x1[2], x1[3], r)});
+                if ((q & 3) == 0) xsc[q >> 2] = am / 127.0f;
+            }
+            ss = wave_sum(ss);
+            if (lane == 0) ssq[first ? 0 : 1] = ss;
+            if (first && lane >= 2 && lane < NSS) ssq[lane] = 0.f;
+        }
+        // the reducer's own 64 rows of the residual, kept in f32
+        float xres = first ? a.x[ROWS * j + lane] : 0.f;
         lds_barrier(); // B0
         for (int li = 0; li < n; ++li) {
             lds_barrier(); // B1: x_li in LDS
@@ -345,13 +420,54 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
                 // ... and add them to the residual in XCD order (the same on every XCD)
                 const int row = ROWS * j + lane;
-                float x1 = xs[padk(row)];
+                float x1 = xres;
 #pragma unroll
                 for (int s = 0; s < NX; ++s) x1 += ps[s][lane];
-                if (li + 1 < n) tag_store_local(xbuf(li) + row, x1);
-                else if (k == 0) *(MOE_GLOBAL float *)(a.y + row) = x1;
+                xres = x1;
+                if (li + 1 < n) {
+                    // publish x' as int8 planes: lanes 0-31 and 32-63 are chunks 2j, 2j+1
+                    uint32_t *xb = xbuf(li);
+                    float am = fabsf(x1);
+                    am = fmaxf(am, dpp_mov<0xB1>(am));
+                    am = fmaxf(am, dpp_mov<0x4E>(am));
+                    am = fmaxf(am, dpp_mov<0x141>(am));
+                    am = fmaxf(am, dpp_mov<0x140>(am));
+                    am = fmaxf(am, __shfl_xor(am, 16));
+                    const float xo = dpp_mov<0xB1>(x1); // the odd partner of an even lane
+                    const float ss = wave_sum(x1 * x1);
+                    if ((lane & 1) == 0)
+                        *(MOE_GLOBAL uint32_t *)(xb + (row >> 1)) = pack_pair(x1, xo, quant_ratio(am));
+                    if ((lane & 31) == 0) tag_store_local(xb + H / 2 + (row >> 5), am / 127.0f);
+                    if (lane == 0) tag_store_local(xb + H / 2 + H / 32 + j, ss);
+                } else if (k == 0) {
+                    *(MOE_GLOBAL float *)(a.y + row) = x1;
+                }
             }
-            if (li + 1 < n) gather_local<XP>(xbuf(li), xs, H, ptid, NPOLL, a.flags, abort_lds);
+            if (li + 1 < n) {
+                // x_{li+1} of this XCD into the planes, scales and partial sums of squares
+                const LocalQuads ld{reinterpret_cast<const uint64_t *>(xbuf(li))};
+                int q[XP];
+                u32x4 v[XP];
+#pragma unroll
+                for (int m = 0; m < XP; ++m) {
+                    q[m] = ptid + m * NPOLL;
+                    v[m] = q[m] < XQ ? ld(q[m]) : u32x4{1u, 1u, 1u, 1u};
+                }
+                // pair words are tagged by being nonzero; the scales and sums of squares
+                // are LSB-tagged f32 words, which are nonzero too
+                poll_until_tagged<XP>(v, q, ld, a.flags, abort_lds, NonzeroTag{});
+#pragma unroll
+                for (int m = 0; m < XP; ++m) {
+                    if (q[m] < XD) {
+                        store_quad(xq, q[m], v[m]);
+                    } else if (q[m] < XD + XS) {
+                        *reinterpret_cast<f32x4 *>(xsc + 4 * (q[m] - XD)) = __builtin_bit_cast(f32x4, v[m]);
+                    } else if (q[m] < XQ) {
+                        const f32x4 f = __builtin_bit_cast(f32x4, v[m]);
+                        ssq[q[m] - XD - XS] = (f[0] + f[1]) + (f[2] + f[3]);
+                    }
+                }
+            }
         }
         return;
     }
@@ -370,7 +486,6 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     const int sbg = w * SBW + ((lane % LPRS) >> 1), hh = lane & 1;
     const uint32_t offSA = (uint32_t)((k * (I / NX) + j * SRP + pA) * ROWB1 + (sbg >> 3) * SB_BYTES);
     const uint32_t qSA = 8 + 16 * (sbg & 7) + 8 * hh;
-    const int xSA = padk(32 * sbg) + 8 * hh;
     // phase B, slot k: rows 8w + st*RPS2 + rr2 of the block, sub-block g2
     const int g2 = lane % LPR2, rr2 = lane / LPR2, ibB = g2 & 7;
     uint32_t offB[STB];
@@ -440,50 +555,46 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         // wave's K share of the workgroup's shared rows (partial g, u: combined by the
         // pollers of every workgroup of the XCD)
         {
-            float xv[32];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                f32x4 q = *reinterpret_cast<const f32x4 *>(xs + padk(32 * g1) + 4 * i);
-                xv[4 * i + 0] = q[0];
-                xv[4 * i + 1] = q[1];
-                xv[4 * i + 2] = q[2];
-                xv[4 * i + 3] = q[3];
-            }
-            float xa[8], xb[8];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const f32x4 qa = *reinterpret_cast<const f32x4 *>(xs + xSA + 4 * i);
-                const f32x4 qb = *reinterpret_cast<const f32x4 *>(xs + xSA + 16 + 4 * i);
+            // this lane's chunk (sub-block g1) of x as int8 planes, and its scale
+            uint32_t xh[8], xl[8];
+            {
+                const u32x4 *c = reinterpret_cast<const u32x4 *>(xq + XQS * g1);
+                const u32x4 h0 = c[0], h1 = c[1], l0 = c[2], l1 = c[3];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    xa[4 * i + e] = qa[e];
-                    xb[4 * i + e] = qb[e];
+                    xh[e] = h0[e];
+                    xh[4 + e] = h1[e];
+                    xl[e] = l0[e];
+                    xl[4 + e] = l1[e];
                 }
             }
+            const float sx = xsc[g1];
+            // shared half sub-block: qs dwords 2hh, 2hh+1 of sub-block sbg
+            const uint32_t *cs = xq + XQS * sbg + 2 * hh;
+            const u32x2 sxh0 = *reinterpret_cast<const u32x2 *>(cs), sxh1 = *reinterpret_cast<const u32x2 *>(cs + 4);
+            const u32x2 sxl0 = *reinterpret_cast<const u32x2 *>(cs + 8), sxl1 = *reinterpret_cast<const u32x2 *>(cs + 12);
+            const float ssx = xsc[sbg];
             // RMSNorm scales every activation by one factor, applied to each row's result
-            // (after the sums) rather than to the 48 activations of every lane
             float inv = 1.0f;
             if (a.rmsnorm) {
                 float ss = 0.f;
 #pragma unroll
-                for (int i = 0; i < 32; ++i) ss = __builtin_fmaf(xv[i], xv[i], ss);
-                ss = lanes_total<LPR1>(ss);
+                for (int i = 0; i < NSS; ++i) ss += ssq[i];
                 inv = 1.0f / sqrtf(ss * (1.0f / (float)H) + 1e-6f);
             }
-            float xsum = 0.f;
-#pragma unroll
-            for (int i = 0; i < 32; ++i) xsum += xv[i];
             uint32_t *hb = hbuf(li);
 #pragma unroll
             for (int st = 0; st < STA; ++st) {
-                float g = sub_scale(ah1[SL][st], ib1) * subblock_dot(aq1[SL][st], xv, xsum);
-                float u = sub_scale(ah3[SL][st], ib1) * subblock_dot(aq3[SL][st], xv, xsum);
+                float g = (sub_scale(ah1[SL][st], ib1) * sx) * subblock_idot(aq1[SL][st], xh, xl);
+                float u = (sub_scale(ah3[SL][st], ib1) * sx) * subblock_idot(aq3[SL][st], xh, xl);
                 g = inv * lanes_total<LPR1>(g);
                 u = inv * lanes_total<LPR1>(u);
                 if (g1 == 0) tag_store_local(hb + rowA + st * RPS1 + rr1, silu(g) * u);
             }
-            float sp = sub_scale(sah[SL], sbg & 7) *
-                       (dword_dot(saq[SL][0], xa, xb) + dword_dot(saq[SL][1], xa + 4, xb + 4));
+            int sah_i = 0, sal_i = 0;
+            dword_idot(saq[SL][0], sxh0[0], sxh1[0], sxl0[0], sxl1[0], sah_i, sal_i);
+            dword_idot(saq[SL][1], sxh0[1], sxh1[1], sxl0[1], sxl1[1], sah_i, sal_i);
+            float sp = (sub_scale(sah[SL], sbg & 7) * ssx) * __builtin_fmaf((float)sal_i, 1.0f / 256.0f, (float)sah_i);
             sp = inv * adjacent_sum<LPRS>(sp);
             if (lane % LPRS == 0 && lane < NSA)
                 tag_store_local(hb + I + ((j * SRP + pA) * NCW + w) * 2 + mA, sp);
@@ -568,8 +679,10 @@ __global__ void k_stack_prep(StackArgs a, uint64_t words) {
     }
 }
 
+// Per layer and XCD: h (3I words), the XCD's partial of every row (H), and x' as int8
+// pair words + chunk scales + per-workgroup sums of squares (H/2 + H/32 + H/64).
 size_t stack_exchange_words(int H, int I, int n_layers) {
-    return (size_t)n_layers * STK_NX * (3 * (size_t)I + 2 * (size_t)H);
+    return (size_t)n_layers * STK_NX * (3 * (size_t)I + (size_t)H + (size_t)(H / 2 + H / 32 + H / 64));
 }
 
 template <int H, int I>

@@ -122,7 +122,10 @@ def test_stack_matches_per_layer_path(gpu, full):
     torch.cuda.synchronize()
     err = normwise_err(y.cpu().numpy(), xr.view(-1).cpu().numpy())
     log(f"  stack vs per-layer normwise diff {err:.3e}")
-    assert err <= 1e-5
+    # the stack's W1/W3 products read x as two int8 planes per 32-element chunk (error per
+    # element <= 1/512 of the chunk scale, 1.6e-5 of the chunk's largest |x|); the per-layer
+    # path reads f32.  Over these six layers the two differ by ~8e-5 (measured).
+    assert err <= 2e-4
 
 
 def test_stack_graph_replays(gpu, full):
