@@ -135,6 +135,13 @@ __device__ __forceinline__ void poll_until_tagged(u32x4 (&v)[MAXQ], const int (&
     }
 }
 
+// Total of each group of G lanes, complete in lane 63 for G = 64 and in every lane otherwise.
+template <int G>
+__device__ __forceinline__ float row_total(float v) {
+    if constexpr (G == 64) return wave_sum_last(v);
+    else return group_sum<G>(v);
+}
+
 // Sum over aligned groups of G adjacent lanes (G = 1, 2, 4, 8), result in every lane.
 template <int G>
 __device__ __forceinline__ float adjacent_sum(float v) {
@@ -262,12 +269,13 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     constexpr int XD = H / 8, XS = H / 128, NSS = NJ / 4, XQ = XD + XS + NSS;
     static_assert(NSS >= 2 && 4 * XQ == H / 2 + H / 32 + NJ, "x exchange layout");
     constexpr int XP = (XQ + NPOLL - 1) / NPOLL;            // quads per poller: x
-    static_assert(I / NX <= 64 && I / 4 <= 4 * 64, "h gather split");
+    static_assert(I / NX <= 64 && I / 4 <= 4 * 64 && (I / 4) % 64 == 0, "h gather split");
 
     __shared__ __attribute__((aligned(16))) uint32_t xq[NCH * XQS]; // x as int8 planes
     __shared__ __attribute__((aligned(16))) float xsc[NCH];         // ... and chunk scales
     __shared__ __attribute__((aligned(16))) float ssq[NSS];         // partial sums of x^2
     __shared__ __attribute__((aligned(16))) float hs[HPAD];
+    __shared__ float hsm[I / 32];       // sums of h_k's 32-element chunks
     __shared__ float part[2][ROWS];     // this workgroup's slot-k and shared contributions
     __shared__ __attribute__((aligned(16))) float ps[NX][ROWS]; // the eight XCD partials of its rows
     __shared__ float rt_w[3][2];        // per layer (ring of 3): weight of slot k, shared
@@ -392,13 +400,19 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                             g += f[2];
                             u += f[3];
                         }
-                        hs[padk(I + lane)] = silu(g) * u;
+                        hs[padk(I + lane)] = silu_rcp(g) * u;
                     }
                 } else {
 #pragma unroll
                     for (int m = 0; m < 4; ++m)
-                        if (lane + 64 * m < I / 4)
-                            *reinterpret_cast<f32x4 *>(hs + padk(4 * q[m])) = __builtin_bit_cast(f32x4, v[m]);
+                        if (64 * m < I / 4) { // wave-uniform: I/4 is a multiple of 64
+                            const f32x4 f = __builtin_bit_cast(f32x4, v[m]);
+                            *reinterpret_cast<f32x4 *>(hs + padk(4 * q[m])) = f;
+                            // chunk sums of h_k (eight adjacent lanes per chunk) for the biased
+                            // codebook correction of phase B
+                            const float cs = group_sum<8>((f[0] + f[1]) + (f[2] + f[3]));
+                            if ((q[m] & 7) == 0) hsm[q[m] >> 3] = cs;
+                        }
                 }
             }
             lds_barrier(); // B2: h_li in LDS
@@ -477,6 +491,8 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     // phase A, slot k: rows (8j + w)*SRP .. +SRP (also their h index)
     const int rowA = (8 * j + w) * SRP;
     const int g1 = lane % LPR1, rr1 = lane / LPR1, sb1 = g1 >> 3, ib1 = g1 & 7;
+    // the lane of each row group that holds the row's total (see row_total)
+    constexpr int LPR1_LAST = LPR1 == 64 ? 63 : 0;
     uint32_t offA[STA];
 #pragma unroll
     for (int st = 0; st < STA; ++st) offA[st] = (uint32_t)((rowA + st * RPS1 + rr1) * ROWB1 + sb1 * SB_BYTES);
@@ -542,6 +558,9 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
 
     lds_barrier(); // B0: routing of layers 0 and 1 is in LDS
     prefetch_a(std::integral_constant<int, 0>{}, 0);
+    // keep the two bursts in the order the loop issues them, so the load counter's state at
+    // the loop head is the same on both paths and phase A waits only for its own weights
+    asm volatile("" ::: "memory");
     prefetch_b(std::integral_constant<int, 0>{}, 0);
     if constexpr (LEAD == 2) {
         prefetch_a(std::integral_constant<int, LEAD - 1>{}, min(1, n - 1));
@@ -580,16 +599,16 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 float ss = 0.f;
 #pragma unroll
                 for (int i = 0; i < NSS; ++i) ss += ssq[i];
-                inv = 1.0f / sqrtf(ss * (1.0f / (float)H) + 1e-6f);
+                inv = __builtin_amdgcn_rsqf(ss * (1.0f / (float)H) + 1e-6f); // v_rsq_f32, 1 ulp
             }
             uint32_t *hb = hbuf(li);
 #pragma unroll
             for (int st = 0; st < STA; ++st) {
                 float g = (sub_scale(ah1[SL][st], ib1) * sx) * subblock_idot(aq1[SL][st], xh, xl);
                 float u = (sub_scale(ah3[SL][st], ib1) * sx) * subblock_idot(aq3[SL][st], xh, xl);
-                g = inv * lanes_total<LPR1>(g);
-                u = inv * lanes_total<LPR1>(u);
-                if (g1 == 0) tag_store_local(hb + rowA + st * RPS1 + rr1, silu(g) * u);
+                g = inv * row_total<LPR1>(g);
+                u = inv * row_total<LPR1>(u);
+                if (g1 == LPR1_LAST) tag_store_local(hb + rowA + st * RPS1 + rr1, silu_rcp(g) * u);
             }
             int sah_i = 0, sal_i = 0;
             dword_idot(saq[SL][0], sxh0[0], sxh1[0], sxl0[0], sxl1[0], sah_i, sal_i);
@@ -601,6 +620,9 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         }
         lds_barrier(); // B2: h_l in LDS; routing of layer li+2 in LDS
         prefetch_a(SLc, min(li + LEAD, n - 1));
+        // nothing of phase B above the burst: its first use of this layer's W2 registers
+        // then waits for those loads only, not for everything (stores included) in flight
+        __builtin_amdgcn_sched_barrier(0);
         // phase B: W2 rows against h, scaled by c * routing weight
         {
             float hv[32];
@@ -612,9 +634,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 hv[4 * i + 2] = q[2];
                 hv[4 * i + 3] = q[3];
             }
-            float hsum = 0.f;
-#pragma unroll
-            for (int i = 0; i < 32; ++i) hsum += hv[i];
+            const float hsum = hsm[g2];
             const float wk = a.c * rt_w[li % 3][0], wsh = a.c * rt_w[li % 3][1];
 #pragma unroll
             for (int st = 0; st < STB; ++st) {

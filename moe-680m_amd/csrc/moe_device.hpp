@@ -198,6 +198,16 @@ __device__ __forceinline__ float group_sum(float v) {
     }
 }
 
+// Whole-wave sum that is complete in lane 63 only (lanes of rows 0-2 hold partial sums):
+// row sums by DPP, then row_bcast:15 (rows 1, 3 += last lane of the row below) and
+// row_bcast:31 (rows 2, 3 += lane 31).  Six DPP adds, no readlane.
+__device__ __forceinline__ float wave_sum_last(float v) {
+    v = sum16(v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false));
+    return v;
+}
+
 // Total over each group of G lanes (G = 64: wave-uniform value through readlane).
 template <int G>
 __device__ __forceinline__ float lanes_total(float v) {
@@ -218,6 +228,8 @@ __device__ __forceinline__ void load32(const float *__restrict__ src, float (&v)
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+// The same with v_rcp_f32 (1 ulp) in place of the IEEE division sequence.
+__device__ __forceinline__ float silu_rcp(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
 // ---------------------------------------------------------------- router (one wave)
 __device__ __forceinline__ float router_key(float v) {
