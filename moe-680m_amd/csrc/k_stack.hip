@@ -13,9 +13,10 @@
 // latency and the synchronisation must come off the critical path:
 //   - the routing of every layer is computed before the launch (k_stack_prep: the logits
 //     are inputs); during layer l a router wave turns layer l+2's expert id into weight
-//     pointers, and every compute wave keeps one layer of its weights in flight in
-//     registers (layer l+1's phase-A weights are requested when phase A of l is done,
-//     phase-B weights when phase B is done);
+//     pointers, and every compute wave keeps its weights in flight in registers: layer
+//     l+1's phase-A weights are requested when phase A of l is done, layer l's phase-B
+//     weights when phase A of l starts (so no weight stream competes with the
+//     latency-bound cross-XCD exchange at the end of a layer);
 //   - activations move between workgroups through per-layer buffers cleared to zero
 //     before the launch; producers store each f32 with its mantissa LSB forced to 1
 //     (<= 1 ulp), consumers poll exactly the words they need until every word carries the
@@ -56,7 +57,6 @@ namespace moe {
 
 constexpr uint32_t STK_SPIN_MAX = 1u << 16;
 constexpr int STK_NX = 8;   // XCDs
-constexpr int STK_LEAD = 1; // layers of weights in flight ahead of the one being computed
 
 // Cross-XCD publish: an agent-scope store writes through this XCD's L2.
 __device__ __forceinline__ void tag_store(uint32_t *p, float v) {
@@ -163,7 +163,7 @@ __device__ __forceinline__ float adjacent_sum(float v) {
 // one word [xl_2w, xh_2w ^ 0x80, xl_2w+1, xh_2w+1 ^ 0x80]: xh is never -128, so byte 1 is
 // never zero and a published word is never zero -- the exchange tag is "word != 0"
 // (the zero-cleared buffer), which costs no bit of precision.
-__device__ __forceinline__ float quant_ratio(float am) { return am > 1e-30f ? 127.0f / am : 0.0f; }
+__device__ __forceinline__ float quant_ratio(float am) { return am > 1e-30f ? 127.0f * __builtin_amdgcn_rcpf(am) : 0.0f; }
 
 __device__ __forceinline__ uint32_t pack_pair(float xe, float xo, float r) {
     const float ue = xe * r, uo = xo * r;
@@ -362,7 +362,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 store_quad(xq, q,
                            u32x4{pack_pair(x0[0], x0[1], r), pack_pair(x0[2], x0[3], r),
                                  pack_pair(x1[0], x1[1], r), pack_pair(x1[2], x1[3], r)});
-                if ((q & 3) == 0) xsc[q >> 2] = am / 127.0f;
+                if ((q & 3) == 0) xsc[q >> 2] = am * (1.0f / 127.0f);
             }
             ss = wave_sum(ss);
             if (lane == 0) ssq[first ? 0 : 1] = ss;
@@ -446,12 +446,17 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                     am = fmaxf(am, dpp_mov<0x4E>(am));
                     am = fmaxf(am, dpp_mov<0x141>(am));
                     am = fmaxf(am, dpp_mov<0x140>(am));
-                    am = fmaxf(am, __shfl_xor(am, 16));
+                    {
+                        const auto sw = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, am),
+                                                                         __builtin_bit_cast(uint32_t, am), false, false);
+                        const uint32_t s0 = sw[0], s1 = sw[1]; // elements by value (whole-vector rule above)
+                        am = fmaxf(__builtin_bit_cast(float, s0), __builtin_bit_cast(float, s1));
+                    }
                     const float xo = dpp_mov<0xB1>(x1); // the odd partner of an even lane
                     const float ss = wave_sum(x1 * x1);
                     if ((lane & 1) == 0)
                         *(MOE_GLOBAL uint32_t *)(xb + (row >> 1)) = pack_pair(x1, xo, quant_ratio(am));
-                    if ((lane & 31) == 0) tag_store_local(xb + H / 2 + (row >> 5), am / 127.0f);
+                    if ((lane & 31) == 0) tag_store_local(xb + H / 2 + (row >> 5), am * (1.0f / 127.0f));
                     if (lane == 0) tag_store_local(xb + H / 2 + H / 32 + j, ss);
                 } else if (k == 0) {
                     *(MOE_GLOBAL float *)(a.y + row) = x1;
@@ -514,62 +519,51 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     const uint32_t qSB = 8 + 16 * (ccB & 7) + 4 * dB;
     const int hSB = padk(I + 32 * tB) + 4 * dB;
 
-    // Register slots of weights in flight: layer li's weights sit in slot li % LEAD; the
-    // slot is refilled with layer li+LEAD's as soon as the phase that reads it is done.
-    constexpr int LEAD = STK_LEAD;
-    u32x4 aq1[LEAD][STA], aq3[LEAD][STA], bq[LEAD][STB];
-    u32x2 ah1[LEAD][STA], ah3[LEAD][STA], bh[LEAD][STB], sah[LEAD], saq[LEAD], sbh[LEAD];
-    uint32_t sbq[LEAD];
+    // Weights in flight, one set per phase.
+    u32x4 aq1[STA], aq3[STA], bq[STB];
+    u32x2 ah1[STA], ah3[STA], bh[STB], sah, saq, sbh;
+    uint32_t sbq;
 
-    // Loads of local layer li's phase-A (W1, W3) and phase-B (W2) weights for this wave into
-    // register slot SL: phase-A weights of layer li+LEAD right after phase A of layer li
-    // (after B2, so that the routing computed during phase A is visible), phase-B weights
-    // after phase B.  The loads are issued unconditionally -- past the last layer they
-    // re-read layer n-1, which is still cached -- because a conditional burst would make the
-    // compiler's load counter path-dependent and turn the waits for older slots into waits
-    // for everything.
-    auto prefetch_a = [&](auto SLc, int li) __attribute__((always_inline)) {
-        constexpr int SL = decltype(SLc)::value;
+    // Loads of layer li's phase-A (W1, W3) weights for this wave, issued right after phase A
+    // of layer li-1 (after B2, so that the routing computed during phase A is visible), and
+    // of its phase-B (W2) weights, issued at B1 of layer li: they stream during phase A and
+    // the h exchange, which are compute- and L2-bound, and arrive before phase B.  The loads
+    // are issued unconditionally -- past the last layer they re-read layer n-1, which is
+    // still cached -- because a conditional burst would make the compiler's load counter
+    // path-dependent and turn the waits for the older burst into waits for everything.
+    auto prefetch_a = [&](int li) __attribute__((always_inline)) {
         const uint8_t *W1 = rt_p[li % 3][0][0];
         const uint8_t *W3 = rt_p[li % 3][0][1];
 #pragma unroll
         for (int st = 0; st < STA; ++st) {
-            ah1[SL][st] = ldg<u32x2>(W1 + offA[st]);
-            aq1[SL][st] = ldg<u32x4>(W1 + offA[st] + 8 + 16 * ib1);
-            ah3[SL][st] = ldg<u32x2>(W3 + offA[st]);
-            aq3[SL][st] = ldg<u32x4>(W3 + offA[st] + 8 + 16 * ib1);
+            ah1[st] = ldg<u32x2>(W1 + offA[st]);
+            aq1[st] = ldg<u32x4>(W1 + offA[st] + 8 + 16 * ib1);
+            ah3[st] = ldg<u32x2>(W3 + offA[st]);
+            aq3[st] = ldg<u32x4>(W3 + offA[st] + 8 + 16 * ib1);
         }
         const uint8_t *WS = rt_p[li % 3][1][mA];
-        sah[SL] = ldg<u32x2>(WS + offSA);
-        saq[SL] = ldg<u32x2>(WS + offSA + qSA);
+        sah = ldg<u32x2>(WS + offSA);
+        saq = ldg<u32x2>(WS + offSA + qSA);
     };
-    auto prefetch_b = [&](auto SLc, int li) __attribute__((always_inline)) {
-        constexpr int SL = decltype(SLc)::value;
+    auto prefetch_b = [&](int li) __attribute__((always_inline)) {
         const uint8_t *W2 = rt_p[li % 3][0][2];
 #pragma unroll
         for (int st = 0; st < STB; ++st) {
-            bh[SL][st] = ldg<u32x2>(W2 + offB[st]);
-            bq[SL][st] = ldg<u32x4>(W2 + offB[st] + 8 + 16 * ibB);
+            bh[st] = ldg<u32x2>(W2 + offB[st]);
+            bq[st] = ldg<u32x4>(W2 + offB[st] + 8 + 16 * ibB);
         }
         const uint8_t *WS = rt_p[li % 3][1][2];
-        sbh[SL] = ldg<u32x2>(WS + offSB);
-        sbq[SL] = ldg<uint32_t>(WS + offSB + qSB);
+        sbh = ldg<u32x2>(WS + offSB);
+        sbq = ldg<uint32_t>(WS + offSB + qSB);
     };
 
     lds_barrier(); // B0: routing of layers 0 and 1 is in LDS
-    prefetch_a(std::integral_constant<int, 0>{}, 0);
-    // keep the two bursts in the order the loop issues them, so the load counter's state at
-    // the loop head is the same on both paths and phase A waits only for its own weights
-    asm volatile("" ::: "memory");
-    prefetch_b(std::integral_constant<int, 0>{}, 0);
-    if constexpr (LEAD == 2) {
-        prefetch_a(std::integral_constant<int, LEAD - 1>{}, min(1, n - 1));
-        prefetch_b(std::integral_constant<int, LEAD - 1>{}, min(1, n - 1));
-    }
+    prefetch_a(0);
 
-    auto layer = [&](auto SLc, int li) __attribute__((always_inline)) {
-        constexpr int SL = decltype(SLc)::value;
+    for (int li = 0; li < n; ++li) {
         lds_barrier(); // B1: x_l in LDS
+        prefetch_b(li);
+        __builtin_amdgcn_sched_barrier(0);
         // phase A: h = silu(W1 xin) * (W3 xin) for this wave's slot-k row pairs, and this
         // wave's K share of the workgroup's shared rows (partial g, u: combined by the
         // pollers of every workgroup of the XCD)
@@ -604,22 +598,22 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             uint32_t *hb = hbuf(li);
 #pragma unroll
             for (int st = 0; st < STA; ++st) {
-                float g = (sub_scale(ah1[SL][st], ib1) * sx) * subblock_idot(aq1[SL][st], xh, xl);
-                float u = (sub_scale(ah3[SL][st], ib1) * sx) * subblock_idot(aq3[SL][st], xh, xl);
+                float g = (sub_scale(ah1[st], ib1) * sx) * subblock_idot(aq1[st], xh, xl);
+                float u = (sub_scale(ah3[st], ib1) * sx) * subblock_idot(aq3[st], xh, xl);
                 g = inv * row_total<LPR1>(g);
                 u = inv * row_total<LPR1>(u);
                 if (g1 == LPR1_LAST) tag_store_local(hb + rowA + st * RPS1 + rr1, silu_rcp(g) * u);
             }
             int sah_i = 0, sal_i = 0;
-            dword_idot(saq[SL][0], sxh0[0], sxh1[0], sxl0[0], sxl1[0], sah_i, sal_i);
-            dword_idot(saq[SL][1], sxh0[1], sxh1[1], sxl0[1], sxl1[1], sah_i, sal_i);
-            float sp = (sub_scale(sah[SL], sbg & 7) * ssx) * __builtin_fmaf((float)sal_i, 1.0f / 256.0f, (float)sah_i);
+            dword_idot(saq[0], sxh0[0], sxh1[0], sxl0[0], sxl1[0], sah_i, sal_i);
+            dword_idot(saq[1], sxh0[1], sxh1[1], sxl0[1], sxl1[1], sah_i, sal_i);
+            float sp = (sub_scale(sah, sbg & 7) * ssx) * __builtin_fmaf((float)sal_i, 1.0f / 256.0f, (float)sah_i);
             sp = inv * adjacent_sum<LPRS>(sp);
             if (lane % LPRS == 0 && lane < NSA)
                 tag_store_local(hb + I + ((j * SRP + pA) * NCW + w) * 2 + mA, sp);
         }
         lds_barrier(); // B2: h_l in LDS; routing of layer li+2 in LDS
-        prefetch_a(SLc, min(li + LEAD, n - 1));
+        prefetch_a(min(li + 1, n - 1));
         // nothing of phase B above the burst: its first use of this layer's W2 registers
         // then waits for those loads only, not for everything (stores included) in flight
         __builtin_amdgcn_sched_barrier(0);
@@ -638,7 +632,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             const float wk = a.c * rt_w[li % 3][0], wsh = a.c * rt_w[li % 3][1];
 #pragma unroll
             for (int st = 0; st < STB; ++st) {
-                float d = sub_scale(bh[SL][st], ibB) * subblock_dot(bq[SL][st], hv, hsum);
+                float d = sub_scale(bh[st], ibB) * subblock_dot(bq[st], hv, hsum);
                 d = group_sum<LPR2>(d);
                 if (g2 == 0) part[0][8 * w + st * RPS2 + rr2] = wk * d;
             }
@@ -652,19 +646,11 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                     hh4[e] = qh[e];
                 }
             }
-            float ds = sub_scale(sbh[SL], ccB & 7) * dword_dot(sbq[SL], hl, hh4);
+            float ds = sub_scale(sbh, ccB & 7) * dword_dot(sbq, hl, hh4);
             ds = adjacent_sum<LPRB>(ds);
             if (lane % LPRB == 0 && lane < NSB) part[1][8 * w + rB] = wsh * ds;
         }
-        // this slot's registers are free: bring in layer li+LEAD
-        prefetch_b(SLc, min(li + LEAD, n - 1));
         lds_barrier(); // B3: contributions in LDS
-    };
-
-    for (int li = 0; li < n; li += LEAD) {
-        layer(std::integral_constant<int, 0>{}, li);
-        if constexpr (LEAD == 2)
-            if (li + 1 < n) layer(std::integral_constant<int, LEAD - 1>{}, li + 1);
     }
 }
 
