@@ -161,8 +161,8 @@ enum {
     MOE_K_PREFILL_DOWN = 6,
     MOE_K_PREFILL_COMBINE = 7,
     MOE_K_DECODE_STACK = 8,
-    MOE_K_PREFILL_GATE_UP_SMALL = 9, /* small-tile variants, run on the context's second stream */
-    MOE_K_PREFILL_DOWN_SMALL = 10,
+    MOE_K_PREFILL_GATE_UP_SMALL = 9, /* no longer launched (small tiles run in the kernels above); */
+    MOE_K_PREFILL_DOWN_SMALL = 10,   /* ids kept so the numbering stays stable; they count 0 */
     MOE_K_COUNT = 11
 };
 moe_status moe_timing_enable(moe_ctx *ctx, int capacity);

@@ -39,7 +39,6 @@
 namespace moe {
 
 constexpr int PF_KC = 128;             // K per LDS stage
-constexpr int PF_LDSK = PF_KC + 8;     // +16 B per row: 16 rows at one column hit 16 bank groups
 constexpr int PF_WAVES = 8;
 constexpr int PF_NGU = 16 * PF_WAVES;  // gate/up columns per workgroup
 constexpr int PF_ND = 32 * PF_WAVES;   // down output rows per workgroup (2 N-tiles per wave)
@@ -214,91 +213,128 @@ __device__ __forceinline__ void wstage_dl(const WStage<NR> &s, int ch, int g, in
 }
 
 // One stage of MFMAs: NR B fragments (dequantized here) against the MT M-tiles of the LDS
-// A stage.  Each K-step first issues the A fragment reads, then the decode VALU work (which
-// covers the LDS latency), then the MFMAs.
+// A chunk.  Each K-step first issues the reads of two A fragments, then the decode VALU work
+// (which covers their LDS latency), then the MFMAs, reading the next A fragment two M-tiles
+// ahead (A fragments are held two at a time, not MT at a time: fewer live registers).
 template <int NR, int MT, int LK>
 __device__ __forceinline__ void stage_mfma(const WStage<NR> &s0, const uint32_t (&dl)[NR][4], const _Float16 *As,
                                            int n, int g, f32x4 (&acc)[MT][NR]) {
-    uint32_t qv[NR][4];
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-        qv[r][0] = s0.q[r][0];
-        qv[r][1] = s0.q[r][1];
-        qv[r][2] = s0.q[r][2];
-        qv[r][3] = s0.q[r][3];
-    }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
         const _Float16 *ap = As + n * LK + 32 * ks + 8 * g;
-        u32x4 av[MT];
+        u32x4 av[2];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) av[mt] = *reinterpret_cast<const u32x4 *>(ap + 16 * mt * LK);
+        for (int mt = 0; mt < (MT < 2 ? MT : 2); ++mt) av[mt] = *reinterpret_cast<const u32x4 *>(ap + 16 * mt * LK);
         u32x4 b[NR];
 #pragma unroll
-        for (int r = 0; r < NR; ++r) b[r] = dq8_f16(qv[r][ks], dl[r][ks]);
+        for (int r = 0; r < NR; ++r) b[r] = dq8_f16(s0.q[r][ks], dl[r][ks]);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt) {
+            const u32x4 cur = av[mt & 1];
+            if (mt + 2 < MT) av[mt & 1] = *reinterpret_cast<const u32x4 *>(ap + 16 * (mt + 2) * LK);
 #pragma unroll
-            for (int r = 0; r < NR; ++r) acc[mt][r] = mfma16(av[mt], b[r], acc[mt][r]);
+            for (int r = 0; r < NR; ++r) acc[mt][r] = mfma16(cur, b[r], acc[mt][r]);
+        }
     }
 }
 
-// The K loop shared by both GEMMs, fully unrolled: with a rolled loop the compiler's vmcnt
-// bookkeeping merges at the loop head and waits for every prefetch in flight.  Per stage ch: request the A rows of stage ch+2 (into
-// register set ch&1) and the weights of stage ch+3 (ring slot (ch+3)&3), run the MFMAs of
-// stage ch from LDS buffer ch&1, then move A of stage ch+1 into the other LDS buffer.  Loads
-// are issued in the order they are needed, so a wave's in-order vmcnt waits never hold a
-// use behind a later prefetch.  Only LDS traffic crosses the barriers.
-template <int NCH, int NR, int MT, int LK, typename ALoad, typename AStore>
-__device__ __forceinline__ void gemm_k_loop(const uint8_t *const (&rows)[NR], _Float16 (*As)[PF_BM * PF_LDSK], int n,
-                                            int g, f32x4 (&acc)[MT][NR], ALoad aload, AStore astore) {
-    WStage<NR> ws[4];
+// ---------------------------------------------------------------- K loop
+// A (the tile's token rows, f16) is resident in LDS one chunk of up to PF_KCH stages (512 K)
+// at a time: every thread helps stage a chunk, one barrier, then the 8 waves run the chunk's
+// stages with no barrier inside -- each wave waits only for its own weight loads, and the
+// other workgroup on the CU hides the chunk boundaries.  Weights come through a per-wave ring
+// of 4 register stages, each requested three stages ahead in the order they are consumed (a
+// wave's in-order vmcnt waits then never hold a use behind a later prefetch); the ring runs
+// on across chunks.  Fully unrolled: with a rolled loop the compiler's vmcnt bookkeeping
+// merges at the loop head and waits for every prefetch in flight.
+constexpr int PF_KCH = 4; // stages per resident chunk
+
+// LDS row stride (halves) of a resident chunk for a K loop of NCH stages: +16 B per row, so
+// the 16 rows of an A fragment read hit 16 different bank groups.
+template <int NCH>
+constexpr int pf_ldsr() { return (NCH < PF_KCH ? NCH : PF_KCH) * PF_KC + 8; }
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>), in order.
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// A wave-uniform pointer moved to SGPRs (loads then take a scalar base and a lane offset).
+template <typename T>
+__device__ __forceinline__ const T *uniform_ptr(const T *p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const T *)(((uint64_t)hi << 32) | lo);
+}
+
+// Weight ring of RD register stages: the prologue requests stages 0..RD-2.
+template <int NCH, int RD, int NR>
+__device__ __forceinline__ void wring_prologue(WStage<NR> (&ws)[RD], const uint8_t *const (&rows)[NR], int lane) {
 #pragma unroll
-    for (int c = 0; c < 3; ++c)
-        if (c < NCH) wstage_load(ws[c], rows, c, n + 16 * g);
-    aload(std::integral_constant<int, 0>{}, 0);
-    if (NCH > 1) aload(std::integral_constant<int, 1>{}, 1);
-    astore(std::integral_constant<int, 0>{}, 0);
-    lds_barrier();
-    auto stage = [&](auto Sc, int ch) __attribute__((always_inline)) {
-        constexpr int S = decltype(Sc)::value; // ch & 3
-        if (ch + 2 < NCH) aload(std::integral_constant<int, S & 1>{}, ch + 2);
+    for (int c = 0; c < RD - 1; ++c) {
+        if (c < NCH) wstage_load(ws[c], rows, c, lane);
         __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// stage_a(c) moves chunk c of A into LDS; chunk 0 is expected in LDS on entry (its loads were
+// issued before the weight ring's, so waiting for them did not wait for the weights).
+template <int NCH, int RD, int NR, int MT, typename StageA>
+__device__ __forceinline__ void gemm_resident(WStage<NR> (&ws)[RD], const uint8_t *const (&rows)[NR],
+                                              const _Float16 *As, int n, int g, f32x4 (&acc)[MT][NR],
+                                              StageA stage_a) {
+    constexpr int KCH = NCH < PF_KCH ? NCH : PF_KCH;
+    constexpr int LK = pf_ldsr<NCH>();
+    static_assert(NCH % KCH == 0, "whole chunks");
+    static_for<NCH>([&](auto CHc) __attribute__((always_inline)) {
+        constexpr int ch = decltype(CHc)::value, S = ch % RD;
+        if constexpr (ch > 0 && ch % KCH == 0) {
+            lds_barrier(); // every wave is done with the previous chunk
+            stage_a(ch / KCH);
+            lds_barrier();
+        }
         uint32_t dl[NR][4];
         wstage_dl(ws[S], ch, g, n, dl);
-        stage_mfma<NR, MT, LK>(ws[S], dl, As[S & 1], n, g, acc);
+        stage_mfma<NR, MT, LK>(ws[S], dl, As + (ch % KCH) * PF_KC, n, g, acc);
+        // keep the scheduler from moving loads across stages: each stage's weights are
+        // requested RD-1 stages ahead, in the order they are consumed
         __builtin_amdgcn_sched_barrier(0);
-        if (ch + 3 < NCH) wstage_load(ws[(S + 3) & 3], rows, ch + 3, n + 16 * g);
+        if constexpr (ch + RD - 1 < NCH) wstage_load(ws[(ch + RD - 1) % RD], rows, ch + RD - 1, n + 16 * g);
         __builtin_amdgcn_sched_barrier(0);
-        if (ch + 1 < NCH) astore(std::integral_constant<int, (S + 1) & 1>{}, (S + 1) & 1);
-        lds_barrier();
-    };
-#pragma unroll
-    for (int c0 = 0; c0 < NCH; c0 += 4) {
-        stage(std::integral_constant<int, 0>{}, c0);
-        if (c0 + 1 < NCH) stage(std::integral_constant<int, 1>{}, c0 + 1);
-        if (c0 + 2 < NCH) stage(std::integral_constant<int, 2>{}, c0 + 2);
-        if (c0 + 3 < NCH) stage(std::integral_constant<int, 3>{}, c0 + 3);
-    }
+    });
 }
 
-// Big tiles hold PF_SMALL_MAX+1 .. PF_BM slots; the GEMM bodies are instantiated for 4 and 8
-// M-tiles of 16 rows so that each inner loop is straight-line code (no per-M-tile branches).
+// A tile holds up to PF_BM slots of one expert and runs as 1, 2 or 4 M-tiles of 16 rows (one
+// instantiation each, picked per workgroup, so every inner loop is straight-line code).  Full
+// PF_BM tiles come first in the list, remainders after: the long work items start first and
+// the short ones fill in.  64-row tiles, not 128: every wave reads each A fragment from LDS
+// once per pair of B fragments, so LDS traffic per K step grows with the tile height;
+// measured, a 128-row tile took 2.5x the time of a 64-row one, more than the second decode of
+// the weights that two 64-row tiles cost.
 template <typename F>
 __device__ __forceinline__ void by_mtiles(int nrows, F f) {
-    if (nrows <= 64) f(std::integral_constant<int, 4>{});
-    else f(std::integral_constant<int, 8>{});
+    static_assert(PF_BM == 64 && PF_SMALL_MAX == 32, "tile classes");
+    if (nrows > PF_SMALL_MAX) f(std::integral_constant<int, 4>{});
+    else if (nrows > 16) f(std::integral_constant<int, 2>{});
+    else f(std::integral_constant<int, 1>{});
 }
 
 // ---------------------------------------------------------------- gate/up
 template <int H, int I>
-__global__ __launch_bounds__(64 * PF_WAVES, 1) void k_pf_gate_up(PrefillArgs a) {
-    constexpr int MG = PF_BM;
-    constexpr int KC = PF_KC, LK = PF_LDSK, NCH = H / KC;
+__global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) {
+    constexpr int NCH = H / PF_KC, KCH = NCH < PF_KCH ? NCH : PF_KCH, KC = KCH * PF_KC;
+    constexpr int LK = pf_ldsr<NCH>();
     constexpr int ROWB = (H / QK) * SB_BYTES;
-    static_assert(H % QK == 0 && I % PF_NGU == 0 && KC * 2 == QK, "gate/up shape");
-    __shared__ __attribute__((aligned(16))) _Float16 As[2][MG * LK];
-    __shared__ uint32_t rowmax[MG];
+    static_assert(H % QK == 0 && I % PF_NGU == 0 && PF_KC * 2 == QK, "gate/up shape");
+    __shared__ __attribute__((aligned(16))) _Float16 As[PF_BM * LK];
+    __shared__ uint32_t rowmax[PF_BM];
+    __shared__ float s_inv[PF_BM];
+    __shared__ int s_tok[PF_BM];
 
     const Tile tl = a.tiles[blockIdx.y];
     if (tl.expert < 0) return;
@@ -306,40 +342,61 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void k_pf_gate_up(PrefillArgs a) 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int c0 = blockIdx.x * PF_NGU + wv * 16; // this wave's h columns
-    if (tid < MG) rowmax[tid] = 0u;
-
-    // A staging: thread -> (row ar, 32 K at column 32*ap of the stage)
-    const int ar = tid >> 2, ap = tid & 3;
-    const int aslot = row0 + (ar < nrows ? ar : nrows - 1);
-    const _Float16 *asrc = a.xh + (size_t)a.sorted_tok[aslot] * H + 32 * ap;
+    // the tile's tokens and their 1/scale (rows past nrows repeat the last token)
+    if (tid < PF_BM) {
+        const int t = a.sorted_tok[row0 + (tid < nrows ? tid : nrows - 1)];
+        s_tok[tid] = t;
+        s_inv[tid] = a.xinv[t];
+        rowmax[tid] = 0u;
+    }
+    lds_barrier();
     // Weights: rows c0 + n of W1 (gate) and W3 (up).
-    const uint8_t *rows[2] = {expert_w(a.L.w1, a.L.s1, a.L.sw1, e, a.E) + (size_t)c0 * ROWB,
-                              expert_w(a.L.w3, a.L.s3, a.L.sw3, e, a.E) + (size_t)c0 * ROWB};
+    const uint8_t *rows[2] = {uniform_ptr(expert_w(a.L.w1, a.L.s1, a.L.sw1, e, a.E) + (size_t)c0 * ROWB),
+                              uniform_ptr(expert_w(a.L.w3, a.L.s3, a.L.sw3, e, a.E) + (size_t)c0 * ROWB)};
 
     by_mtiles(nrows, [&](auto MTc) __attribute__((always_inline)) {
         constexpr int MT = decltype(MTc)::value;
-        const bool arow = ar < 16 * MT; // only the rows of the M-tiles in use are moved
-        u32x4 ra[2][4];
-        auto aload = [&](auto Rc, int ch) __attribute__((always_inline)) {
-            constexpr int R = decltype(Rc)::value;
-            if (arow) {
-                const u32x4 *p = reinterpret_cast<const u32x4 *>(asrc + ch * KC);
+        // chunk c of A: 16*MT rows x KC halves, one wave per row and pass (KC/8 lanes x 16 B)
+        constexpr int QPR = KC / 8, PER = 16 * MT * QPR / (64 * PF_WAVES);
+        static_assert(PER >= 1 && 16 * MT * QPR % (64 * PF_WAVES) == 0 && QPR == 64, "A staging split");
+        u32x4 va[PER];
+        // quads [i0, i1) of chunk c: global -> registers, registers -> LDS
+        auto load_a = [&](int c, int i0, int i1) __attribute__((always_inline)) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) ra[R][i] = ldg<u32x4>(p + i);
-            }
+            for (int i = 0; i < PER; ++i)
+                if (i >= i0 && i < i1) {
+                    const int idx = i * 64 * PF_WAVES + tid, r = idx / QPR, q = idx % QPR;
+                    // r is the same for the whole wave (QPR = 64): the token index in an SGPR
+                    const int tok = __builtin_amdgcn_readfirstlane(s_tok[r]);
+                    va[i] = ldg<u32x4>(a.xh + (size_t)tok * H + c * KC + 8 * q);
+                }
         };
-        auto astore = [&](auto Rc, int buf) __attribute__((always_inline)) {
-            constexpr int R = decltype(Rc)::value;
-            if (arow) {
-                u32x4 *d = reinterpret_cast<u32x4 *>(&As[buf][ar * LK + 32 * ap]);
+        auto store_a = [&](int i0, int i1) __attribute__((always_inline)) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) d[i] = ra[R][i];
-            }
+            for (int i = 0; i < PER; ++i)
+                if (i >= i0 && i < i1) {
+                    const int idx = i * 64 * PF_WAVES + tid, r = idx / QPR, q = idx % QPR;
+                    *reinterpret_cast<u32x4 *>(As + r * LK + 8 * q) = va[i];
+                }
         };
+        constexpr int RD = 3; // weight ring depth: two stages ahead (register budget)
+        WStage<2> ws[RD];
+        load_a(0, 0, PER);
+        wring_prologue<NCH, RD>(ws, rows, lane);
+        store_a(0, PER);
+        lds_barrier();
         f32x4 acc[MT][2];
 #pragma unroll
         for (int i = 0; i < MT; ++i) acc[i][0] = acc[i][1] = f32x4{0, 0, 0, 0};
-        gemm_k_loop<NCH, 2, MT, LK>(rows, As, n, g, acc, aload, astore);
+        // later chunks are moved in two halves while the weight ring and the accumulators
+        // are live (fewer registers held at once)
+        constexpr int HALF = (PER + 1) / 2;
+        gemm_resident<NCH, RD, 2, MT>(ws, rows, As, n, g, acc, [&](int c) __attribute__((always_inline)) {
+            load_a(c, 0, HALF);
+            store_a(0, HALF);
+            load_a(c, HALF, PER);
+            store_a(HALF, PER);
+        });
 
         // epilogue: h = silu(g) * u with the token scale undone; per-row max|h| of the block
 #pragma unroll
@@ -349,10 +406,9 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void k_pf_gate_up(PrefillArgs a) 
                 const int m = 16 * mt + 4 * g + i;
                 float hv = 0.0f;
                 if (m < nrows) {
-                    const int slot = row0 + m;
-                    const float inv = a.xinv[a.sorted_tok[slot]];
+                    const float inv = s_inv[m];
                     hv = silu(acc[mt][0][i] * inv) * (acc[mt][1][i] * inv);
-                    a.hf[(size_t)slot * I + c0 + n] = hv;
+                    a.hf[(size_t)(row0 + m) * I + c0 + n] = hv;
                 }
                 const float rm = max16(fabsf(hv));
                 if (n == 0) atomicMax(&rowmax[m], __builtin_bit_cast(uint32_t, rm));
@@ -364,14 +420,15 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void k_pf_gate_up(PrefillArgs a) 
 
 // ---------------------------------------------------------------- down
 template <int H, int I>
-__global__ __launch_bounds__(64 * PF_WAVES, 1) void k_pf_down(PrefillArgs a) {
-    constexpr int MG = PF_BM, NTW = 2;
-    constexpr int KC = PF_KC, LK = PF_LDSK, NCH = I / KC;
+__global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
+    constexpr int NTW = 2, NCH = I / PF_KC, KCH = NCH < PF_KCH ? NCH : PF_KCH, KC = KCH * PF_KC;
+    constexpr int LK = pf_ldsr<NCH>();
     constexpr int ROWB = (I / QK) * SB_BYTES;
     constexpr int NHB = I / PF_NGU; // h max blocks per row
-    static_assert(I % QK == 0 && H % PF_ND == 0 && KC * 2 == QK, "down shape");
-    __shared__ __attribute__((aligned(16))) _Float16 As[2][MG * LK];
-    __shared__ float s_scale[MG], s_inv[MG];
+    constexpr int BPR = KC / 32;     // 32-blocks per row in a chunk
+    static_assert(I % QK == 0 && H % PF_ND == 0 && PF_KC * 2 == QK, "down shape");
+    __shared__ __attribute__((aligned(16))) _Float16 As[PF_BM * LK];
+    __shared__ float s_scale[PF_BM], s_inv[PF_BM];
 
     const Tile tl = a.tiles[blockIdx.y];
     if (tl.expert < 0) return;
@@ -380,7 +437,8 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void k_pf_down(PrefillArgs a) {
     const int n = lane & 15, g = lane >> 4;
     const int r0 = blockIdx.x * PF_ND + wv * 32; // this wave's output rows r0 .. r0+31
 
-    if (tid < MG) {
+    // h rows are scaled by a power of two from their max into f16 as they are staged
+    if (tid < PF_BM) {
         float mx = 0.f;
         if (tid < nrows)
 #pragma unroll
@@ -389,56 +447,48 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void k_pf_down(PrefillArgs a) {
         s_scale[tid] = pow2_scale(mx, &inv);
         s_inv[tid] = inv;
     }
-    __syncthreads();
-
-    const int ar = tid >> 2, ap = tid & 3;
-    const int aslot = row0 + (ar < nrows ? ar : nrows - 1);
-    const float *asrc = a.hf + (size_t)aslot * I + 32 * ap;
-    const float asc = s_scale[ar];
+    lds_barrier();
     const uint8_t *w2 = expert_w(a.L.w2, a.L.s2, a.L.sw2, e, a.E);
-    const uint8_t *rows[NTW] = {w2 + (size_t)r0 * ROWB, w2 + (size_t)(r0 + 16) * ROWB};
+    const uint8_t *rows[NTW] = {uniform_ptr(w2 + (size_t)r0 * ROWB), uniform_ptr(w2 + (size_t)(r0 + 16) * ROWB)};
 
     by_mtiles(nrows, [&](auto MTc) __attribute__((always_inline)) {
         constexpr int MT = decltype(MTc)::value;
-        const bool arow = ar < 16 * MT;
-        f32x4 ra[2][8];
-        auto aload = [&](auto Rc, int ch) __attribute__((always_inline)) {
-            constexpr int R = decltype(Rc)::value;
-            if (arow) {
-                const f32x4 *p = reinterpret_cast<const f32x4 *>(asrc + ch * KC);
+        // chunk c of A: 16*MT rows x BPR 32-blocks, one block (32 f32 -> 32 f16 in the
+        // weights' K order) per thread and pass
+        auto stage_a = [&](int c) __attribute__((always_inline)) {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) ra[R][i] = ldg<f32x4>(p + i);
+            for (int it0 = 0; it0 < 16 * MT * BPR; it0 += 64 * PF_WAVES) {
+                const int it = it0 + tid;
+                if (it0 + 64 * PF_WAVES <= 16 * MT * BPR || it < 16 * MT * BPR) {
+                    const int ar = it / BPR, ab = it % BPR;
+                    const int slot = row0 + (ar < nrows ? ar : nrows - 1);
+                    const float sc = s_scale[ar];
+                    float v[32];
+                    load32(a.hf + (size_t)slot * I + c * KC + 32 * ab, v);
+                    u32x4 o[4];
+#pragma unroll
+                    for (int p = 0; p < 16; ++p) {
+                        const int gg = (2 * p) >> 3, j = (2 * p) & 7;
+                        const int k0 = j < 4 ? 4 * gg + j : 16 + 4 * gg + (j - 4);
+                        o[p >> 2][p & 3] = pack_f16x2(v[k0] * sc, v[k0 + 1] * sc);
+                    }
+                    u32x4 *d = reinterpret_cast<u32x4 *>(As + ar * LK + 32 * ab);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) d[i] = o[i];
+                }
             }
         };
-        auto astore = [&](auto Rc, int buf) __attribute__((always_inline)) {
-            constexpr int R = decltype(Rc)::value;
-            if (arow) {
-                float v[32];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    v[4 * i + 0] = ra[R][i][0] * asc;
-                    v[4 * i + 1] = ra[R][i][1] * asc;
-                    v[4 * i + 2] = ra[R][i][2] * asc;
-                    v[4 * i + 3] = ra[R][i][3] * asc;
-                }
-                u32x4 o[4];
-#pragma unroll
-                for (int p = 0; p < 16; ++p) {
-                    const int gg = (2 * p) >> 3, j = (2 * p) & 7;
-                    const int k0 = j < 4 ? 4 * gg + j : 16 + 4 * gg + (j - 4);
-                    o[p >> 2][p & 3] = pack_f16x2(v[k0], v[k0 + 1]);
-                }
-                u32x4 *d = reinterpret_cast<u32x4 *>(&As[buf][ar * LK + 32 * ap]);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) d[i] = o[i];
-            }
-        };
+        constexpr int RD = 4; // weight ring depth: three stages ahead
+        WStage<NTW> ws[RD];
+        wring_prologue<NCH, RD>(ws, rows, lane);
+        stage_a(0);
+        lds_barrier();
         f32x4 acc[MT][NTW];
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
             for (int t = 0; t < NTW; ++t) acc[i][t] = f32x4{0, 0, 0, 0};
-        gemm_k_loop<NCH, NTW, MT, LK>(rows, As, n, g, acc, aload, astore);
+        gemm_resident<NCH, RD, NTW, MT>(ws, rows, As, n, g, acc, stage_a);
 
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
@@ -454,155 +504,6 @@ __global__ __launch_bounds__(64 * PF_WAVES, 1) void k_pf_down(PrefillArgs a) {
                 }
             }
     });
-}
-
-// ---------------------------------------------------------------- small tiles
-// Tiles of at most PF_SM (16) slots: the tile's whole A operand (16 rows x K, f16) is staged in
-// LDS once, after which the 8 waves run their K loops independently -- no barrier inside the
-// loop, each wave only waits for its own weight loads, and two workgroups share a CU so one
-// hides the other's load latency.
-template <int NCH, int NR>
-__device__ __forceinline__ void wring_prologue(WStage<NR> (&ws)[4], const uint8_t *const (&rows)[NR], int lane) {
-#pragma unroll
-    for (int c = 0; c < 3; ++c) {
-        if (c < NCH) wstage_load(ws[c], rows, c, lane);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-}
-
-// K loop over an LDS-resident A; the ring's first three stages were requested by
-// wring_prologue (before the A staging, so both latencies overlap).
-template <int NCH, int NR, int LK>
-__device__ __forceinline__ void gemm_k_loop_resident(WStage<NR> (&ws)[4], const uint8_t *const (&rows)[NR],
-                                                     const _Float16 *As, int n, int g, f32x4 (&acc)[1][NR]) {
-    auto stage = [&](auto Sc, int ch) __attribute__((always_inline)) {
-        constexpr int S = decltype(Sc)::value;
-        uint32_t dl[NR][4];
-        wstage_dl(ws[S], ch, g, n, dl);
-        stage_mfma<NR, 1, LK>(ws[S], dl, As + ch * PF_KC, n, g, acc);
-        // keep the scheduler from moving loads across stages: each stage's weights are
-        // requested exactly three stages ahead, in the order they are consumed
-        __builtin_amdgcn_sched_barrier(0);
-        if (ch + 3 < NCH) wstage_load(ws[(S + 3) & 3], rows, ch + 3, n + 16 * g);
-        __builtin_amdgcn_sched_barrier(0);
-    };
-#pragma unroll
-    for (int c0 = 0; c0 < NCH; c0 += 4) {
-        stage(std::integral_constant<int, 0>{}, c0);
-        if (c0 + 1 < NCH) stage(std::integral_constant<int, 1>{}, c0 + 1);
-        if (c0 + 2 < NCH) stage(std::integral_constant<int, 2>{}, c0 + 2);
-        if (c0 + 3 < NCH) stage(std::integral_constant<int, 3>{}, c0 + 3);
-    }
-}
-
-template <int H, int I>
-__global__ __launch_bounds__(64 * PF_WAVES, 2) void k_pf_gate_up_s(PrefillArgs a) {
-    constexpr int LKS = H + 8, NCH = H / PF_KC;
-    constexpr int ROWB = (H / QK) * SB_BYTES;
-    constexpr int CH = H / 32; // halves per staging thread (32 threads per row)
-    static_assert(CH % 8 == 0, "small gate/up staging");
-    __shared__ __attribute__((aligned(16))) _Float16 As[PF_SM * LKS];
-    __shared__ uint32_t rowmax[PF_SM];
-
-    const Tile tl = a.tiles[a.tile_max + blockIdx.y];
-    if (tl.expert < 0) return;
-    const int e = tl.expert, row0 = tl.row0, nrows = tl.nrows;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int n = lane & 15, g = lane >> 4;
-    const int c0 = blockIdx.x * PF_NGU + wv * 16;
-    if (tid < PF_SM) rowmax[tid] = 0u;
-    const uint8_t *rows[2] = {expert_w(a.L.w1, a.L.s1, a.L.sw1, e, a.E) + (size_t)c0 * ROWB,
-                              expert_w(a.L.w3, a.L.s3, a.L.sw3, e, a.E) + (size_t)c0 * ROWB};
-    WStage<2> ws[4];
-    wring_prologue<NCH>(ws, rows, lane);
-    {
-        const int ar = tid >> 5, ac = (tid & 31) * CH;
-        const int slot = row0 + (ar < nrows ? ar : nrows - 1);
-        const u32x4 *src = reinterpret_cast<const u32x4 *>(a.xh + (size_t)a.sorted_tok[slot] * H + ac);
-        u32x4 *dst = reinterpret_cast<u32x4 *>(As + ar * LKS + ac);
-#pragma unroll
-        for (int i = 0; i < CH / 8; ++i) dst[i] = ldg<u32x4>(src + i);
-    }
-    lds_barrier();
-    f32x4 acc[1][2];
-    acc[0][0] = acc[0][1] = f32x4{0, 0, 0, 0};
-    gemm_k_loop_resident<NCH, 2, LKS>(ws, rows, As, n, g, acc);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = 4 * g + i;
-        float hv = 0.0f;
-        if (m < nrows) {
-            const int slot = row0 + m;
-            const float inv = a.xinv[a.sorted_tok[slot]];
-            hv = silu(acc[0][0][i] * inv) * (acc[0][1][i] * inv);
-            a.hf[(size_t)slot * I + c0 + n] = hv;
-        }
-        const float rm = max16(fabsf(hv));
-        if (n == 0) atomicMax(&rowmax[m], __builtin_bit_cast(uint32_t, rm));
-    }
-    __syncthreads();
-    if (tid < nrows) a.hmax[(size_t)(row0 + tid) * (I / PF_NGU) + blockIdx.x] = __builtin_bit_cast(float, rowmax[tid]);
-}
-
-template <int H, int I>
-__global__ __launch_bounds__(64 * PF_WAVES, 2) void k_pf_down_s(PrefillArgs a) {
-    constexpr int LKS = I + 8, NCH = I / PF_KC, NTW = 2;
-    constexpr int ROWB = (I / QK) * SB_BYTES;
-    constexpr int NHB = I / PF_NGU;
-    constexpr int TPR = I / 32; // staging threads per row, one 32-block each
-    __shared__ __attribute__((aligned(16))) _Float16 As[PF_SM * LKS];
-
-    const Tile tl = a.tiles[a.tile_max + blockIdx.y];
-    if (tl.expert < 0) return;
-    const int e = tl.expert, row0 = tl.row0, nrows = tl.nrows;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int n = lane & 15, g = lane >> 4;
-    const int r0 = blockIdx.x * PF_ND + wv * 32;
-    const uint8_t *w2 = expert_w(a.L.w2, a.L.s2, a.L.sw2, e, a.E);
-    const uint8_t *rows[NTW] = {w2 + (size_t)r0 * ROWB, w2 + (size_t)(r0 + 16) * ROWB};
-    WStage<NTW> ws[4];
-    wring_prologue<NCH>(ws, rows, lane);
-    if (tid < PF_SM * TPR) {
-        const int ar = tid / TPR, ab = tid % TPR;
-        const int slot = row0 + (ar < nrows ? ar : nrows - 1);
-        float mx = 0.f;
-#pragma unroll
-        for (int b = 0; b < NHB; ++b) mx = fmaxf(mx, a.hmax[(size_t)slot * NHB + b]);
-        float inv;
-        const float sc = pow2_scale(mx, &inv);
-        float v[32];
-        load32(a.hf + (size_t)slot * I + 32 * ab, v);
-        u32x4 o[4];
-#pragma unroll
-        for (int p = 0; p < 16; ++p) {
-            const int gg = (2 * p) >> 3, j = (2 * p) & 7;
-            const int k0 = j < 4 ? 4 * gg + j : 16 + 4 * gg + (j - 4);
-            o[p >> 2][p & 3] = pack_f16x2(v[k0] * sc, v[k0 + 1] * sc);
-        }
-        u32x4 *d = reinterpret_cast<u32x4 *>(As + ar * LKS + 32 * ab);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) d[i] = o[i];
-    }
-    lds_barrier();
-    f32x4 acc[1][NTW];
-    acc[0][0] = acc[0][1] = f32x4{0, 0, 0, 0};
-    gemm_k_loop_resident<NCH, NTW, LKS>(ws, rows, As, n, g, acc);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = 4 * g + i;
-        if (m < nrows) {
-            const int slot = row0 + m;
-            float mx = 0.f;
-#pragma unroll
-            for (int b = 0; b < NHB; ++b) mx = fmaxf(mx, a.hmax[(size_t)slot * NHB + b]);
-            float inv;
-            (void)pow2_scale(mx, &inv);
-            const float sc = a.c * a.sorted_w[slot] * inv;
-            float *prow = a.part + (size_t)slot * H + r0 + n;
-#pragma unroll
-            for (int t = 0; t < NTW; ++t) prow[16 * t] = sc * acc[0][t][i];
-        }
-    }
 }
 
 // ---------------------------------------------------------------- combine
@@ -627,35 +528,21 @@ __global__ __launch_bounds__(256) void k_pf_combine(PrefillArgs a) {
 }
 
 template <int H, int I>
-static hipError_t launch_prefill_t(const PrefillArgs &a, hipStream_t st, hipStream_t aux, hipEvent_t ev_fork,
-                                   hipEvent_t ev_join, KernelTimer *T) {
+static hipError_t launch_prefill_t(const PrefillArgs &a, hipStream_t st, KernelTimer *T) {
     {
         TimedLaunch tl(T, MOE_K_PREFILL_PREP, st);
         hipLaunchKernelGGL((k_pf_prep<H>), dim3((a.M + 3) / 4), dim3(256), 0, st, a);
     }
-    // small tiles on the second stream, concurrently with the big tiles
-    hipError_t he = hipEventRecord(ev_fork, st);
-    if (he == hipSuccess) he = hipStreamWaitEvent(aux, ev_fork, 0);
-    if (he != hipSuccess) return he;
-    {
-        TimedLaunch tl(T, MOE_K_PREFILL_GATE_UP_SMALL, aux);
-        hipLaunchKernelGGL((k_pf_gate_up_s<H, I>), dim3(I / PF_NGU, a.stile_max), dim3(64 * PF_WAVES), 0, aux, a);
-    }
-    {
-        TimedLaunch tl(T, MOE_K_PREFILL_DOWN_SMALL, aux);
-        hipLaunchKernelGGL((k_pf_down_s<H, I>), dim3(H / PF_ND, a.stile_max), dim3(64 * PF_WAVES), 0, aux, a);
-    }
+    // one launch over both tile lists (full and big remainder tiles, then small remainders)
+    const int ntiles = a.tile_max + a.stile_max;
     {
         TimedLaunch tl(T, MOE_K_PREFILL_GATE_UP, st);
-        hipLaunchKernelGGL((k_pf_gate_up<H, I>), dim3(I / PF_NGU, a.tile_max), dim3(64 * PF_WAVES), 0, st, a);
+        hipLaunchKernelGGL((k_pf_gate_up<H, I>), dim3(I / PF_NGU, ntiles), dim3(64 * PF_WAVES), 0, st, a);
     }
     {
         TimedLaunch tl(T, MOE_K_PREFILL_DOWN, st);
-        hipLaunchKernelGGL((k_pf_down<H, I>), dim3(H / PF_ND, a.tile_max), dim3(64 * PF_WAVES), 0, st, a);
+        hipLaunchKernelGGL((k_pf_down<H, I>), dim3(H / PF_ND, ntiles), dim3(64 * PF_WAVES), 0, st, a);
     }
-    he = hipEventRecord(ev_join, aux);
-    if (he == hipSuccess) he = hipStreamWaitEvent(st, ev_join, 0);
-    if (he != hipSuccess) return he;
     {
         TimedLaunch tl(T, MOE_K_PREFILL_COMBINE, st);
         hipLaunchKernelGGL((k_pf_combine<H>), dim3(a.M), dim3(256), 0, st, a);
@@ -663,10 +550,9 @@ static hipError_t launch_prefill_t(const PrefillArgs &a, hipStream_t st, hipStre
     return hipGetLastError();
 }
 
-hipError_t launch_prefill(int H, int I, const PrefillArgs &a, hipStream_t st, hipStream_t aux, hipEvent_t ev_fork,
-                          hipEvent_t ev_join, KernelTimer *T) {
-    if (H == 2048 && I == 512) return launch_prefill_t<2048, 512>(a, st, aux, ev_fork, ev_join, T);
-    if (H == 512 && I == 256) return launch_prefill_t<512, 256>(a, st, aux, ev_fork, ev_join, T);
+hipError_t launch_prefill(int H, int I, const PrefillArgs &a, hipStream_t st, KernelTimer *T) {
+    if (H == 2048 && I == 512) return launch_prefill_t<2048, 512>(a, st, T);
+    if (H == 512 && I == 256) return launch_prefill_t<512, 256>(a, st, T);
     return hipErrorInvalidValue;
 }
 

@@ -148,7 +148,7 @@ __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
             uint32_t v = n;
             if (wv == 1) v = n / PF_BM;
             else if (wv == 2) v = rem > PF_SMALL_MAX ? 1u : 0u;
-            else if (wv == 3) v = (rem > 0 && rem <= PF_SMALL_MAX) ? (rem + PF_SM - 1) / PF_SM : 0u;
+            else if (wv == 3) v = (rem > 0 && rem <= PF_SMALL_MAX) ? 1u : 0u;
             const uint32_t inc = wave_incl_scan(v, lane);
             if (e < E1) dst[e] = carry + inc - v;
             carry += __shfl(inc, 63);
@@ -167,9 +167,8 @@ __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
             for (int j = 0; j < nf; ++j) a.tiles[ts[e] + j] = Tile{e, (int)rg[e] + j * PF_BM, PF_BM, 0};
             if (rem > PF_SMALL_MAX) {
                 a.tiles[nfull + tp[e]] = Tile{e, (int)rg[e] + nf * PF_BM, rem, 0};
-            } else {
-                for (int j = 0; j * PF_SM < rem; ++j)
-                    small[tsm[e] + j] = Tile{e, (int)rg[e] + nf * PF_BM + j * PF_SM, min(PF_SM, rem - j * PF_SM), 0};
+            } else if (rem > 0) {
+                small[tsm[e]] = Tile{e, (int)rg[e] + nf * PF_BM, rem, 0};
             }
         }
         for (int i = (int)(nfull + tp[E1]) + tid; i < a.tile_max; i += BF_THREADS) a.tiles[i] = Tile{-1, 0, 0, 0};

@@ -43,8 +43,6 @@ struct moe_ctx {
     uint16_t *srid = nullptr;    // decode stack: routing of every layer
     float *srw = nullptr;
     int stack_ok = 0;            // all stack workgroups fit on the device at once
-    hipStream_t aux = nullptr;   // prefill small-tile GEMMs (non-blocking, default priority)
-    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     KernelTimer timer;
 };
 
@@ -186,17 +184,6 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
         delete c;
         return hip_fail(he, "moe_create: clearing workspace");
     }
-    he = hipStreamCreateWithFlags(&c->aux, hipStreamNonBlocking);
-    if (he == hipSuccess) he = hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming);
-    if (he == hipSuccess) he = hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming);
-    if (he != hipSuccess) {
-        if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
-        if (c->aux) (void)hipStreamDestroy(c->aux);
-        if (c->rpk) (void)hipFree(c->rpk);
-        (void)hipFree(c->arena);
-        delete c;
-        return hip_fail(he, "moe_create: second stream");
-    }
     // The decode stack needs every one of its workgroups resident at once.
     int per_cu = 0, ncu = 0;
     if (stack_occupancy(H, I, &per_cu) == hipSuccess &&
@@ -211,9 +198,6 @@ moe_status moe_destroy(moe_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipDeviceSynchronize();
     timer_free(ctx->timer);
-    if (ctx->ev_fork) (void)hipEventDestroy(ctx->ev_fork);
-    if (ctx->ev_join) (void)hipEventDestroy(ctx->ev_join);
-    if (ctx->aux) (void)hipStreamDestroy(ctx->aux);
     if (ctx->rpk) (void)hipFree(ctx->rpk);
     hipError_t he = hipFree(ctx->arena);
     delete ctx;
@@ -382,7 +366,7 @@ moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids,
     p.tile_max = b.tile_max;
     p.stile_max = b.stile_max;
     p.c = c;
-    he = launch_prefill(H, I, p, st, ctx->aux, ctx->ev_fork, ctx->ev_join, T);
+    he = launch_prefill(H, I, p, st, T);
     if (he != hipSuccess) return hip_fail(he, "moe_ffn: prefill launch");
     return ok();
 }

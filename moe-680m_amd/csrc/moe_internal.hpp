@@ -12,9 +12,8 @@ struct Tile {
     int32_t expert, row0, nrows, pad;
 };
 
-constexpr int PF_BM = 128; // prefill big-tile rows (token slots of one expert)
-constexpr int PF_SM = 16;  // prefill small-tile rows
-constexpr int PF_SMALL_MAX = 32; // remainders of at most this many slots become small tiles
+constexpr int PF_BM = 64;  // prefill big-tile rows (token slots of one expert)
+constexpr int PF_SMALL_MAX = 32; // remainders of at most this many slots are listed as small tiles
 
 struct DecodeArgs {
     LayerPtrs L;
@@ -123,18 +122,16 @@ hipError_t launch_router_topk(const float *logits, int M, int E, int renorm, uin
                               float *w, hipStream_t st, KernelTimer *T);
 hipError_t launch_bucket_fill(const BucketArgs &a, hipStream_t st, KernelTimer *T);
 hipError_t launch_decode(int H, int I, const DecodeArgs &a, hipStream_t st, KernelTimer *T);
-// Big-tile GEMMs run on st, small-tile GEMMs on aux (forked after prep with ev_fork and
-// joined back before the combine with ev_join); both streams see the same timer.
-hipError_t launch_prefill(int H, int I, const PrefillArgs &a, hipStream_t st, hipStream_t aux, hipEvent_t ev_fork,
-                          hipEvent_t ev_join, KernelTimer *T);
+// prep, one gate/up and one down launch over both tile lists, combine -- all on st.
+hipError_t launch_prefill(int H, int I, const PrefillArgs &a, hipStream_t st, KernelTimer *T);
 hipError_t launch_stack(int H, int I, const StackArgs &a, hipStream_t st, KernelTimer *T);
 hipError_t stack_occupancy(int H, int I, int *blocks_per_cu);
 int stack_blocks(int H);
 size_t stack_exchange_words(int H, int I, int n_layers);
 
 // Big tiles: PF_BM-slot tiles of every expert plus remainders above PF_SMALL_MAX slots.
-// Small tiles: remainders of 1..PF_SMALL_MAX slots cut into PF_SM-slot tiles (<= 2 per expert).
+// Small tiles: remainders of 1..PF_SMALL_MAX slots, one tile per expert.
 inline int tile_max_for(int M, int E1) { return (9 * M + PF_BM - 1) / PF_BM + E1; }
-inline int stile_max_for(int E1) { return 2 * E1; }
+inline int stile_max_for(int E1) { return E1; }
 
 } // namespace moe
