@@ -239,20 +239,23 @@ __device__ __forceinline__ void stage_mfma(const WStage<NR> &s0, const uint32_t 
 }
 
 // ---------------------------------------------------------------- K loop
-// A (the tile's token rows, f16) is resident in LDS one chunk of up to PF_KCH stages (512 K)
-// at a time: every thread helps stage a chunk, one barrier, then the 8 waves run the chunk's
-// stages with no barrier inside -- each wave waits only for its own weight loads, and the
-// other workgroup on the CU hides the chunk boundaries.  Weights come through a per-wave ring
+// A (the tile's token rows, f16) is resident in LDS one chunk at a time -- 64 KB: all of K for
+// 16-row tiles, 1024 K for 32 rows, 512 K for 64 rows: every thread helps stage a chunk, one
+// barrier, then the 8 waves run the chunk's stages with no barrier inside -- each wave waits
+// only for its own weight loads, and the other workgroup on the CU hides the chunk
+// boundaries.  Weights come through a per-wave ring
 // of 4 register stages, each requested three stages ahead in the order they are consumed (a
 // wave's in-order vmcnt waits then never hold a use behind a later prefetch); the ring runs
 // on across chunks.  Fully unrolled: with a rolled loop the compiler's vmcnt bookkeeping
 // merges at the loop head and waits for every prefetch in flight.
-constexpr int PF_KCH = 4; // stages per resident chunk
-
-// LDS row stride (halves) of a resident chunk for a K loop of NCH stages: +16 B per row, so
-// the 16 rows of an A fragment read hit 16 different bank groups.
-template <int NCH>
-constexpr int pf_ldsr() { return (NCH < PF_KCH ? NCH : PF_KCH) * PF_KC + 8; }
+// Stages per resident chunk for MT M-tiles (16*MT rows x KCH*PF_KC halves = 64 KB), and the
+// chunk's LDS row stride in halves: +16 B per row, so the 16 rows of an A fragment read hit
+// 16 different bank groups.
+template <int NCH, int MT>
+constexpr int pf_kch() { return NCH < 16 / MT ? NCH : 16 / MT; }
+template <int NCH, int MT>
+constexpr int pf_ldsr() { return pf_kch<NCH, MT>() * PF_KC + 8; }
+constexpr int PF_AS_HALVES = PF_BM * (4 * PF_KC + 8); // the largest chunk (64 rows x 520)
 
 // f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>), in order.
 template <typename F, int... Is>
@@ -288,9 +291,9 @@ template <int NCH, int RD, int NR, int MT, typename StageA>
 __device__ __forceinline__ void gemm_resident(WStage<NR> (&ws)[RD], const uint8_t *const (&rows)[NR],
                                               const _Float16 *As, int n, int g, f32x4 (&acc)[MT][NR],
                                               StageA stage_a) {
-    constexpr int KCH = NCH < PF_KCH ? NCH : PF_KCH;
-    constexpr int LK = pf_ldsr<NCH>();
-    static_assert(NCH % KCH == 0, "whole chunks");
+    constexpr int KCH = pf_kch<NCH, MT>();
+    constexpr int LK = pf_ldsr<NCH, MT>();
+    static_assert(NCH % KCH == 0 && 16 * MT * LK <= PF_AS_HALVES, "whole chunks that fit");
     static_for<NCH>([&](auto CHc) __attribute__((always_inline)) {
         constexpr int ch = decltype(CHc)::value, S = ch % RD;
         if constexpr (ch > 0 && ch % KCH == 0) {
@@ -327,11 +330,10 @@ __device__ __forceinline__ void by_mtiles(int nrows, F f) {
 // ---------------------------------------------------------------- gate/up
 template <int H, int I>
 __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) {
-    constexpr int NCH = H / PF_KC, KCH = NCH < PF_KCH ? NCH : PF_KCH, KC = KCH * PF_KC;
-    constexpr int LK = pf_ldsr<NCH>();
+    constexpr int NCH = H / PF_KC;
     constexpr int ROWB = (H / QK) * SB_BYTES;
     static_assert(H % QK == 0 && I % PF_NGU == 0 && PF_KC * 2 == QK, "gate/up shape");
-    __shared__ __attribute__((aligned(16))) _Float16 As[PF_BM * LK];
+    __shared__ __attribute__((aligned(16))) _Float16 As[PF_AS_HALVES];
     __shared__ uint32_t rowmax[PF_BM];
     __shared__ float s_inv[PF_BM];
     __shared__ int s_tok[PF_BM];
@@ -356,9 +358,10 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
 
     by_mtiles(nrows, [&](auto MTc) __attribute__((always_inline)) {
         constexpr int MT = decltype(MTc)::value;
-        // chunk c of A: 16*MT rows x KC halves, one wave per row and pass (KC/8 lanes x 16 B)
+        constexpr int KC = pf_kch<NCH, MT>() * PF_KC, LK = pf_ldsr<NCH, MT>();
+        // chunk c of A: 16*MT rows x KC halves, 16 B per lane, a row spanning whole waves
         constexpr int QPR = KC / 8, PER = 16 * MT * QPR / (64 * PF_WAVES);
-        static_assert(PER >= 1 && 16 * MT * QPR % (64 * PF_WAVES) == 0 && QPR == 64, "A staging split");
+        static_assert(PER >= 1 && 16 * MT * QPR % (64 * PF_WAVES) == 0 && QPR % 64 == 0, "A staging split");
         u32x4 va[PER];
         // quads [i0, i1) of chunk c: global -> registers, registers -> LDS
         auto load_a = [&](int c, int i0, int i1) __attribute__((always_inline)) {
@@ -366,7 +369,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
             for (int i = 0; i < PER; ++i)
                 if (i >= i0 && i < i1) {
                     const int idx = i * 64 * PF_WAVES + tid, r = idx / QPR, q = idx % QPR;
-                    // r is the same for the whole wave (QPR = 64): the token index in an SGPR
+                    // r is the same for the whole wave (QPR % 64 == 0): the token index in an SGPR
                     const int tok = __builtin_amdgcn_readfirstlane(s_tok[r]);
                     va[i] = ldg<u32x4>(a.xh + (size_t)tok * H + c * KC + 8 * q);
                 }
@@ -414,21 +417,22 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
                 if (n == 0) atomicMax(&rowmax[m], __builtin_bit_cast(uint32_t, rm));
             }
     });
-    __syncthreads();
+    // LDS only: a __syncthreads here would also wait for the h stores to complete
+    lds_barrier();
     if (tid < nrows) a.hmax[(size_t)(row0 + tid) * (I / PF_NGU) + blockIdx.x] = __builtin_bit_cast(float, rowmax[tid]);
 }
 
 // ---------------------------------------------------------------- down
 template <int H, int I>
 __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
-    constexpr int NTW = 2, NCH = I / PF_KC, KCH = NCH < PF_KCH ? NCH : PF_KCH, KC = KCH * PF_KC;
-    constexpr int LK = pf_ldsr<NCH>();
+    constexpr int NTW = 2, NCH = I / PF_KC;
     constexpr int ROWB = (I / QK) * SB_BYTES;
     constexpr int NHB = I / PF_NGU; // h max blocks per row
-    constexpr int BPR = KC / 32;     // 32-blocks per row in a chunk
+    constexpr int BPR = I / 32;      // 32-blocks per row
     static_assert(I % QK == 0 && H % PF_ND == 0 && PF_KC * 2 == QK, "down shape");
-    __shared__ __attribute__((aligned(16))) _Float16 As[PF_BM * LK];
-    __shared__ float s_scale[PF_BM], s_inv[PF_BM];
+    static_assert(pf_kch<NCH, 4>() == NCH, "all of K = inter resident in one chunk");
+    __shared__ __attribute__((aligned(16))) _Float16 As[PF_AS_HALVES];
+    __shared__ float s_inv[PF_BM];
 
     const Tile tl = a.tiles[blockIdx.y];
     if (tl.expert < 0) return;
@@ -436,59 +440,64 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
     const int r0 = blockIdx.x * PF_ND + wv * 32; // this wave's output rows r0 .. r0+31
-
-    // h rows are scaled by a power of two from their max into f16 as they are staged
-    if (tid < PF_BM) {
-        float mx = 0.f;
-        if (tid < nrows)
-#pragma unroll
-            for (int b = 0; b < NHB; ++b) mx = fmaxf(mx, a.hmax[(size_t)(row0 + tid) * NHB + b]);
-        float inv;
-        s_scale[tid] = pow2_scale(mx, &inv);
-        s_inv[tid] = inv;
-    }
-    lds_barrier();
     const uint8_t *w2 = expert_w(a.L.w2, a.L.s2, a.L.sw2, e, a.E);
     const uint8_t *rows[NTW] = {uniform_ptr(w2 + (size_t)r0 * ROWB), uniform_ptr(w2 + (size_t)(r0 + 16) * ROWB)};
 
     by_mtiles(nrows, [&](auto MTc) __attribute__((always_inline)) {
         constexpr int MT = decltype(MTc)::value;
-        // chunk c of A: 16*MT rows x BPR 32-blocks, one block (32 f32 -> 32 f16 in the
-        // weights' K order) per thread and pass
-        auto stage_a = [&](int c) __attribute__((always_inline)) {
+        constexpr int LK = pf_ldsr<NCH, MT>();
+        // A: 16*MT rows x BPR 32-blocks; a thread takes blocks tid, tid + 512, ... -- each one
+        // 32 f32 of h, scaled by a power of two from the row's max into 32 f16 in the weights'
+        // K order.  All loads (h and the row's max blocks) are issued before any is used.
+        constexpr int NIT = 16 * MT * BPR, IPT = (NIT + 64 * PF_WAVES - 1) / (64 * PF_WAVES);
+        f32x4 hv[IPT][8];
+        float hm[IPT][NHB];
 #pragma unroll
-            for (int it0 = 0; it0 < 16 * MT * BPR; it0 += 64 * PF_WAVES) {
-                const int it = it0 + tid;
-                if (it0 + 64 * PF_WAVES <= 16 * MT * BPR || it < 16 * MT * BPR) {
-                    const int ar = it / BPR, ab = it % BPR;
-                    const int slot = row0 + (ar < nrows ? ar : nrows - 1);
-                    const float sc = s_scale[ar];
-                    float v[32];
-                    load32(a.hf + (size_t)slot * I + c * KC + 32 * ab, v);
-                    u32x4 o[4];
+        for (int j = 0; j < IPT; ++j) {
+            const int it = j * 64 * PF_WAVES + tid;
+            if (IPT * 64 * PF_WAVES == NIT || it < NIT) {
+                const int ar = it / BPR, ab = it % BPR;
+                const int slot = row0 + (ar < nrows ? ar : nrows - 1);
+                const f32x4 *src = reinterpret_cast<const f32x4 *>(a.hf + (size_t)slot * I + 32 * ab);
 #pragma unroll
-                    for (int p = 0; p < 16; ++p) {
-                        const int gg = (2 * p) >> 3, j = (2 * p) & 7;
-                        const int k0 = j < 4 ? 4 * gg + j : 16 + 4 * gg + (j - 4);
-                        o[p >> 2][p & 3] = pack_f16x2(v[k0] * sc, v[k0 + 1] * sc);
-                    }
-                    u32x4 *d = reinterpret_cast<u32x4 *>(As + ar * LK + 32 * ab);
+                for (int i = 0; i < 8; ++i) hv[j][i] = ldg<f32x4>(src + i);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) d[i] = o[i];
-                }
+                for (int b = 0; b < NHB; ++b) hm[j][b] = a.hmax[(size_t)slot * NHB + b];
             }
-        };
+        }
         constexpr int RD = 4; // weight ring depth: three stages ahead
         WStage<NTW> ws[RD];
         wring_prologue<NCH, RD>(ws, rows, lane);
-        stage_a(0);
+#pragma unroll
+        for (int j = 0; j < IPT; ++j) {
+            const int it = j * 64 * PF_WAVES + tid;
+            if (IPT * 64 * PF_WAVES == NIT || it < NIT) {
+                const int ar = it / BPR, ab = it % BPR;
+                float mx = 0.f;
+#pragma unroll
+                for (int b = 0; b < NHB; ++b) mx = fmaxf(mx, hm[j][b]);
+                float inv;
+                const float sc = pow2_scale(ar < nrows ? mx : 0.0f, &inv);
+                if (ab == 0) s_inv[ar] = inv;
+                u32x4 o[4];
+#pragma unroll
+                for (int p = 0; p < 16; ++p) {
+                    const int gg = (2 * p) >> 3, jj = (2 * p) & 7;
+                    const int k0 = jj < 4 ? 4 * gg + jj : 16 + 4 * gg + (jj - 4);
+                    o[p >> 2][p & 3] = pack_f16x2(hv[j][k0 >> 2][k0 & 3] * sc, hv[j][(k0 + 1) >> 2][(k0 + 1) & 3] * sc);
+                }
+                u32x4 *d = reinterpret_cast<u32x4 *>(As + ar * LK + 32 * ab);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) d[i] = o[i];
+            }
+        }
         lds_barrier();
         f32x4 acc[MT][NTW];
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
             for (int t = 0; t < NTW; ++t) acc[i][t] = f32x4{0, 0, 0, 0};
-        gemm_resident<NCH, RD, NTW, MT>(ws, rows, As, n, g, acc, stage_a);
+        gemm_resident<NCH, RD, NTW, MT>(ws, rows, As, n, g, acc, [](int) {});
 
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
