@@ -93,43 +93,55 @@ __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
     uint32_t *tp = ts + (E1 + 1);   // partial big tile index (after all full ones)
     uint32_t *tsm = tp + (E1 + 1);  // first small tile
     if (tid == 0) s_flags = 0;
+    __syncthreads();
+    // Each wave owns one chunk (64 tokens) and one bitmap set at a time, and LDS operations
+    // of one wave complete in order, so phases 1 and 3 need no barrier inside.  The first
+    // pass keeps its tokens' ids in registers for phase 3.
+    uint32_t idk[SLOTS];
+    uint32_t *bm = bm_all + (size_t)(wv < CW ? wv : 0) * E1 * 2;
+    const uint32_t bit = 1u << (lane & 31);
 
     // Phase 1: per-chunk bucket counts.
     for (int base = 0; base < nch; base += CW) {
         const int c = base + wv;
-        const bool active = (wv < CW) && (c < nch);
-        uint32_t *bm = bm_all + (size_t)(wv < CW ? wv : 0) * E1 * 2;
-        if (active)
+        if (wv < CW && c < nch) {
             for (int i = lane; i < 2 * E1; i += 64) bm[i] = 0;
-        __syncthreads();
-        if (active) {
             const int t = c * 64 + lane;
+            uint32_t f = 0;
             if (t < M) {
-                uint32_t f = 0;
+                uint32_t e9[SLOTS];
+#pragma unroll
+                for (int s = 0; s < SLOTS; ++s) e9[s] = a.ids[(size_t)t * SLOTS + s];
+#pragma unroll
                 for (int s = 0; s < SLOTS; ++s) {
-                    int e = a.ids[(size_t)t * SLOTS + s];
-                    if (e >= E1) { f |= MOE_DEVFLAG_BAD_ID; continue; }
-                    uint32_t bit = 1u << (lane & 31);
-                    uint32_t old = atomicOr(&bm[2 * e + (lane >> 5)], bit);
+                    if (base == 0) idk[s] = e9[s];
+                    const uint32_t e = e9[s];
+                    if (e >= (uint32_t)E1) { f |= MOE_DEVFLAG_BAD_ID; continue; }
+                    const uint32_t old = atomicOr(&bm[2 * e + (lane >> 5)], bit);
                     if (old & bit) f |= MOE_DEVFLAG_DUP_ID;
                 }
-                if (f) atomicOr(&s_flags, f);
             }
-        }
-        __syncthreads();
-        if (active)
+            if (f) atomicOr(&s_flags, f);
             for (int e = lane; e < E1; e += 64)
                 a.chunk_cnt[(size_t)c * E1 + e] = __popc(bm[2 * e]) + __popc(bm[2 * e + 1]);
-        __syncthreads();
+        }
     }
+    __syncthreads();
 
-    // Phase 2a: exclusive scan of each bucket's chunk counts (in place), bucket totals.
+    // Phase 2a: exclusive scan of each bucket's chunk counts (in place), bucket totals; the
+    // counts are loaded 16 at a time as independent loads before any is overwritten.
     for (int e = tid; e < E1; e += BF_THREADS) {
         uint32_t run = 0;
-        for (int c = 0; c < nch; ++c) {
-            uint32_t v = a.chunk_cnt[(size_t)c * E1 + e];
-            a.chunk_cnt[(size_t)c * E1 + e] = run;
-            run += v;
+        for (int c0 = 0; c0 < nch; c0 += 16) {
+            uint32_t v[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = c0 + j < nch ? a.chunk_cnt[(size_t)(c0 + j) * E1 + e] : 0u;
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                if (c0 + j < nch) {
+                    a.chunk_cnt[(size_t)(c0 + j) * E1 + e] = run;
+                    run += v[j];
+                }
         }
         tot[e] = run;
     }
@@ -178,40 +190,38 @@ __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
     // Phase 3: rebuild each chunk's bitmaps and scatter.
     for (int base = 0; base < nch; base += CW) {
         const int c = base + wv;
-        const bool active = (wv < CW) && (c < nch);
-        uint32_t *bm = bm_all + (size_t)(wv < CW ? wv : 0) * E1 * 2;
-        if (active)
+        if (wv < CW && c < nch) {
             for (int i = lane; i < 2 * E1; i += 64) bm[i] = 0;
-        __syncthreads();
-        const int t = c * 64 + lane;
-        uint32_t ok = 0;
-        if (active && t < M) {
-            for (int s = 0; s < SLOTS; ++s) {
-                int e = a.ids[(size_t)t * SLOTS + s];
-                if (e >= E1) continue;
-                uint32_t bit = 1u << (lane & 31);
-                uint32_t old = atomicOr(&bm[2 * e + (lane >> 5)], bit);
-                if (!(old & bit)) ok |= 1u << s;
-            }
-        }
-        __syncthreads();
-        if (active && t < M) {
-            const uint32_t below = (1u << (lane & 31)) - 1u;
-            for (int s = 0; s < SLOTS; ++s) {
-                uint32_t p = 0xFFFFFFFFu;
-                if ((ok >> s) & 1u) {
-                    int e = a.ids[(size_t)t * SLOTS + s];
-                    uint32_t rank = __popc(bm[2 * e + (lane >> 5)] & below) +
-                                    ((lane >> 5) ? __popc(bm[2 * e]) : 0u);
-                    p = rg[e] + a.chunk_cnt[(size_t)c * E1 + e] + rank;
-                    a.sorted_tok[p] = (uint16_t)t;
-                    a.sorted_w[p] = a.w[(size_t)t * SLOTS + s];
+            const int t = c * 64 + lane;
+            uint32_t ok = 0;
+            uint32_t e9[SLOTS];
+            if (t < M) {
+#pragma unroll
+                for (int s = 0; s < SLOTS; ++s) e9[s] = base == 0 ? idk[s] : (uint32_t)a.ids[(size_t)t * SLOTS + s];
+#pragma unroll
+                for (int s = 0; s < SLOTS; ++s) {
+                    if (e9[s] >= (uint32_t)E1) continue;
+                    const uint32_t old = atomicOr(&bm[2 * e9[s] + (lane >> 5)], bit);
+                    if (!(old & bit)) ok |= 1u << s;
                 }
-                if (a.pos) a.pos[(size_t)t * SLOTS + s] = p;
+                const uint32_t below = bit - 1u;
+#pragma unroll
+                for (int s = 0; s < SLOTS; ++s) {
+                    uint32_t p = 0xFFFFFFFFu;
+                    if ((ok >> s) & 1u) {
+                        const uint32_t e = e9[s];
+                        const uint32_t rank = __popc(bm[2 * e + (lane >> 5)] & below) +
+                                              ((lane >> 5) ? __popc(bm[2 * e]) : 0u);
+                        p = rg[e] + a.chunk_cnt[(size_t)c * E1 + e] + rank;
+                        a.sorted_tok[p] = (uint16_t)t;
+                        a.sorted_w[p] = a.w[(size_t)t * SLOTS + s];
+                    }
+                    if (a.pos) a.pos[(size_t)t * SLOTS + s] = p;
+                }
             }
         }
-        __syncthreads();
     }
+    __syncthreads();
     if (tid == 0 && s_flags) set_flag(a.flags, s_flags);
 }
 
