@@ -174,6 +174,14 @@ __global__ __launch_bounds__(256) void k_pf_prep(PrefillArgs a) {
 }
 
 // ---------------------------------------------------------------- shared pipeline pieces
+// A wave-uniform pointer moved to SGPRs (loads then take a scalar base and a lane offset).
+template <typename T>
+__device__ __forceinline__ const T *uniform_ptr(const T *p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const T *)(((uint64_t)hi << 32) | lo);
+}
+
 // Raw IQ4_XS data of one K stage (PF_KC = 128 K = 4 sub-blocks, half a super-block) for NR
 // 16-row weight groups, read from the R16 layout (k_repack_r16): lane (g, n) gets the
 // header of row n and, in one 16-byte load, dword g of each of the stage's 4 sub-blocks of
@@ -191,11 +199,15 @@ struct WStage {
 template <int NR>
 __device__ __forceinline__ void wstage_load(WStage<NR> &s, const uint8_t *const (&groups)[NR], int ch, int lane) {
     const int sb = ch >> 1, h = ch & 1;
+    // unsigned lane offsets (zero-extended) on a wave-uniform block base that goes through
+    // readfirstlane: the loads then take an SGPR base and one 32-bit lane offset; past the
+    // immediate-offset range the compiler would otherwise rebuild a 64-bit VGPR address
+    const uint32_t oh = 8u * (uint32_t)(lane & 15), oq = 16u * (uint32_t)lane;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-        const uint8_t *blk = groups[r] + (size_t)sb * R16_BLOCK;
-        s.hdr[r] = ldg<u32x2>(blk + 8 * (lane & 15));
-        s.q[r] = ldg<u32x4>(blk + 128 + 1024 * h + 16 * lane);
+        const uint8_t *blk = uniform_ptr(groups[r] + (size_t)sb * R16_BLOCK);
+        s.hdr[r] = ldg<u32x2>(blk + oh);
+        s.q[r] = ldg<u32x4>(blk + 128 + 1024 * h + oq);
     }
 }
 
@@ -265,14 +277,6 @@ __device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int
 template <int N, typename F>
 __device__ __forceinline__ void static_for(F &&f) {
     static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
-// A wave-uniform pointer moved to SGPRs (loads then take a scalar base and a lane offset).
-template <typename T>
-__device__ __forceinline__ const T *uniform_ptr(const T *p) {
-    const uint64_t v = (uint64_t)p;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return (const T *)(((uint64_t)hi << 32) | lo);
 }
 
 // Weight ring of RD register stages: the prologue requests stages 0..RD-2.
@@ -369,9 +373,10 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
             for (int i = 0; i < PER; ++i)
                 if (i >= i0 && i < i1) {
                     const int idx = i * 64 * PF_WAVES + tid, r = idx / QPR, q = idx % QPR;
-                    // r is the same for the whole wave (QPR % 64 == 0): the token index in an SGPR
+                    // r is the same for the whole wave (QPR % 64 == 0): the row base in SGPRs
                     const int tok = __builtin_amdgcn_readfirstlane(s_tok[r]);
-                    va[i] = ldg<u32x4>(a.xh + (size_t)tok * H + c * KC + 8 * q);
+                    const _Float16 *rowp = uniform_ptr(a.xh + (size_t)tok * H + c * KC);
+                    va[i] = ldg<u32x4>(rowp + 8u * (uint32_t)q);
                 }
         };
         auto store_a = [&](int i0, int i1) __attribute__((always_inline)) {
