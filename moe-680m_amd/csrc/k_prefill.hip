@@ -8,15 +8,15 @@
 //   prep:    per token, x (RMSNorm fused when asked) times a power of two s_t that puts
 //            max|x| in [2^14, 2^15), stored as f16 with K permuted inside 32-blocks (the
 //            order the weight nibbles arrive in, see below); 1/s_t kept per token;
-//   gate_up: per (tile, 128 gate/up column pairs) a workgroup of 8 waves; the tile's token
-//            rows (gathered -- the reference's kernel skipped this gather) are staged in
-//            LDS 128 K at a time, double-buffered, and shared by the 8 waves; every wave
-//            decodes its own 16 W1 rows and 16 W3 rows straight into MFMA B fragments in
-//            registers (no LDS, no barrier for weights) and runs v_mfma_f32_16x16x32_f16;
+//   gate_up: per (tile, 128 gate/up column pairs) a workgroup of 8 waves, two per CU; the
+//            tile's token rows (gathered -- the reference's kernel skipped this gather) are
+//            resident in LDS one 64 KB chunk of K at a time and shared by the 8 waves; every
+//            wave decodes its own 16 W1 rows and 16 W3 rows straight into MFMA B fragments
+//            in registers (no LDS, no barrier for weights) and runs v_mfma_f32_16x16x32_f16;
 //            epilogue: silu(g) * u with the 1/s_t undone, f32 h, plus the per-row max|h|
 //            of each 128-column block;
-//   down:    per (tile, 256 output rows) the same over K = inter; the f32 h rows are
-//            scaled per row by a power of two (from the row max) into f16 as they are
+//   down:    per (tile, 256 output rows) the same over K = inter (one chunk); the f32 h rows
+//            are scaled per row by a power of two (from the row max) into f16 as they are
 //            staged; epilogue multiplies by 2^-s_row * c * slot weight, one f32 row per slot;
 //   combine: y_t (+)= sum over t's 9 slots in slot order -- deterministic, no atomics, no
 //            f16 read-modify-write race (the reference's w2_scatter.comp:77-86 RMW).
