@@ -83,13 +83,19 @@ struct NonzeroTag {
     }
 };
 
-// 16-byte loads that miss the CU's L1.  Remote: system scope (sc0 sc1) -- the line comes
-// from memory as last written through by any XCD.  Local: two agent-scope (sc1) atomic
-// 8-byte loads -- served by this XCD's L2, where the plain stores of its workgroups land.
-// Both are volatile or atomic, so the compiler re-issues them on every poll round.
+// 16-byte loads that miss the CU's L1, as two relaxed 8-byte atomic loads (atomic, so the
+// compiler re-issues them on every poll round; relaxed, so it does not wait for each one as
+// it does after a volatile load).  Remote: system scope (sc0 sc1) -- the line comes from
+// memory as last written through by any XCD.  Local: agent scope (sc1) -- served by this
+// XCD's L2, where the plain stores of its workgroups land.
 struct RemoteQuads {
     const u32x4 *p;
-    __device__ __forceinline__ u32x4 operator()(int q) const { return *(const volatile MOE_GLOBAL u32x4 *)(p + q); }
+    __device__ __forceinline__ u32x4 operator()(int q) const {
+        const MOE_GLOBAL uint64_t *g = (const MOE_GLOBAL uint64_t *)(p + q);
+        const uint64_t lo = __hip_atomic_load(g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        const uint64_t hi = __hip_atomic_load(g + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        return u32x4{(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
+    }
 };
 struct LocalQuads {
     const uint64_t *p;
