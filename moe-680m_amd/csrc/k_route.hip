@@ -12,11 +12,12 @@ namespace moe {
 // lower index wins ties exactly like the shader's strict '>' insertion
 // (router_topk.comp:76).  The softmax sum is one DPP + readlane reduction.
 template <int NV>
-__global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ logits, int M, int E,
-                                                     int renorm, uint16_t *__restrict__ ids,
-                                                     float *__restrict__ w) {
+__global__ __launch_bounds__(64) void k_router_topk(const float *__restrict__ logits, int M, int E,
+                                                    int renorm, uint16_t *__restrict__ ids,
+                                                    float *__restrict__ w) {
+    // one wave per workgroup: the dispatcher spreads the tokens over every CU and SIMD
     const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int t = blockIdx.x;
     if (t >= M) return; // whole wave leaves together
     int sel[TOPK];
     float ws[TOPK];
@@ -38,13 +39,13 @@ __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ l
 hipError_t launch_router_topk(const float *logits, int M, int E, int renorm, uint16_t *ids, float *w,
                               hipStream_t st, KernelTimer *T) {
     if (M <= 0) return hipSuccess;
-    dim3 grid((unsigned)((M + 3) / 4));
+    dim3 grid((unsigned)M);
     {
         TimedLaunch tl(T, MOE_K_ROUTER_TOPK, st);
         if (E <= 256)
-            hipLaunchKernelGGL(k_router_topk<4>, grid, dim3(256), 0, st, logits, M, E, renorm, ids, w);
+            hipLaunchKernelGGL(k_router_topk<4>, grid, dim3(64), 0, st, logits, M, E, renorm, ids, w);
         else
-            hipLaunchKernelGGL(k_router_topk<16>, grid, dim3(256), 0, st, logits, M, E, renorm, ids, w);
+            hipLaunchKernelGGL(k_router_topk<16>, grid, dim3(64), 0, st, logits, M, E, renorm, ids, w);
     }
     return hipGetLastError();
 }
@@ -70,13 +71,22 @@ __host__ inline size_t bucket_smem(int E1) {
     return (size_t)bucket_cw(E1) * E1 * 8 + 5 * (size_t)(E1 + 1) * 4;
 }
 
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        uint32_t o = __shfl_up(v, off);
-        if (lane >= off) v += o;
-    }
-    return v;
+// Inclusive scan over the wave by DPP: shifts of 1-3 lanes of the original values, then 4 and
+// 8 lanes of the partial sums (bank masks keep the lanes whose source is in the same row), then
+// row_bcast:15/31 carry the row totals into the rows above -- no LDS round trip.
+template <int CTRL, int ROW_MASK, int BANK_MASK>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, BANK_MASK, true);
+}
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+    uint32_t s = x + dpp_u<0x111, 0xF, 0xF>(x); // row_shr:1
+    s += dpp_u<0x112, 0xF, 0xF>(x);             // row_shr:2
+    s += dpp_u<0x113, 0xF, 0xF>(x);             // row_shr:3
+    s += dpp_u<0x114, 0xF, 0xE>(s);             // row_shr:4, banks 1-3
+    s += dpp_u<0x118, 0xF, 0xC>(s);             // row_shr:8, banks 2-3
+    s += dpp_u<0x142, 0xA, 0xF>(s);             // row_bcast:15 into rows 1, 3
+    s += dpp_u<0x143, 0xC, 0xF>(s);             // row_bcast:31 into rows 2, 3
+    return s;
 }
 
 __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
@@ -98,6 +108,7 @@ __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
     // of one wave complete in order, so phases 1 and 3 need no barrier inside.  The first
     // pass keeps its tokens' ids in registers for phase 3.
     uint32_t idk[SLOTS];
+    float wk[SLOTS];
     uint32_t *bm = bm_all + (size_t)(wv < CW ? wv : 0) * E1 * 2;
     const uint32_t bit = 1u << (lane & 31);
 
@@ -112,6 +123,9 @@ __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
                 uint32_t e9[SLOTS];
 #pragma unroll
                 for (int s = 0; s < SLOTS; ++s) e9[s] = a.ids[(size_t)t * SLOTS + s];
+                if (base == 0)
+#pragma unroll
+                    for (int s = 0; s < SLOTS; ++s) wk[s] = a.w[(size_t)t * SLOTS + s];
 #pragma unroll
                 for (int s = 0; s < SLOTS; ++s) {
                     if (base == 0) idk[s] = e9[s];
@@ -161,9 +175,9 @@ __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
             if (wv == 1) v = n / PF_BM;
             else if (wv == 2) v = rem > PF_SMALL_MAX ? 1u : 0u;
             else if (wv == 3) v = (rem > 0 && rem <= PF_SMALL_MAX) ? 1u : 0u;
-            const uint32_t inc = wave_incl_scan(v, lane);
+            const uint32_t inc = wave_incl_scan(v);
             if (e < E1) dst[e] = carry + inc - v;
-            carry += __shfl(inc, 63);
+            carry += (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
         }
         if (lane == 0) dst[E1] = carry;
     }
@@ -214,7 +228,7 @@ __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
                                               ((lane >> 5) ? __popc(bm[2 * e]) : 0u);
                         p = rg[e] + a.chunk_cnt[(size_t)c * E1 + e] + rank;
                         a.sorted_tok[p] = (uint16_t)t;
-                        a.sorted_w[p] = a.w[(size_t)t * SLOTS + s];
+                        a.sorted_w[p] = base == 0 ? wk[s] : a.w[(size_t)t * SLOTS + s];
                     }
                     if (a.pos) a.pos[(size_t)t * SLOTS + s] = p;
                 }
