@@ -115,13 +115,14 @@ __device__ __forceinline__ float max16(float v) {
 }
 
 // ---------------------------------------------------------------- prep
-// One wave per token; lane owns 32-blocks lane, lane+64, ... of the row.
+// One wave per token (and per workgroup, so the tokens spread over every CU); lane owns
+// 32-blocks lane, lane+64, ... of the row.
 template <int H>
-__global__ __launch_bounds__(256) void k_pf_prep(PrefillArgs a) {
+__global__ __launch_bounds__(64) void k_pf_prep(PrefillArgs a) {
     constexpr int NB = H / 32 / 64 > 0 ? H / 32 / 64 : 1; // 32-blocks per lane
     static_assert(H % (32 * 64) == 0 || H == 512, "prep shape");
     const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int t = blockIdx.x;
     if (t >= a.M) return;
     constexpr int NBK = H / 32;
     float v[NB][32];
@@ -545,7 +546,7 @@ template <int H, int I>
 static hipError_t launch_prefill_t(const PrefillArgs &a, hipStream_t st, KernelTimer *T) {
     {
         TimedLaunch tl(T, MOE_K_PREFILL_PREP, st);
-        hipLaunchKernelGGL((k_pf_prep<H>), dim3((a.M + 3) / 4), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((k_pf_prep<H>), dim3(a.M), dim3(64), 0, st, a);
     }
     // one launch over both tile lists (full and big remainder tiles, then small remainders)
     const int ntiles = a.tile_max + a.stile_max;
