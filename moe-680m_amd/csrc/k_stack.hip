@@ -196,29 +196,29 @@ __device__ __forceinline__ void store_quad(uint32_t *xq, int q, u32x4 v) {
 
 // One qs dword (weights 4d..4d+3 low nibbles, 16+4d.. high nibbles) against the planes'
 // dwords of those elements: xh_lo = dword d, xh_hi = dword 4+d (and the same for xl).
-__device__ __forceinline__ void dword_idot(uint32_t q, uint32_t xh_lo, uint32_t xh_hi, uint32_t xl_lo,
+// lo, hi: the signed codebook bytes of the dword's low and high nibbles (kv_signed8).
+__device__ __forceinline__ void dword_idot(uint32_t lo, uint32_t hi, uint32_t xh_lo, uint32_t xh_hi, uint32_t xl_lo,
                                            uint32_t xl_hi, int &ah, int &al) {
-    uint32_t lo, hi;
-    kv_signed8(q, lo, hi);
     ah = __builtin_amdgcn_sdot4((int)lo, (int)xh_lo, ah, false);
     ah = __builtin_amdgcn_sdot4((int)hi, (int)xh_hi, ah, false);
     al = __builtin_amdgcn_sdot4((int)lo, (int)xl_lo, al, false);
     al = __builtin_amdgcn_sdot4((int)hi, (int)xl_hi, al, false);
 }
 
-// Whole sub-block against chunk planes xh[8], xl[8]: sum kv * (xh + xl/256), unscaled.
-__device__ __forceinline__ float subblock_idot(u32x4 qs, const uint32_t (&xh)[8], const uint32_t (&xl)[8]) {
+// Whole sub-block, already looked up (kv[2d], kv[2d+1] = kv_signed8 of qs dword d), against
+// chunk planes xh[8], xl[8]: sum kv * (xh + xl/256), unscaled.
+__device__ __forceinline__ float subblock_idot(const uint32_t (&kv)[8], const uint32_t (&xh)[8],
+                                               const uint32_t (&xl)[8]) {
     int ah = 0, al = 0;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) dword_idot(qs[d], xh[d], xh[4 + d], xl[d], xl[4 + d], ah, al);
+    for (int d = 0; d < 4; ++d) dword_idot(kv[2 * d], kv[2 * d + 1], xh[d], xh[4 + d], xl[d], xl[4 + d], ah, al);
     return __builtin_fmaf((float)al, 1.0f / 256.0f, (float)ah);
 }
 
 // 8 weights of one qs dword -- weights 4d..4d+3 (low nibbles) and 16+4d..16+4d+3 (high
-// nibbles) of a sub-block -- against their activations xl[0..3], xh[0..3]; unscaled.
-__device__ __forceinline__ float dword_dot(uint32_t q, const float *xl, const float *xh) {
-    uint32_t lo, hi;
-    kv_biased8(q, lo, hi);
+// nibbles) of a sub-block, as the biased codebook bytes lo, hi (kv_biased8) -- against their
+// activations xl[0..3], xh[0..3]; unscaled.
+__device__ __forceinline__ float dword_dot(uint32_t lo, uint32_t hi, const float *xl, const float *xh) {
     float a0 = ubyte(lo, 0) * xl[0], a1 = ubyte(lo, 1) * xl[1];
     a0 = __builtin_fmaf(ubyte(lo, 2), xl[2], a0);
     a1 = __builtin_fmaf(ubyte(lo, 3), xl[3], a1);
@@ -228,6 +228,25 @@ __device__ __forceinline__ float dword_dot(uint32_t q, const float *xl, const fl
     a1 = __builtin_fmaf(ubyte(hi, 3), xh[3], a1);
     const float xs = ((xl[0] + xl[1]) + (xl[2] + xl[3])) + ((xh[0] + xh[1]) + (xh[2] + xh[3]));
     return (a0 + a1) - 128.f * xs;
+}
+
+// Whole sub-block, already looked up (kv[2d], kv[2d+1] = kv_biased8 of qs dword d), against
+// its 32 activations xv; xs = their sum.  Unscaled.
+__device__ __forceinline__ float subblock_dot(const uint32_t (&kv)[8], const float (&xv)[32], float xs) {
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const uint32_t lo = kv[2 * d], hi = kv[2 * d + 1];
+        a0 = __builtin_fmaf(ubyte(lo, 0), xv[4 * d + 0], a0);
+        a1 = __builtin_fmaf(ubyte(lo, 1), xv[4 * d + 1], a1);
+        a2 = __builtin_fmaf(ubyte(lo, 2), xv[4 * d + 2], a2);
+        a3 = __builtin_fmaf(ubyte(lo, 3), xv[4 * d + 3], a3);
+        a0 = __builtin_fmaf(ubyte(hi, 0), xv[16 + 4 * d + 0], a0);
+        a1 = __builtin_fmaf(ubyte(hi, 1), xv[16 + 4 * d + 1], a1);
+        a2 = __builtin_fmaf(ubyte(hi, 2), xv[16 + 4 * d + 2], a2);
+        a3 = __builtin_fmaf(ubyte(hi, 3), xv[16 + 4 * d + 3], a3);
+    }
+    return ((a0 + a1) + (a2 + a3)) - 128.f * xs;
 }
 
 template <int H, int I>
@@ -379,6 +398,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         lds_barrier(); // B0
         for (int li = 0; li < n; ++li) {
             lds_barrier(); // B1: x_li in LDS
+            __builtin_amdgcn_s_setprio(0);
             {
                 // h of the XCD: the first poller wave takes the shared rows (lane t: the 16
                 // words of shared row t -- eight waves' partial (g, u) -- combined here), the
@@ -423,6 +443,9 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             }
             lds_barrier(); // B2: h_li in LDS
             lds_barrier(); // B3: this workgroup's contributions in LDS
+            // until B1 the compute waves only decode the next layer's weights, which is off
+            // the critical path: let the exchange win every VALU issue slot on its SIMD
+            __builtin_amdgcn_s_setprio(2);
             if (first) {
                 // publish this XCD's partial of rows [64j, 64j+64) ...
                 uint32_t *pb = pbuf(li);
@@ -529,6 +552,13 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     u32x4 aq1[STA], aq3[STA], bq[STB];
     u32x2 ah1[STA], ah3[STA], bh[STB], sah, saq, sbh;
     uint32_t sbq;
+    // Phase-A weights of the next layer decoded -- codebook bytes and sub-block scales -- while
+    // the compute waves would otherwise wait for x (the lookup does not depend on x).
+    uint32_t ak1[STA][8], ak3[STA][8], sak[4];
+    float as1[STA], as3[STA], sas;
+    // ... and this layer's phase-B weights, while the pollers exchange h
+    uint32_t bk[STB][8], sbk[2];
+    float bs[STB], sbs;
 
     // Loads of layer li's phase-A (W1, W3) weights for this wave, issued right after phase A
     // of layer li-1 (after B2, so that the routing computed during phase A is visible), and
@@ -563,11 +593,64 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         sbq = ldg<uint32_t>(WS + offSB + qSB);
     };
 
+    auto decode_a = [&]() __attribute__((always_inline)) {
+        // The loaded words pass through empty volatile asm statements, which keep their order
+        // with the barrier's: otherwise the compiler may hoist this register-only work above
+        // the preceding barrier, onto the critical path.
+#pragma unroll
+        for (int st = 0; st < STA; ++st) asm volatile("" : "+v"(aq1[st]), "+v"(aq3[st]), "+v"(ah1[st]), "+v"(ah3[st]));
+        asm volatile("" : "+v"(saq), "+v"(sah));
+#pragma unroll
+        for (int st = 0; st < STA; ++st) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                kv_signed8(aq1[st][d], ak1[st][2 * d], ak1[st][2 * d + 1]);
+                kv_signed8(aq3[st][d], ak3[st][2 * d], ak3[st][2 * d + 1]);
+            }
+            as1[st] = sub_scale(ah1[st], ib1);
+            as3[st] = sub_scale(ah3[st], ib1);
+        }
+        kv_signed8(saq[0], sak[0], sak[1]);
+        kv_signed8(saq[1], sak[2], sak[3]);
+        sas = sub_scale(sah, sbg & 7);
+        // ... and the results as well, so that the work is not sunk below the next barrier
+        // either
+#pragma unroll
+        for (int st = 0; st < STA; ++st)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(ak1[st][e]), "+v"(ak3[st][e]));
+        asm volatile("" : "+v"(sak[0]), "+v"(sak[1]), "+v"(sak[2]), "+v"(sak[3]));
+        asm volatile("" : "+v"(as1), "+v"(as3), "+v"(sas));
+    };
+
+    auto decode_b = [&]() __attribute__((always_inline)) {
+        // after this wave's phase-A stores ("memory"), for the reason given in decode_a
+#pragma unroll
+        for (int st = 0; st < STB; ++st) asm volatile("" : "+v"(bq[st]), "+v"(bh[st]) : : "memory");
+        asm volatile("" : "+v"(sbq), "+v"(sbh) : : "memory");
+#pragma unroll
+        for (int st = 0; st < STB; ++st) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) kv_biased8(bq[st][d], bk[st][2 * d], bk[st][2 * d + 1]);
+            bs[st] = sub_scale(bh[st], ibB);
+        }
+        kv_biased8(sbq, sbk[0], sbk[1]);
+        sbs = sub_scale(sbh, ccB & 7);
+#pragma unroll
+        for (int st = 0; st < STB; ++st)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(bk[st][e]));
+        asm volatile("" : "+v"(sbk[0]), "+v"(sbk[1]), "+v"(bs), "+v"(sbs));
+    };
+
     lds_barrier(); // B0: routing of layers 0 and 1 is in LDS
     prefetch_a(0);
+    decode_a();
 
     for (int li = 0; li < n; ++li) {
         lds_barrier(); // B1: x_l in LDS
+        // phase A ahead of the other compute wave's decode on this SIMD
+        __builtin_amdgcn_s_setprio(1);
         prefetch_b(li);
         __builtin_amdgcn_sched_barrier(0);
         // phase A: h = silu(W1 xin) * (W3 xin) for this wave's slot-k row pairs, and this
@@ -604,20 +687,22 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             uint32_t *hb = hbuf(li);
 #pragma unroll
             for (int st = 0; st < STA; ++st) {
-                float g = (sub_scale(ah1[st], ib1) * sx) * subblock_idot(aq1[st], xh, xl);
-                float u = (sub_scale(ah3[st], ib1) * sx) * subblock_idot(aq3[st], xh, xl);
+                float g = (as1[st] * sx) * subblock_idot(ak1[st], xh, xl);
+                float u = (as3[st] * sx) * subblock_idot(ak3[st], xh, xl);
                 g = inv * row_total<LPR1>(g);
                 u = inv * row_total<LPR1>(u);
                 if (g1 == LPR1_LAST) tag_store_local(hb + rowA + st * RPS1 + rr1, silu_rcp(g) * u);
             }
             int sah_i = 0, sal_i = 0;
-            dword_idot(saq[0], sxh0[0], sxh1[0], sxl0[0], sxl1[0], sah_i, sal_i);
-            dword_idot(saq[1], sxh0[1], sxh1[1], sxl0[1], sxl1[1], sah_i, sal_i);
-            float sp = (sub_scale(sah, sbg & 7) * ssx) * __builtin_fmaf((float)sal_i, 1.0f / 256.0f, (float)sah_i);
+            dword_idot(sak[0], sak[1], sxh0[0], sxh1[0], sxl0[0], sxl1[0], sah_i, sal_i);
+            dword_idot(sak[2], sak[3], sxh0[1], sxh1[1], sxl0[1], sxl1[1], sah_i, sal_i);
+            float sp = (sas * ssx) * __builtin_fmaf((float)sal_i, 1.0f / 256.0f, (float)sah_i);
             sp = inv * adjacent_sum<LPRS>(sp);
             if (lane % LPRS == 0 && lane < NSA)
                 tag_store_local(hb + I + ((j * SRP + pA) * NCW + w) * 2 + mA, sp);
         }
+        __builtin_amdgcn_s_setprio(0);
+        decode_b();
         lds_barrier(); // B2: h_l in LDS; routing of layer li+2 in LDS
         prefetch_a(min(li + 1, n - 1));
         // nothing of phase B above the burst: its first use of this layer's W2 registers
@@ -638,7 +723,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             const float wk = a.c * rt_w[li % 3][0], wsh = a.c * rt_w[li % 3][1];
 #pragma unroll
             for (int st = 0; st < STB; ++st) {
-                float d = sub_scale(bh[st], ibB) * subblock_dot(bq[st], hv, hsum);
+                float d = bs[st] * subblock_dot(bk[st], hv, hsum);
                 d = group_sum<LPR2>(d);
                 if (g2 == 0) part[0][8 * w + st * RPS2 + rr2] = wk * d;
             }
@@ -652,11 +737,14 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                     hh4[e] = qh[e];
                 }
             }
-            float ds = sub_scale(sbh, ccB & 7) * dword_dot(sbq, hl, hh4);
+            float ds = sbs * dword_dot(sbk[0], sbk[1], hl, hh4);
             ds = adjacent_sum<LPRB>(ds);
             if (lane % LPRB == 0 && lane < NSB) part[1][8 * w + rB] = wsh * ds;
         }
         lds_barrier(); // B3: contributions in LDS
+        // the pollers now gather the partials and exchange x: decode layer li+1's phase-A
+        // weights (requested at B2) meanwhile
+        decode_a();
     }
 }
 
