@@ -240,6 +240,39 @@ hipError_t launch_repack_r16(const void *src, uint64_t src_stride, const void *s
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- split repack (decode stack)
+// One-time copy of a bound layer into the layout the decode stack reads.  Per matrix of nsb
+// super-blocks (row-major: rows x super-blocks per row):
+//     [nsb x 128-byte qs] [nsb x 8-byte header (d, scales_h, scales_l)]
+// -- the bytes of the natural layout (136 per super-block) split in two, so that every
+// 16-byte qs read is aligned and the headers a wave needs lie in a few cache lines.
+__global__ __launch_bounds__(256) void k_repack_split(const uint8_t *__restrict__ src, uint64_t src_stride,
+                                                      const uint8_t *__restrict__ shared, uint8_t *__restrict__ dst,
+                                                      uint64_t dst_stride, int E, uint64_t nsb) {
+    const int e = blockIdx.y;
+    const uint8_t *m = (e == E) ? shared : src + (uint64_t)e * src_stride;
+    uint8_t *o = dst + (uint64_t)e * dst_stride;
+    // one thread per 8-byte word (17 per super-block; word 0 is the header)
+    for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < nsb * 17;
+         t += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t sb = t / 17;
+        const int wd = (int)(t % 17);
+        const uint64_t v = *reinterpret_cast<const uint64_t *>(m + sb * SB_BYTES + 8u * wd);
+        uint8_t *to = wd == 0 ? o + nsb * 128 + sb * 8 : o + sb * 128 + 8u * (wd - 1);
+        *reinterpret_cast<uint64_t *>(to) = v;
+    }
+}
+
+hipError_t launch_repack_split(const void *src, uint64_t src_stride, const void *shared, void *dst,
+                               uint64_t dst_stride, int E, int rows, int cols, hipStream_t st) {
+    const uint64_t nsb = (uint64_t)rows * (cols / QK);
+    const uint64_t blocks = (nsb * 17 + 255) / 256;
+    dim3 grid((unsigned)(blocks < 4096 ? blocks : 4096), (unsigned)(E + 1));
+    hipLaunchKernelGGL(k_repack_split, grid, dim3(256), 0, st, (const uint8_t *)src, src_stride,
+                       (const uint8_t *)shared, (uint8_t *)dst, dst_stride, E, nsb);
+    return hipGetLastError();
+}
+
 hipError_t launch_dequant(const void *blocks, uint64_t n_sb, float *out, hipStream_t st) {
     uint64_t threads = n_sb * 8;
     if (threads == 0) return hipSuccess;

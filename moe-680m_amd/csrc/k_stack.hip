@@ -265,7 +265,6 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     // phase A, slot k: SRP row pairs per compute wave, a lane owning one sub-block of a row
     constexpr int LPR1 = (H / QK) * 8;       // lanes per W1/W3 row
     constexpr int RPS1 = 64 / LPR1;          // rows per wave step
-    constexpr int ROWB1 = (H / QK) * SB_BYTES;
     static_assert(SRP % RPS1 == 0 && SRP >= RPS1, "phase A split");
     static_assert(8 * SRP * NJ == I && SRP * NJ == I / NX, "phase A covers slot k and the shared share");
     constexpr int STA = SRP / RPS1;
@@ -279,7 +278,6 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     // W2_k (one sub-block per lane), and the XCD's CPX shared chunks (one qs dword per lane)
     constexpr int LPR2 = (I / QK) * 8;       // lanes per W2 row
     constexpr int RPS2 = 64 / LPR2;
-    constexpr int ROWB2 = (I / QK) * SB_BYTES;
     static_assert(8 % RPS2 == 0, "phase B split");
     constexpr int STB = 8 / RPS2;
     constexpr int LPRB = 4 * CPX;            // lanes per row, shared part
@@ -527,31 +525,77 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     const int g1 = lane % LPR1, rr1 = lane / LPR1, sb1 = g1 >> 3, ib1 = g1 & 7;
     // the lane of each row group that holds the row's total (see row_total)
     constexpr int LPR1_LAST = LPR1 == 64 ? 63 : 0;
+    // Weights are read from the split copy of the layer (k_repack_split): per matrix, the
+    // 128-byte qs of super-block (row, s) at 128 (row * SBR + s), then the 8-byte headers at
+    // HDR + 8 (row * SBR + s).
+    constexpr int SBR1 = H / QK, SBR2 = I / QK;
+    constexpr uint32_t HDR1 = (uint32_t)I * SBR1 * 128, HDR2 = (uint32_t)H * SBR2 * 128;
     uint32_t offA[STA];
 #pragma unroll
-    for (int st = 0; st < STA; ++st) offA[st] = (uint32_t)((rowA + st * RPS1 + rr1) * ROWB1 + sb1 * SB_BYTES);
+    for (int st = 0; st < STA; ++st) offA[st] = (uint32_t)(((rowA + st * RPS1 + rr1) * SBR1 + sb1) * 128 + 16 * ib1);
     // phase A, shared: lane -> row ri (pair ri/2, W1 or W3 by ri&1), sub-block sbg of this
     // wave's K range, half hh.  Lanes past NSA repeat valid addresses; their sums are dropped.
     const int ri = (lane / LPRS) % (2 * SRP), pA = ri >> 1, mA = ri & 1;
     const int sbg = w * SBW + ((lane % LPRS) >> 1), hh = lane & 1;
-    const uint32_t offSA = (uint32_t)((k * (I / NX) + j * SRP + pA) * ROWB1 + (sbg >> 3) * SB_BYTES);
-    const uint32_t qSA = 8 + 16 * (sbg & 7) + 8 * hh;
+    const uint32_t offSA = (uint32_t)(((k * (I / NX) + j * SRP + pA) * SBR1 + (sbg >> 3)) * 128 + 16 * (sbg & 7) + 8 * hh);
     // phase B, slot k: rows 8w + st*RPS2 + rr2 of the block, sub-block g2
     const int g2 = lane % LPR2, rr2 = lane / LPR2, ibB = g2 & 7;
     uint32_t offB[STB];
 #pragma unroll
     for (int st = 0; st < STB; ++st)
-        offB[st] = (uint32_t)((ROWS * j + 8 * w + st * RPS2 + rr2) * ROWB2 + (g2 >> 3) * SB_BYTES);
+        offB[st] = (uint32_t)(((ROWS * j + 8 * w + st * RPS2 + rr2) * SBR2 + (g2 >> 3)) * 128 + 16 * ibB);
     // phase B, shared: lane -> row rB of the wave's 8, chunk tB of the XCD's CPX, dword dB
     const int rB = (lane / LPRB) & 7, tB = (lane >> 2) % CPX, dB = lane & 3, ccB = CPX * k + tB;
-    const uint32_t offSB = (uint32_t)((ROWS * j + 8 * w + rB) * ROWB2 + (ccB >> 3) * SB_BYTES);
-    const uint32_t qSB = 8 + 16 * (ccB & 7) + 4 * dB;
+    const uint32_t offSB = (uint32_t)(((ROWS * j + 8 * w + rB) * SBR2 + (ccB >> 3)) * 128 + 16 * (ccB & 7) + 4 * dB);
     const int hSB = padk(I + 32 * tB) + 4 * dB;
+    // The super-block headers a wave needs of one layer, one per lane, fetched by one load
+    // (from a few cache lines of the header arrays) and handed to the lanes that use them
+    // with ds_bpermute: a load per header set -- every header is shared by 8-16 lanes --
+    // would cost address-unit time that the phases' own loads and stores queue behind.
+    // Lane order: phase A slot rows (W1, W3 x STA x RPS1 rows x super-blocks), phase A
+    // shared rows (2 SRP), phase B slot rows (STB x RPS2 rows x super-blocks), phase B
+    // shared rows (8).
+    constexpr int NHA = 2 * STA * RPS1 * SBR1, NHS = 2 * SRP, NHB = STB * RPS2 * SBR2;
+    static_assert(NHA + NHS + NHB + 8 <= 64, "one header per lane");
+    static_assert(SBW <= 8 && 8 % SBW == 0, "a wave's shared K range lies in one super-block");
+    int hsel;       // 0 W1, 1 W3, 2/3 shared W1/W3, 4 W2, 5 shared W2
+    uint32_t hoff;  // header offset in that matrix
+    {
+        const int L = lane < NHA + NHS + NHB + 8 ? lane : 0;
+        if (L < NHA) {
+            const int r = L / SBR1, rr = r % RPS1, st = (r / RPS1) % STA;
+            hsel = r / (RPS1 * STA);
+            hoff = HDR1 + (uint32_t)(((rowA + st * RPS1 + rr) * SBR1 + L % SBR1) * 8);
+        } else if (L < NHA + NHS) {
+            const int r = L - NHA;
+            hsel = 2 + (r & 1);
+            hoff = HDR1 + (uint32_t)(((k * (I / NX) + j * SRP + (r >> 1)) * SBR1 + ((w * SBW) >> 3)) * 8);
+        } else if (L < NHA + NHS + NHB) {
+            const int r = L - NHA - NHS;
+            hsel = 4;
+            hoff = HDR2 + (uint32_t)(((ROWS * j + 8 * w + r / SBR2) * SBR2 + r % SBR2) * 8);
+        } else {
+            hsel = 5;
+            hoff = HDR2 + (uint32_t)(((ROWS * j + 8 * w + (L - NHA - NHS - NHB)) * SBR2 + ((CPX * k) >> 3)) * 8);
+        }
+    }
+    // the lanes holding this lane's headers (x4: ds_bpermute byte addresses)
+    int hA1[STA], hA3[STA];
+#pragma unroll
+    for (int st = 0; st < STA; ++st) {
+        hA1[st] = 4 * (((0 * STA + st) * RPS1 + rr1) * SBR1 + sb1);
+        hA3[st] = 4 * (((1 * STA + st) * RPS1 + rr1) * SBR1 + sb1);
+    }
+    const int hSA = 4 * (NHA + ri);
+    int hB[STB];
+#pragma unroll
+    for (int st = 0; st < STB; ++st) hB[st] = 4 * (NHA + NHS + (st * RPS2 + rr2) * SBR2 + (g2 >> 3));
+    const int hSBr = 4 * (NHA + NHS + NHB + rB);
 
-    // Weights in flight, one set per phase.
+    // Weights in flight, one set per phase, and the headers of a layer.
     u32x4 aq1[STA], aq3[STA], bq[STB];
-    u32x2 ah1[STA], ah3[STA], bh[STB], sah, saq, sbh;
-    uint32_t sbq;
+    u32x2 saq;
+    uint32_t sbq, hd0, hd1;
     // Phase-A weights of the next layer decoded -- codebook bytes and sub-block scales -- while
     // the compute waves would otherwise wait for x (the lookup does not depend on x).
     uint32_t ak1[STA][8], ak3[STA][8], sak[4];
@@ -572,25 +616,33 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         const uint8_t *W3 = rt_p[li % 3][0][1];
 #pragma unroll
         for (int st = 0; st < STA; ++st) {
-            ah1[st] = ldg<u32x2>(W1 + offA[st]);
-            aq1[st] = ldg<u32x4>(W1 + offA[st] + 8 + 16 * ib1);
-            ah3[st] = ldg<u32x2>(W3 + offA[st]);
-            aq3[st] = ldg<u32x4>(W3 + offA[st] + 8 + 16 * ib1);
+            aq1[st] = ldg<u32x4>(W1 + offA[st]);
+            aq3[st] = ldg<u32x4>(W3 + offA[st]);
         }
-        const uint8_t *WS = rt_p[li % 3][1][mA];
-        sah = ldg<u32x2>(WS + offSA);
-        saq = ldg<u32x2>(WS + offSA + qSA);
+        saq = ldg<u32x2>(rt_p[li % 3][1][mA] + offSA);
+        // every header of the layer (phase B's too: used before the next such load)
+        const uint64_t b2 = (uint64_t)rt_p[li % 3][1][0], b3 = (uint64_t)rt_p[li % 3][1][1];
+        const uint64_t b4 = (uint64_t)rt_p[li % 3][0][2], b5 = (uint64_t)rt_p[li % 3][1][2];
+        uint64_t hb = (uint64_t)W1;
+        hb = hsel == 1 ? (uint64_t)W3 : hb;
+        hb = hsel == 2 ? b2 : hb;
+        hb = hsel == 3 ? b3 : hb;
+        hb = hsel == 4 ? b4 : hb;
+        hb = hsel == 5 ? b5 : hb;
+        const u32x2 hd = ldg<u32x2>((const uint8_t *)hb + hoff);
+        hd0 = hd.x;
+        hd1 = hd.y;
     };
     auto prefetch_b = [&](int li) __attribute__((always_inline)) {
         const uint8_t *W2 = rt_p[li % 3][0][2];
 #pragma unroll
-        for (int st = 0; st < STB; ++st) {
-            bh[st] = ldg<u32x2>(W2 + offB[st]);
-            bq[st] = ldg<u32x4>(W2 + offB[st] + 8 + 16 * ibB);
-        }
-        const uint8_t *WS = rt_p[li % 3][1][2];
-        sbh = ldg<u32x2>(WS + offSB);
-        sbq = ldg<uint32_t>(WS + offSB + qSB);
+        for (int st = 0; st < STB; ++st) bq[st] = ldg<u32x4>(W2 + offB[st]);
+        sbq = ldg<uint32_t>(rt_p[li % 3][1][2] + offSB);
+    };
+    // the header held by another lane (byte address 4 x lane)
+    auto header = [&](int from) __attribute__((always_inline)) {
+        return u32x2{(uint32_t)__builtin_amdgcn_ds_bpermute(from, (int)hd0),
+                     (uint32_t)__builtin_amdgcn_ds_bpermute(from, (int)hd1)};
     };
 
     auto decode_a = [&]() __attribute__((always_inline)) {
@@ -598,8 +650,8 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         // with the barrier's: otherwise the compiler may hoist this register-only work above
         // the preceding barrier, onto the critical path.
 #pragma unroll
-        for (int st = 0; st < STA; ++st) asm volatile("" : "+v"(aq1[st]), "+v"(aq3[st]), "+v"(ah1[st]), "+v"(ah3[st]));
-        asm volatile("" : "+v"(saq), "+v"(sah));
+        for (int st = 0; st < STA; ++st) asm volatile("" : "+v"(aq1[st]), "+v"(aq3[st]));
+        asm volatile("" : "+v"(saq), "+v"(hd0), "+v"(hd1));
 #pragma unroll
         for (int st = 0; st < STA; ++st) {
 #pragma unroll
@@ -607,12 +659,12 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 kv_signed8(aq1[st][d], ak1[st][2 * d], ak1[st][2 * d + 1]);
                 kv_signed8(aq3[st][d], ak3[st][2 * d], ak3[st][2 * d + 1]);
             }
-            as1[st] = sub_scale(ah1[st], ib1);
-            as3[st] = sub_scale(ah3[st], ib1);
+            as1[st] = sub_scale(header(hA1[st]), ib1);
+            as3[st] = sub_scale(header(hA3[st]), ib1);
         }
         kv_signed8(saq[0], sak[0], sak[1]);
         kv_signed8(saq[1], sak[2], sak[3]);
-        sas = sub_scale(sah, sbg & 7);
+        sas = sub_scale(header(hSA), sbg & 7);
         // ... and the results as well, so that the work is not sunk below the next barrier
         // either
 #pragma unroll
@@ -626,16 +678,16 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     auto decode_b = [&]() __attribute__((always_inline)) {
         // after this wave's phase-A stores ("memory"), for the reason given in decode_a
 #pragma unroll
-        for (int st = 0; st < STB; ++st) asm volatile("" : "+v"(bq[st]), "+v"(bh[st]) : : "memory");
-        asm volatile("" : "+v"(sbq), "+v"(sbh) : : "memory");
+        for (int st = 0; st < STB; ++st) asm volatile("" : "+v"(bq[st]) : : "memory");
+        asm volatile("" : "+v"(sbq), "+v"(hd0), "+v"(hd1) : : "memory");
 #pragma unroll
         for (int st = 0; st < STB; ++st) {
 #pragma unroll
             for (int d = 0; d < 4; ++d) kv_biased8(bq[st][d], bk[st][2 * d], bk[st][2 * d + 1]);
-            bs[st] = sub_scale(bh[st], ibB);
+            bs[st] = sub_scale(header(hB[st]), ibB);
         }
         kv_biased8(sbq, sbk[0], sbk[1]);
-        sbs = sub_scale(sbh, ccB & 7);
+        sbs = sub_scale(header(hSBr), ccB & 7);
 #pragma unroll
         for (int st = 0; st < STB; ++st)
 #pragma unroll

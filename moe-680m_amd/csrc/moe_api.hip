@@ -23,6 +23,7 @@ struct moe_ctx {
     std::vector<LayerPtrs> rlayers; // R16 repacked copies (prefill)
     std::vector<char> bound;
     uint8_t *rpk = nullptr;         // [n_layers][E+1][W1|W3|W2] R16, when m_max > MOE_DECODE_MAX_M
+    uint8_t *spk = nullptr;         // [n_layers][E+1][W1|W3|W2] split layout (decode stack)
     void *arena = nullptr; // one device allocation, carved below
     size_t arena_bytes = 0;
     uint32_t *flags = nullptr;
@@ -38,7 +39,7 @@ struct moe_ctx {
     uint32_t *pos = nullptr;     // [m_max][9]
     uint32_t *chunk = nullptr;   // [ceil(m_max/64)][E+1]
     Tile *tiles = nullptr;       // [tile_max(m_max) + stile_max]
-    LayerPtrs *dlayers = nullptr; // device copy of the layer table (decode stack)
+    LayerPtrs *dlayers = nullptr; // device layer table of the split copies (decode stack)
     uint32_t *xtag = nullptr;    // decode stack exchange buffers
     uint16_t *srid = nullptr;    // decode stack: routing of every layer
     float *srw = nullptr;
@@ -176,6 +177,19 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
                         hipGetErrorString(he));
         }
     }
+    {
+        // the decode stack reads a split copy of every bound layer (see k_repack_split)
+        const size_t mat = (size_t)H * I / QK * SB_BYTES;
+        const size_t sbytes = (size_t)cfg->n_layers * E1 * 3 * mat;
+        he = hipMalloc((void **)&c->spk, sbytes);
+        if (he != hipSuccess) {
+            if (c->rpk) (void)hipFree(c->rpk);
+            (void)hipFree(c->arena);
+            delete c;
+            return fail(MOE_ENOMEM, "moe_create: hipMalloc(%zu) for the decode-stack weight layout: %s", sbytes,
+                        hipGetErrorString(he));
+        }
+    }
     he = hipMemset(c->flags, 0, 256);
     if (he == hipSuccess) he = hipMemset(c->dlayers, 0, (size_t)cfg->n_layers * sizeof(LayerPtrs));
     if (he == hipSuccess) he = hipDeviceSynchronize();
@@ -199,6 +213,7 @@ moe_status moe_destroy(moe_ctx *ctx) {
     (void)hipDeviceSynchronize();
     timer_free(ctx->timer);
     if (ctx->rpk) (void)hipFree(ctx->rpk);
+    if (ctx->spk) (void)hipFree(ctx->spk);
     hipError_t he = hipFree(ctx->arena);
     delete ctx;
     if (he != hipSuccess) return hip_fail(he, "moe_destroy: hipFree");
@@ -229,10 +244,28 @@ moe_status moe_bind_layer(moe_ctx *ctx, int layer, const moe_layer_weights *lw) 
     L.sw1 = (const uint8_t *)lw->shared_w1;
     L.sw3 = (const uint8_t *)lw->shared_w3;
     L.sw2 = (const uint8_t *)lw->shared_w2;
-    hipError_t he = hipMemcpy(ctx->dlayers + layer, &L, sizeof(LayerPtrs), hipMemcpyHostToDevice);
-    if (he != hipSuccess) return hip_fail(he, "moe_bind_layer: copying the layer table");
+    const int H = ctx->cfg.hidden, I = ctx->cfg.inter, E = ctx->cfg.n_experts;
+    hipError_t he;
+    {
+        const size_t es = 3 * mat;
+        uint8_t *base = ctx->spk + (size_t)layer * (E + 1) * es;
+        he = launch_repack_split(L.w1, L.s1, L.sw1, base, es, E, I, H, nullptr);
+        if (he == hipSuccess) he = launch_repack_split(L.w3, L.s3, L.sw3, base + mat, es, E, I, H, nullptr);
+        if (he == hipSuccess) he = launch_repack_split(L.w2, L.s2, L.sw2, base + 2 * mat, es, E, H, I, nullptr);
+        if (he == hipSuccess) he = hipDeviceSynchronize();
+        if (he != hipSuccess) return hip_fail(he, "moe_bind_layer: repacking for the decode stack");
+        LayerPtrs S;
+        S.w1 = base;
+        S.w3 = base + mat;
+        S.w2 = base + 2 * mat;
+        S.s1 = S.s3 = S.s2 = es;
+        S.sw1 = base + (size_t)E * es;
+        S.sw3 = S.sw1 + mat;
+        S.sw2 = S.sw1 + 2 * mat;
+        he = hipMemcpy(ctx->dlayers + layer, &S, sizeof(LayerPtrs), hipMemcpyHostToDevice);
+        if (he != hipSuccess) return hip_fail(he, "moe_bind_layer: copying the layer table");
+    }
     if (ctx->rpk) {
-        const int H = ctx->cfg.hidden, I = ctx->cfg.inter, E = ctx->cfg.n_experts;
         const size_t es = 3 * mat;
         uint8_t *base = ctx->rpk + (size_t)layer * (E + 1) * es;
         he = launch_repack_r16(L.w1, L.s1, L.sw1, base, es, E, I, H, nullptr);

@@ -113,6 +113,10 @@ struct TimedLaunch {
 hipError_t launch_dequant(const void *blocks, uint64_t n_sb, float *out, hipStream_t st);
 hipError_t launch_repack_r16(const void *src, uint64_t src_stride, const void *shared, void *dst, uint64_t dst_stride,
                              int E, int rows, int cols, hipStream_t st);
+// Decode-stack copy of a layer: per matrix, the 128-byte qs of every super-block, then its
+// 8-byte headers, same order (k_repack_split).
+hipError_t launch_repack_split(const void *src, uint64_t src_stride, const void *shared, void *dst,
+                               uint64_t dst_stride, int E, int rows, int cols, hipStream_t st);
 hipError_t launch_gen_iq4xs(void *dst, uint64_t n, uint64_t seed, uint64_t first, hipStream_t st);
 hipError_t launch_gen_normal(float *dst, uint64_t n, uint64_t seed, uint64_t first, float mean,
                              float stdv, hipStream_t st);
