@@ -82,13 +82,18 @@ typedef struct {
 } moe_layer_weights;
 
 /* Create a context on HIP device `device`: validates the shape, allocates every
- * workspace for m_max tokens (nothing is allocated later).
+ * workspace for m_max tokens and the device copies of the weights that moe_bind_layer
+ * fills (nothing is allocated later): a decode-stack layout of every layer, and for
+ * m_max > MOE_DECODE_MAX_M a prefill layout -- each n_layers x (E+1) x 3 matrices.
  * Replaces the MoE slice of InferenceEngine::new (src/inference.rs:85-126) and the
  * scratch / routing regions of ArenaLayout::compute (src/memory.rs:32-96). */
 moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out);
 moe_status moe_destroy(moe_ctx *ctx);
 
-/* Record one layer's weight table (device pointers, not copied).
+/* Record one layer's weight table (device pointers; the single-layer decode path reads
+ * them in place) and copy the layer into the context's decode-stack layout and, for a
+ * prefill context, its prefill layout (same bytes, rearranged).  Synchronises the device;
+ * rebinding a layer replaces its copies.
  * Replaces LayerWeights::from_registry (src/memory.rs:227-291). */
 moe_status moe_bind_layer(moe_ctx *ctx, int layer, const moe_layer_weights *lw);
 
