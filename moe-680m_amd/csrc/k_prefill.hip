@@ -407,24 +407,37 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
             store_a(HALF, PER);
         });
 
-        // epilogue: h = silu(g) * u with the token scale undone; per-row max|h| of the block
+        // epilogue: h = silu(g) * u with the token scale undone; per-row max|h| of the block,
+        // then h as f16 scaled by the power of two that puts that max in [2^14, 2^15), stored
+        // in the down kernel's K order (perm32_pos inside every 32-column block)
+        float hv[MT][4];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int m = 16 * mt + 4 * g + i;
-                float hv = 0.0f;
+                hv[mt][i] = 0.0f;
                 if (m < nrows) {
                     const float inv = s_inv[m];
-                    hv = silu(acc[mt][0][i] * inv) * (acc[mt][1][i] * inv);
-                    a.hf[(size_t)(row0 + m) * I + c0 + n] = hv;
+                    hv[mt][i] = silu(acc[mt][0][i] * inv) * (acc[mt][1][i] * inv);
                 }
-                const float rm = max16(fabsf(hv));
+                const float rm = max16(fabsf(hv[mt][i]));
                 if (n == 0) atomicMax(&rowmax[m], __builtin_bit_cast(uint32_t, rm));
             }
+        lds_barrier();
+        const int col = c0 + n, hcol = (col & ~31) + perm32_pos(col & 31);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = 16 * mt + 4 * g + i;
+                if (m < nrows) {
+                    float unused;
+                    const float sc = pow2_scale(__builtin_bit_cast(float, rowmax[m]), &unused);
+                    a.hh[(size_t)(row0 + m) * I + hcol] = (_Float16)(hv[mt][i] * sc);
+                }
+            }
     });
-    // LDS only: a __syncthreads here would also wait for the h stores to complete
-    lds_barrier();
     if (tid < nrows) a.hmax[(size_t)(row0 + tid) * (I / PF_NGU) + blockIdx.x] = __builtin_bit_cast(float, rowmax[tid]);
 }
 
@@ -453,10 +466,13 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
         constexpr int MT = decltype(MTc)::value;
         constexpr int LK = pf_ldsr<NCH, MT>();
         // A: 16*MT rows x BPR 32-blocks; a thread takes blocks tid, tid + 512, ... -- each one
-        // 32 f32 of h, scaled by a power of two from the row's max into 32 f16 in the weights'
-        // K order.  All loads (h and the row's max blocks) are issued before any is used.
+        // 32 f16 of h, already in the weights' K order and scaled by its 128-column block's
+        // power of two; rescaled here to the power of two of the row's max (a factor 2^-j,
+        // exact for normal f16).  All loads (h and the row's max blocks) are issued before any
+        // is used.
         constexpr int NIT = 16 * MT * BPR, IPT = (NIT + 64 * PF_WAVES - 1) / (64 * PF_WAVES);
-        f32x4 hv[IPT][8];
+        static_assert(PF_NGU % 32 == 0, "max blocks of whole 32-blocks");
+        u32x4 hq[IPT][4];
         float hm[IPT][NHB];
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
@@ -464,9 +480,9 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
             if (IPT * 64 * PF_WAVES == NIT || it < NIT) {
                 const int ar = it / BPR, ab = it % BPR;
                 const int slot = row0 + (ar < nrows ? ar : nrows - 1);
-                const f32x4 *src = reinterpret_cast<const f32x4 *>(a.hf + (size_t)slot * I + 32 * ab);
+                const u32x4 *src = reinterpret_cast<const u32x4 *>(a.hh + (size_t)slot * I + 32 * ab);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) hv[j][i] = ldg<f32x4>(src + i);
+                for (int i = 0; i < 4; ++i) hq[j][i] = ldg<u32x4>(src + i);
 #pragma unroll
                 for (int b = 0; b < NHB; ++b) hm[j][b] = a.hmax[(size_t)slot * NHB + b];
             }
@@ -482,19 +498,21 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
                 float mx = 0.f;
 #pragma unroll
                 for (int b = 0; b < NHB; ++b) mx = fmaxf(mx, hm[j][b]);
-                float inv;
+                float inv, inv_b;
                 const float sc = pow2_scale(ar < nrows ? mx : 0.0f, &inv);
+                (void)pow2_scale(hm[j][ab / (PF_NGU / 32)], &inv_b);
                 if (ab == 0) s_inv[ar] = inv;
-                u32x4 o[4];
-#pragma unroll
-                for (int p = 0; p < 16; ++p) {
-                    const int gg = (2 * p) >> 3, jj = (2 * p) & 7;
-                    const int k0 = jj < 4 ? 4 * gg + jj : 16 + 4 * gg + (jj - 4);
-                    o[p >> 2][p & 3] = pack_f16x2(hv[j][k0 >> 2][k0 & 3] * sc, hv[j][(k0 + 1) >> 2][(k0 + 1) & 3] * sc);
-                }
+                const _Float16 f = (_Float16)(sc * inv_b); // 2^-j, j >= 0 for a real row
+                const f16x2 f2 = {f, f};
                 u32x4 *d = reinterpret_cast<u32x4 *>(As + ar * LK + 32 * ab);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) d[i] = o[i];
+                for (int i = 0; i < 4; ++i) {
+                    const u32x4 q4 = hq[j][i];
+                    u32x4 o;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) o[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, (uint32_t)q4[e]) * f2);
+                    d[i] = o;
+                }
             }
         }
         lds_barrier();

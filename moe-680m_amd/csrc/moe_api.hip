@@ -30,7 +30,7 @@ struct moe_ctx {
     float *hbuf = nullptr;       // decode h: [8][9][I] f32
     _Float16 *xh = nullptr;      // [m_max][H]
     float *xinv = nullptr;       // [m_max]
-    float *hf = nullptr;         // [9 m_max][I]
+    _Float16 *hh = nullptr;      // [9 m_max][I]
     float *hmax = nullptr;       // [9 m_max][I/128]
     float *part = nullptr;       // [9 m_max][H]
     uint32_t *ranges = nullptr;  // [E+2]
@@ -138,7 +138,7 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
         {(void **)&c->hbuf, (size_t)MOE_DECODE_MAX_M * SLOTS * I * sizeof(float)},
         {(void **)&c->xh, mm * H * 2},
         {(void **)&c->xinv, mm * 4},
-        {(void **)&c->hf, SLOTS * mm * I * 4},
+        {(void **)&c->hh, SLOTS * mm * I * 2},
         {(void **)&c->hmax, SLOTS * mm * (I / 128) * 4},
         {(void **)&c->part, SLOTS * mm * H * sizeof(float)},
         {(void **)&c->ranges, (E1 + 1) * 4},
@@ -388,7 +388,7 @@ moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids,
     p.sorted_w = ctx->sw;
     p.pos = ctx->pos;
     p.tiles = ctx->tiles;
-    p.hf = ctx->hf;
+    p.hh = ctx->hh;
     p.hmax = ctx->hmax;
     p.part = ctx->part;
     p.y = y;

@@ -52,7 +52,9 @@ struct PrefillArgs {
     const float *sorted_w;
     const uint32_t *pos; // [M][9]
     const Tile *tiles;
-    float *hf;           // [9M][I] f32 h = silu(g) * u, sorted slot order
+    _Float16 *hh;        // [9M][I] h = silu(g) * u as f16, sorted slot order: each 128-column
+                         // block scaled by the power of two of its max (hmax), K order of the
+                         // down kernel's A (perm32_pos inside 32-column blocks)
     float *hmax;         // [9M][I/128] max |h| per row and 128-column block
     float *part;         // [9M][H] f32, c*w-scaled expert outputs, sorted slot order
     float *y;
