@@ -67,8 +67,10 @@ __host__ __device__ inline int bucket_cw(int E1) {
     int cw = BF_BITMAP_BYTES / (E1 * 8);
     return cw > 16 ? 16 : (cw < 1 ? 1 : cw);
 }
-__host__ inline size_t bucket_smem(int E1) {
-    return (size_t)bucket_cw(E1) * E1 * 8 + 5 * (size_t)(E1 + 1) * 4;
+// KEEP: every chunk has its own bitmap set (M <= 64 * bucket_cw): phase 1's bitmaps serve
+// phase 3 as they are, and the chunk counts stay in LDS.
+__host__ inline size_t bucket_smem(int E1, bool keep) {
+    return (size_t)bucket_cw(E1) * E1 * (keep ? 12 : 8) + 5 * (size_t)(E1 + 1) * 4;
 }
 
 // Inclusive scan over the wave by DPP: shifts of 1-3 lanes of the original values, then 4 and
@@ -89,6 +91,7 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
     return s;
 }
 
+template <bool KEEP>
 __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
     extern __shared__ uint32_t smem[];
     __shared__ uint32_t s_flags;
@@ -97,7 +100,9 @@ __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
     const int nch = (M + 63) / 64;
     const int CW = bucket_cw(E1);
     uint32_t *bm_all = smem;
-    uint32_t *tot = smem + (size_t)CW * E1 * 2;
+    // chunk counts [nch][E1]: in LDS after the bitmaps when KEEP, else in global memory
+    uint32_t *cnt = KEEP ? smem + (size_t)CW * E1 * 2 : a.chunk_cnt;
+    uint32_t *tot = smem + (size_t)CW * E1 * (KEEP ? 3 : 2);
     uint32_t *rg = tot + (E1 + 1);  // bucket starts
     uint32_t *ts = rg + (E1 + 1);   // first full big tile of each bucket
     uint32_t *tp = ts + (E1 + 1);   // partial big tile index (after all full ones)
@@ -109,6 +114,7 @@ __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
     // pass keeps its tokens' ids in registers for phase 3.
     uint32_t idk[SLOTS];
     float wk[SLOTS];
+    uint32_t okk = 0; // KEEP: bit s = slot s is its token's first naming of the expert
     uint32_t *bm = bm_all + (size_t)(wv < CW ? wv : 0) * E1 * 2;
     const uint32_t bit = 1u << (lane & 31);
 
@@ -133,11 +139,12 @@ __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
                     if (e >= (uint32_t)E1) { f |= MOE_DEVFLAG_BAD_ID; continue; }
                     const uint32_t old = atomicOr(&bm[2 * e + (lane >> 5)], bit);
                     if (old & bit) f |= MOE_DEVFLAG_DUP_ID;
+                    else okk |= 1u << s;
                 }
             }
             if (f) atomicOr(&s_flags, f);
             for (int e = lane; e < E1; e += 64)
-                a.chunk_cnt[(size_t)c * E1 + e] = __popc(bm[2 * e]) + __popc(bm[2 * e + 1]);
+                cnt[(size_t)c * E1 + e] = __popc(bm[2 * e]) + __popc(bm[2 * e + 1]);
         }
     }
     __syncthreads();
@@ -149,11 +156,11 @@ __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
         for (int c0 = 0; c0 < nch; c0 += 16) {
             uint32_t v[16];
 #pragma unroll
-            for (int j = 0; j < 16; ++j) v[j] = c0 + j < nch ? a.chunk_cnt[(size_t)(c0 + j) * E1 + e] : 0u;
+            for (int j = 0; j < 16; ++j) v[j] = c0 + j < nch ? cnt[(size_t)(c0 + j) * E1 + e] : 0u;
 #pragma unroll
             for (int j = 0; j < 16; ++j)
                 if (c0 + j < nch) {
-                    a.chunk_cnt[(size_t)(c0 + j) * E1 + e] = run;
+                    cnt[(size_t)(c0 + j) * E1 + e] = run;
                     run += v[j];
                 }
         }
@@ -201,23 +208,25 @@ __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
         for (int i = (int)tsm[E1] + tid; i < a.stile_max; i += BF_THREADS) small[i] = Tile{-1, 0, 0, 0};
     }
 
-    // Phase 3: rebuild each chunk's bitmaps and scatter.
+    // Phase 3: each chunk's bitmaps (kept from phase 1, or rebuilt) and the scatter.
     for (int base = 0; base < nch; base += CW) {
         const int c = base + wv;
         if (wv < CW && c < nch) {
-            for (int i = lane; i < 2 * E1; i += 64) bm[i] = 0;
+            if (!KEEP)
+                for (int i = lane; i < 2 * E1; i += 64) bm[i] = 0;
             const int t = c * 64 + lane;
-            uint32_t ok = 0;
+            uint32_t ok = KEEP ? okk : 0u;
             uint32_t e9[SLOTS];
             if (t < M) {
 #pragma unroll
                 for (int s = 0; s < SLOTS; ++s) e9[s] = base == 0 ? idk[s] : (uint32_t)a.ids[(size_t)t * SLOTS + s];
+                if (!KEEP)
 #pragma unroll
-                for (int s = 0; s < SLOTS; ++s) {
-                    if (e9[s] >= (uint32_t)E1) continue;
-                    const uint32_t old = atomicOr(&bm[2 * e9[s] + (lane >> 5)], bit);
-                    if (!(old & bit)) ok |= 1u << s;
-                }
+                    for (int s = 0; s < SLOTS; ++s) {
+                        if (e9[s] >= (uint32_t)E1) continue;
+                        const uint32_t old = atomicOr(&bm[2 * e9[s] + (lane >> 5)], bit);
+                        if (!(old & bit)) ok |= 1u << s;
+                    }
                 const uint32_t below = bit - 1u;
 #pragma unroll
                 for (int s = 0; s < SLOTS; ++s) {
@@ -226,7 +235,7 @@ __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
                         const uint32_t e = e9[s];
                         const uint32_t rank = __popc(bm[2 * e + (lane >> 5)] & below) +
                                               ((lane >> 5) ? __popc(bm[2 * e]) : 0u);
-                        p = rg[e] + a.chunk_cnt[(size_t)c * E1 + e] + rank;
+                        p = rg[e] + cnt[(size_t)c * E1 + e] + rank;
                         a.sorted_tok[p] = (uint16_t)t;
                         a.sorted_w[p] = base == 0 ? wk[s] : a.w[(size_t)t * SLOTS + s];
                     }
@@ -241,10 +250,12 @@ __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
 
 hipError_t launch_bucket_fill(const BucketArgs &a, hipStream_t st, KernelTimer *T) {
     if (a.M < 0) return hipSuccess; // M == 0 still writes all-zero ranges
-    size_t smem = bucket_smem(a.E1);
+    const bool keep = (a.M + 63) / 64 <= bucket_cw(a.E1);
+    const size_t smem = bucket_smem(a.E1, keep);
     {
         TimedLaunch tl(T, MOE_K_BUCKET_FILL, st);
-        hipLaunchKernelGGL(k_bucket_fill, dim3(1), dim3(BF_THREADS), smem, st, a);
+        if (keep) hipLaunchKernelGGL(k_bucket_fill<true>, dim3(1), dim3(BF_THREADS), smem, st, a);
+        else hipLaunchKernelGGL(k_bucket_fill<false>, dim3(1), dim3(BF_THREADS), smem, st, a);
     }
     return hipGetLastError();
 }
