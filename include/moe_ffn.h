@@ -161,7 +161,7 @@ enum {
     MOE_K_BUCKET_FILL = 1,
     MOE_K_DECODE_GATE_UP = 2,
     MOE_K_DECODE_DOWN = 3,
-    MOE_K_PREFILL_PREP = 4,
+    MOE_K_PREFILL_PREP = 4,          /* no longer launched: moe_ffn's prep runs in its BUCKET_FILL launch */
     MOE_K_PREFILL_GATE_UP = 5,
     MOE_K_PREFILL_DOWN = 6,
     MOE_K_PREFILL_COMBINE = 7,

@@ -35,6 +35,7 @@
 // v_perm places each byte under an 0x64 high byte, which is the f16 1024 + byte, exactly;
 // one packed f16 add of -1152 gives kv exactly and one packed multiply applies dl.
 #include "moe_internal.hpp"
+#include "bucket_fill.hpp"
 
 namespace moe {
 
@@ -115,15 +116,10 @@ __device__ __forceinline__ float max16(float v) {
 }
 
 // ---------------------------------------------------------------- prep
-// One wave per token (and per workgroup, so the tokens spread over every CU); lane owns
-// 32-blocks lane, lane+64, ... of the row.
+// One wave per token; lane owns 32-blocks lane, lane+64, ... of the row.
 template <int H>
-__global__ __launch_bounds__(64) void k_pf_prep(PrefillArgs a) {
+__device__ __forceinline__ void prep_token(const PrefillArgs &a, int t, int lane) {
     constexpr int NB = H / 32 / 64 > 0 ? H / 32 / 64 : 1; // 32-blocks per lane
-    static_assert(H % (32 * 64) == 0 || H == 512, "prep shape");
-    const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x;
-    if (t >= a.M) return;
     constexpr int NBK = H / 32;
     float v[NB][32];
     const bool own = lane < NBK;
@@ -172,6 +168,20 @@ __global__ __launch_bounds__(64) void k_pf_prep(PrefillArgs a) {
         }
     }
     if (lane == 0) a.xinv[t] = inv_s;
+}
+
+// The chain's first launch: workgroup 0 runs the bucket fill (one CU, latency-bound), the
+// others the prep of 16 tokens each (one wave per token) -- independent work that would
+// otherwise be two launches in a row.
+template <int H, bool KEEP>
+__global__ __launch_bounds__(BF_THREADS) void k_pf_route_prep(BucketArgs b, PrefillArgs a) {
+    static_assert(H % (32 * 64) == 0 || H == 512, "prep shape");
+    if (blockIdx.x == 0) {
+        bucket_fill_body<KEEP>(b);
+        return;
+    }
+    const int t = (blockIdx.x - 1) * (BF_THREADS / 64) + (int)(threadIdx.x >> 6);
+    if (t < a.M) prep_token<H>(a, t, threadIdx.x & 63); // whole waves
 }
 
 // ---------------------------------------------------------------- shared pipeline pieces
@@ -561,10 +571,14 @@ __global__ __launch_bounds__(256) void k_pf_combine(PrefillArgs a) {
 }
 
 template <int H, int I>
-static hipError_t launch_prefill_t(const PrefillArgs &a, hipStream_t st, KernelTimer *T) {
+static hipError_t launch_prefill_t(const BucketArgs &b, const PrefillArgs &a, hipStream_t st, KernelTimer *T) {
     {
-        TimedLaunch tl(T, MOE_K_PREFILL_PREP, st);
-        hipLaunchKernelGGL((k_pf_prep<H>), dim3(a.M), dim3(64), 0, st, a);
+        TimedLaunch tl(T, MOE_K_BUCKET_FILL, st);
+        const bool keep = (b.M + 63) / 64 <= bucket_cw(b.E1);
+        const dim3 grid((unsigned)(1 + (a.M + BF_THREADS / 64 - 1) / (BF_THREADS / 64)));
+        const size_t smem = bucket_smem(b.E1, keep);
+        if (keep) hipLaunchKernelGGL((k_pf_route_prep<H, true>), grid, dim3(BF_THREADS), smem, st, b, a);
+        else hipLaunchKernelGGL((k_pf_route_prep<H, false>), grid, dim3(BF_THREADS), smem, st, b, a);
     }
     // one launch over both tile lists (full and big remainder tiles, then small remainders)
     const int ntiles = a.tile_max + a.stile_max;
@@ -583,9 +597,9 @@ static hipError_t launch_prefill_t(const PrefillArgs &a, hipStream_t st, KernelT
     return hipGetLastError();
 }
 
-hipError_t launch_prefill(int H, int I, const PrefillArgs &a, hipStream_t st, KernelTimer *T) {
-    if (H == 2048 && I == 512) return launch_prefill_t<2048, 512>(a, st, T);
-    if (H == 512 && I == 256) return launch_prefill_t<512, 256>(a, st, T);
+hipError_t launch_prefill(int H, int I, const BucketArgs &b, const PrefillArgs &a, hipStream_t st, KernelTimer *T) {
+    if (H == 2048 && I == 512) return launch_prefill_t<2048, 512>(b, a, st, T);
+    if (H == 512 && I == 256) return launch_prefill_t<512, 256>(b, a, st, T);
     return hipErrorInvalidValue;
 }
 

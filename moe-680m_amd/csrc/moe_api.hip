@@ -377,8 +377,6 @@ moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids,
     b.stile_max = stile_max_for(E + 1);
     b.flags = ctx->flags;
     KernelTimer *T = timer_for(ctx, st);
-    he = launch_bucket_fill(b, st, T);
-    if (he != hipSuccess) return hip_fail(he, "moe_ffn: bucket fill launch");
     PrefillArgs p{};
     p.L = ctx->rlayers[layer];
     p.x = x;
@@ -399,7 +397,7 @@ moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids,
     p.tile_max = b.tile_max;
     p.stile_max = b.stile_max;
     p.c = c;
-    he = launch_prefill(H, I, p, st, T);
+    he = launch_prefill(H, I, b, p, st, T);
     if (he != hipSuccess) return hip_fail(he, "moe_ffn: prefill launch");
     return ok();
 }

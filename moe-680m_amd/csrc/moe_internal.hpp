@@ -129,7 +129,8 @@ hipError_t launch_router_topk(const float *logits, int M, int E, int renorm, uin
 hipError_t launch_bucket_fill(const BucketArgs &a, hipStream_t st, KernelTimer *T);
 hipError_t launch_decode(int H, int I, const DecodeArgs &a, hipStream_t st, KernelTimer *T);
 // prep, one gate/up and one down launch over both tile lists, combine -- all on st.
-hipError_t launch_prefill(int H, int I, const PrefillArgs &a, hipStream_t st, KernelTimer *T);
+// Bucket fill and prep (one launch), gate/up, down, combine.
+hipError_t launch_prefill(int H, int I, const BucketArgs &b, const PrefillArgs &a, hipStream_t st, KernelTimer *T);
 hipError_t launch_stack(int H, int I, const StackArgs &a, hipStream_t st, KernelTimer *T);
 hipError_t stack_occupancy(int H, int I, int *blocks_per_cu);
 int stack_blocks(int H);

@@ -191,8 +191,10 @@ def test_kernel_timing_hook(gpu, full):
     ctx.ffn(0, xp, idp, wp)
     t = ctx.timing_read()
     assert t["router_topk"][0] == 2 and t["decode_gate_up"][0] == 1 and t["decode_down"][0] == 1
-    for k in ("bucket_fill", "prefill_prep", "prefill_gate_up", "prefill_down", "prefill_combine"):
+    # the prefill chain: bucket fill and prep in one launch, then gate/up, down, combine
+    for k in ("bucket_fill", "prefill_gate_up", "prefill_down", "prefill_combine"):
         assert t[k][0] == 1 and t[k][1] > 0
+    assert "prefill_prep" not in t
     assert ctx.timing_read() == {}
     ctx.timing_enable(0)
     ctx.ffn(0, x, ids, w)
