@@ -533,19 +533,31 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
             for (int t = 0; t < NTW; ++t) acc[i][t] = f32x4{0, 0, 0, 0};
         gemm_resident<NCH, RD, NTW, MT>(ws, rows, As, n, g, acc, [](int) {});
 
+        // epilogue: the scaled results through LDS (As is free once every wave is done with
+        // it), so that each lane stores whole 16-byte row pieces -- 8 store instructions per
+        // wave for 64 rows instead of 32 four-byte ones
+        static_assert(PF_WAVES * PF_BM * 32 * 4 <= PF_AS_HALVES * 2, "transpose fits in As");
+        lds_barrier();
+        float *T = reinterpret_cast<float *>(As) + wv * (16 * MT * 32); // [16 MT rows][32 columns]
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int m = 16 * mt + 4 * g + i;
-                if (m < nrows) {
-                    const int slot = row0 + m;
-                    const float sc = a.c * a.sorted_w[slot] * s_inv[m];
-                    float *prow = a.part + (size_t)slot * H + r0 + n;
+                const float sc = m < nrows ? a.c * a.sorted_w[row0 + m] * s_inv[m] : 0.0f;
 #pragma unroll
-                    for (int t = 0; t < NTW; ++t) prow[16 * t] = sc * acc[mt][t][i];
-                }
+                for (int t = 0; t < NTW; ++t) T[m * 32 + 16 * t + n] = sc * acc[mt][t][i];
             }
+        // lanes read what other lanes of this wave wrote: LDS keeps a wave's accesses in
+        // order, the compiler must too
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int k = lane; k < 16 * MT * 8; k += 64) {
+            const int r = k >> 3, q = k & 7;
+            if (r < nrows)
+                *reinterpret_cast<f32x4 *>(a.part + (size_t)(row0 + r) * H + r0 + 4 * q) =
+                    *reinterpret_cast<const f32x4 *>(T + r * 32 + 4 * q);
+        }
     });
 }
 
