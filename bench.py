@@ -100,6 +100,8 @@ def main():
     ap.add_argument("--prefill-steps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra-configs", action="store_true",
+                    help="skip the config 3 (M=2,4,8 single layer) and config 4 (M=4096) legs")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="run a plain device copy of this size first (scales PMC byte counters)")
     args = ap.parse_args()
@@ -256,6 +258,86 @@ def main():
     pgu_us = pkern["prefill_gate_up"]["avg_us"]
     pgu_tflops = (PREFILL_FLOPS * 2 / 3) / (pgu_us * 1e-6) / 1e12
 
+    # ---------------------------------------------------------------- configs 3 and 4
+    extra = {}
+    if not args.no_extra_configs:
+        # config 3: one layer, M = 2, 4, 8 tokens with independent activations and logits;
+        # algorithmic bytes = the distinct experts the step selects + the tokens' x, logits, y
+        c3 = {}
+        for Mv in (2, 4, 8):
+            n3 = 3 + 30
+            x3 = pkg.gen_normal(Mv * H, pkg.seed_for(3, Mv, pkg.TAG_X)).view(Mv, H)
+            y3 = torch.empty_like(x3)
+            l3 = pkg.gen_logits(n3 * Mv, E, pkg.seed_for(3, Mv, pkg.TAG_L)).view(n3, Mv, E)
+            i3 = torch.empty((n3, Mv, 9), dtype=torch.uint16, device=dev)
+            w3 = torch.empty((n3, Mv, 9), dtype=torch.float32, device=dev)
+
+            def step3(s, Mv=Mv, x3=x3, y3=y3, l3=l3, i3=i3, w3=w3):
+                ctx.router_topk(l3[s], i3[s], w3[s])
+                ctx.ffn(s % LAYERS, x3, i3[s], w3[s], y=y3)
+
+            step3(0)
+            torch.cuda.synchronize()
+            g3 = [capture(torch, lambda s=s, f=step3: f(s)) for s in range(n3)]
+            for s in range(3):
+                g3[s].replay()
+            torch.cuda.synchronize()
+            ev0.record()
+            for s in range(3, n3):
+                g3[s].replay()
+            ev1.record()
+            torch.cuda.synchronize()
+            us3 = ev0.elapsed_time(ev1) * 1e3 / (n3 - 3)
+            nexp = [int(torch.unique(i3[s].view(-1).to(torch.int32)).numel()) for s in range(3, n3)]
+            b3 = sum(nexp) / len(nexp) * EXPERT_BYTES + Mv * (H * 4 + E * 4 + H * 4)
+            gbs3 = b3 / (us3 * 1e-6) / 1e9
+            c3[f"M{Mv}"] = {"us_per_step": round(us3, 2), "distinct_experts": round(sum(nexp) / len(nexp), 1),
+                            "bytes_per_step": int(b3), "gbs": round(gbs3, 1),
+                            "hbm_peak_frac": round(gbs3 / HBM_PEAK_GBS, 4)}
+            log(f"config 3, M={Mv}: {us3:.1f} us/step (router + moe_ffn), {gbs3:.0f} GB/s = "
+                f"{100 * gbs3 / HBM_PEAK_GBS:.1f}% of HBM peak; {c3[f'M{Mv}']['distinct_experts']} experts")
+            del g3
+        extra["config3"] = {"workload": "config 3: one layer, M in {2, 4, 8}, independent N(0,1) x and "
+                                        "logits per token; router + moe_ffn per step, graph replays",
+                            **c3}
+        # config 4: M = 4096, N(0,1) logits with 5% of the tokens forced onto one hot expert
+        M4 = 4096
+        ctx4 = pkg.Context(H, I, E, 1, M4, pkg.W_REF)
+        ctx4.bind_packed(0, layers[0])
+        n4 = 2 + 6
+        x4 = pkg.gen_normal(M4 * H, pkg.seed_for(4, 0, pkg.TAG_X)).view(M4, H)
+        y4 = torch.empty_like(x4)
+        l4 = pkg.gen_logits(n4 * M4, E, pkg.seed_for(4, 0, pkg.TAG_L), 2, 0.05, 1000.0).view(n4, M4, E)
+        i4 = torch.empty((n4, M4, 9), dtype=torch.uint16, device=dev)
+        w4 = torch.empty((n4, M4, 9), dtype=torch.float32, device=dev)
+
+        def step4(s):
+            ctx4.router_topk(l4[s], i4[s], w4[s])
+            ctx4.ffn(0, x4, i4[s], w4[s], y=y4)
+
+        step4(0)
+        torch.cuda.synchronize()
+        g4 = [capture(torch, lambda s=s: step4(s)) for s in range(n4)]
+        for s in range(2):
+            g4[s].replay()
+        torch.cuda.synchronize()
+        ev0.record()
+        for s in range(2, n4):
+            g4[s].replay()
+        ev1.record()
+        torch.cuda.synchronize()
+        us4 = ev0.elapsed_time(ev1) * 1e3 / (n4 - 2)
+        fl4 = 2 * (9 * M4) * 3 * I * H
+        tf4 = fl4 / (us4 * 1e-6) / 1e12
+        log(f"config 4, M={M4}: {us4:.1f} us/step, {M4 / (us4 * 1e-6):.0f} tok/s, {tf4:.1f} TFLOP/s = "
+            f"{100 * tf4 / BF16_PEAK_TFLOPS:.2f}% of the f16/bf16 MFMA peak")
+        del g4
+        ctx4.close()
+        extra["config4"] = {"workload": "config 4: one layer, M=4096, N(0,1) logits with 5% of tokens "
+                                        "forced onto one hot expert; router + moe_ffn per step",
+                            "us_per_step": round(us4, 1), "tok_per_s": round(M4 / (us4 * 1e-6), 1),
+                            "tflops": round(tf4, 2), "mfma_frac": round(tf4 / BF16_PEAK_TFLOPS, 4)}
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(pkg, layers[0], args.cpu_seconds)
@@ -302,6 +384,7 @@ def main():
                                  "unit": "TFLOP/s", "frac": round(pgu_tflops / BF16_PEAK_TFLOPS, 4),
                                  "avg_us": pgu_us},
                     "kernels": pkern},
+        **extra,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
