@@ -5,9 +5,9 @@
 // shaders/w2_scatter_m1.comp), 18 dispatches and 18 barriers per layer, with SiLU fused
 // into the down projection and the combine done as an f16 read-modify-write of the
 // hidden state.  Here one layer is two launches:
-//   gate_up: every (expert, W1/W3 row pair) of the 9 selected experts, SiLU*up fused,
+//   gate_up: every (token, slot, W1/W3 row pair) of the selected experts, SiLU*up fused,
 //            RMSNorm of the input fused (each wave holds the whole activation row);
-//   down:    one workgroup per 8 output rows with one wave per slot, the 9 weighted
+//   down:    one workgroup per 16 or 32 output rows with one wave per slot, the 9 weighted
 //            contributions summed in slot order in LDS (deterministic, no atomics) and
 //            the residual added in the same store.
 // Lane mapping: a lane owns one 32-weight sub-block of a row (8-byte header load +
@@ -53,14 +53,10 @@ __global__ __launch_bounds__(256) void k_decode_gate_up(DecodeArgs a) {
         h3[r] = ldg<u32x2>(W3 + off);
         q3[r] = ldg<u32x4>(W3 + off + 8 + 16 * ib);
     }
-    // With several tokens, the first token naming expert e serves every later token that
-    // names it, so each selected expert's rows are fetched once for all tokens.
-    if (a.M > 1) {
-        bool seen = false;
-        for (int p = lane; p < t0 * SLOTS; p += 64) seen |= (a.ids[p] == e);
-        if (__any(seen)) return;
-    }
-
+    // Every (token, slot) item runs on its own, also when several tokens name the same
+    // expert: the repeated row reads are L2 hits, and one item serving all later tokens
+    // serialised their work (at M = 8 the shared expert's items did eight tokens each:
+    // 42 against 26 us for this kernel).
     auto run = [&](float(&xr)[32], int p) {
         if (a.rmsnorm) {
             float ss = 0.f;
@@ -84,16 +80,6 @@ __global__ __launch_bounds__(256) void k_decode_gate_up(DecodeArgs a) {
         }
     };
     run(xv, item);
-    for (int p = (t0 + 1) * SLOTS; p < a.M * SLOTS; ++p) {
-        if (a.ids[p] != e) continue;
-        // Keep the weight decode inside this loop: hoisting the decoded floats of all rows
-        // out of it would take ~250 registers and one wave per SIMD.
-#pragma unroll
-        for (int r = 0; r < RP; ++r) asm volatile("" : "+v"(q1[r]), "+v"(q3[r]), "+v"(h1[r]), "+v"(h3[r]));
-        float xt[32];
-        load32(a.x + (size_t)(p / SLOTS) * H + 32 * gsb, xt);
-        run(xt, p);
-    }
 }
 
 template <int H, int I, int STEPS>
@@ -168,14 +154,17 @@ static hipError_t launch_decode_t(const DecodeArgs &a, hipStream_t st, KernelTim
         TimedLaunch tl(T, MOE_K_DECODE_GATE_UP, st);
         hipLaunchKernelGGL((k_decode_gate_up<H, I, RP>), g1, dim3(256), 0, st, a);
     }
-    constexpr int STEPS = 2;
+    // down: 4 row steps per wave up to 4 tokens, 8 beyond (more rows in flight per wave once
+    // there are enough workgroups; measured at M = 2, 4, 8)
     constexpr int LPR2 = (I / QK) * 8;
-    constexpr int RPW2 = (64 / LPR2) * STEPS;
-    static_assert(H % RPW2 == 0, "down grid");
-    dim3 g2(H / RPW2, a.M);
+    constexpr int RPW4 = (64 / LPR2) * 4, RPW8 = (64 / LPR2) * 8;
+    static_assert(H % RPW8 == 0, "down grid");
     {
         TimedLaunch tl(T, MOE_K_DECODE_DOWN, st);
-        hipLaunchKernelGGL((k_decode_down<H, I, STEPS>), g2, dim3(64 * SLOTS), 0, st, a);
+        if (a.M <= 4)
+            hipLaunchKernelGGL((k_decode_down<H, I, 4>), dim3(H / RPW4, a.M), dim3(64 * SLOTS), 0, st, a);
+        else
+            hipLaunchKernelGGL((k_decode_down<H, I, 8>), dim3(H / RPW8, a.M), dim3(64 * SLOTS), 0, st, a);
     }
     return hipGetLastError();
 }
