@@ -6,9 +6,11 @@ Metric: "MoE-FFN decode HBM GB/s (% of peak) @M=1; prefill tok/s
 per layer router softmax/top-8 over seeded logits, RMSNorm + the 9-expert IQ4_XS FFN +
 weighted combine + residual.  All 40 x 257 experts (17.2 GB) are resident in HBM and
 every step routes differently, so weights stream from HBM.  `value` is algorithmic bytes
-(602,316,800 per token) / wall time.  The prefill leg (config 1: M=512, Zipf(1.1)-biased
-router) is reported in the same line, with tok/s and the MFMA fraction (f16 operands; the f16
-and bf16 dense peaks are the same 2.5 PFLOP/s).
+(602,316,800 per token) / wall time of the timed steps (HIP graphs of 8 tokens; the HIP-event
+time is logged beside it).  The prefill leg (config 1: M=512, Zipf(1.1)-biased router) is reported in the
+same line, with tok/s and the MFMA fraction (f16 operands; the f16 and bf16 dense peaks are
+the same 2.5 PFLOP/s), and so are config 3 (one layer at M = 2, 4, 8: GB/s of the distinct
+experts selected) and config 4 (M = 4096: MFMA fraction).
 
     python bench.py [--steps K] [--warmup W]      # one JSON line on stdout
 """
@@ -231,16 +233,20 @@ def main():
 
     prefill(0)
     torch.cuda.synchronize()
-    pgraphs = [capture(torch, lambda s=s: prefill(s)) for s in range(pn)]
-    for s in range(pw):
-        pgraphs[s].replay()
+    # warm-up steps one per graph, timed steps five per graph (so the host's launch rate does
+    # not show in a step), wall time bracketed by synchronisation like the decode leg
+    PG = 5
+    pgraphs = [capture(torch, lambda s=s: prefill(s)) for s in range(pw)]
+    pgraphs += [capture(torch, lambda b=b: [prefill(s) for s in range(b, min(b + PG, pn))])
+                for b in range(pw, pn, PG)]
+    for g in pgraphs[:pw]:
+        g.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for s in range(pw, pn):
-        pgraphs[s].replay()
+    for g in pgraphs[pw:]:
+        g.replay()
     torch.cuda.synchronize()
-    pwall = time.perf_counter() - t0
-    p_ms = pwall * 1e3 / PK
+    p_ms = (time.perf_counter() - t0) * 1e3 / PK
     p_tflops = PREFILL_FLOPS / (p_ms * 1e-3) / 1e12
     active = [int(torch.unique(pids[s].view(-1).to(torch.int32)).numel()) for s in range(pw, pn)]
     log(f"prefill M={PREFILL_M}: {p_ms * 1e3:.1f} us/step, {PREFILL_M / (p_ms * 1e-3):.0f} tok/s, "
