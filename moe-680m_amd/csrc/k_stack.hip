@@ -396,7 +396,9 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         lds_barrier(); // B0
         for (int li = 0; li < n; ++li) {
             lds_barrier(); // B1: x_li in LDS
-            __builtin_amdgcn_s_setprio(0);
+            // the h exchange: ahead of the compute waves' phase-B lookups (priority 0), level
+            // with phase A (priority 1; the older compute waves win the ties)
+            __builtin_amdgcn_s_setprio(1);
             {
                 // h of the XCD: the first poller wave takes the shared rows (lane t: the 16
                 // words of shared row t -- eight waves' partial (g, u) -- combined here), the
