@@ -7,17 +7,21 @@
 // and a list of tiles (up to PF_BM slots of one expert):
 //   prep:    per token, x (RMSNorm fused when asked) times a power of two s_t that puts
 //            max|x| in [2^14, 2^15), stored as f16 with K permuted inside 32-blocks (the
-//            order the weight nibbles arrive in, see below); 1/s_t kept per token;
+//            order the weight nibbles arrive in, see below); 1/s_t kept per token -- run in
+//            the same launch as the bucket fill (k_pf_route_prep), which does not need it;
 //   gate_up: per (tile, 128 gate/up column pairs) a workgroup of 8 waves, two per CU; the
 //            tile's token rows (gathered -- the reference's kernel skipped this gather) are
 //            resident in LDS one 64 KB chunk of K at a time and shared by the 8 waves; every
 //            wave decodes its own 16 W1 rows and 16 W3 rows straight into MFMA B fragments
 //            in registers (no LDS, no barrier for weights) and runs v_mfma_f32_16x16x32_f16;
-//            epilogue: silu(g) * u with the 1/s_t undone, f32 h, plus the per-row max|h|
-//            of each 128-column block;
-//   down:    per (tile, 256 output rows) the same over K = inter (one chunk); the f32 h rows
-//            are scaled per row by a power of two (from the row max) into f16 as they are
-//            staged; epilogue multiplies by 2^-s_row * c * slot weight, one f32 row per slot;
+//            epilogue: silu(g) * u with the 1/s_t undone, the per-row max|h| of each
+//            128-column block, and h as f16 scaled by that max's power of two, stored in the
+//            down kernel's K order;
+//   down:    per (tile, 256 output rows) the same over K = inter (one chunk); each 128-column
+//            block of the f16 h rows is rescaled to the power of two of the row's max (a
+//            factor 2^-j, exact for normal f16) as it is staged; epilogue multiplies by
+//            2^-s_row * c * slot weight and writes one f32 row per slot through LDS (16-byte
+//            pieces per lane);
 //   combine: y_t (+)= sum over t's 9 slots in slot order -- deterministic, no atomics, no
 //            f16 read-modify-write race (the reference's w2_scatter.comp:77-86 RMW).
 //
