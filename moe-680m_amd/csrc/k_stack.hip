@@ -16,7 +16,11 @@
 //     pointers, and every compute wave keeps its weights in flight in registers: layer
 //     l+1's phase-A weights are requested when phase A of l is done, layer l's phase-B
 //     weights when phase A of l starts (so no weight stream competes with the
-//     latency-bound cross-XCD exchange at the end of a layer);
+//     latency-bound cross-XCD exchange at the end of a layer).  The weights are read from
+//     the split copy of each layer (dense qs, then compact headers; k_repack_split) with one
+//     header load per wave and layer, and their codebook lookups are done in the waits --
+//     layer l+1's phase-A weights after B3 of l, layer l's phase-B weights after its
+//     phase A -- so the phases themselves run only the dot products;
 //   - activations move between workgroups through per-layer buffers cleared to zero
 //     before the launch; producers store each f32 with its mantissa LSB forced to 1
 //     (<= 1 ulp), consumers poll exactly the words they need until every word carries the
