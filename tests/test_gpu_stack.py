@@ -157,3 +157,30 @@ def test_stack_errors(gpu, full):
         ctx.decode_stack(39, x, lg)          # runs past the last layer
     with pytest.raises(gpu.MoeError):
         ctx.decode_stack(0, x[1:], lg)       # misaligned
+
+
+def test_rebind_refreshes_copies(gpu, small):
+    """Rebinding a layer rewrites the library's own copies of it (the stack's split layout,
+    the prefill layout): results equal those of a fresh context bound to the new weights."""
+    import torch
+    ctx, layers, (hidden, inter, nexp) = small
+    other = gpu.gen_layer(hidden, inter, nexp, 999)
+    fresh = gpu.Context(hidden, inter, nexp, 6, 16, gpu.W_REF)
+    try:
+        ctx.bind_packed(0, other)
+        fresh.bind_packed(0, other)
+        x = gpu.gen_normal(hidden, 1001)
+        logits = gpu.gen_logits(1, nexp, 1002)
+        a = ctx.decode_stack(0, x, logits).clone()
+        b = fresh.decode_stack(0, x, logits).clone()
+        xp = gpu.gen_normal(12 * hidden, 1003).view(12, hidden)
+        ids, w = ctx.router_topk(gpu.gen_logits(12, nexp, 1004))
+        ya = ctx.ffn(0, xp, ids, w).clone()
+        yb = fresh.ffn(0, xp, ids, w).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+        assert torch.equal(ya.view(torch.int32), yb.view(torch.int32))
+        assert ctx.device_flags() == 0 and fresh.device_flags() == 0
+    finally:
+        ctx.bind_packed(0, layers[0])  # the module's other tests use the original layer 0
+        fresh.close()
