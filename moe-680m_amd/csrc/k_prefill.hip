@@ -9,15 +9,16 @@
 //            max|x| in [2^14, 2^15), stored as f16 with K permuted inside 32-blocks (the
 //            order the weight nibbles arrive in, see below); 1/s_t kept per token -- run in
 //            the same launch as the bucket fill (k_pf_route_prep), which does not need it;
-//   gate_up: per (tile, 128 gate/up column pairs) a workgroup of 8 waves, two per CU; the
-//            tile's token rows (gathered -- the reference's kernel skipped this gather) are
-//            resident in LDS one 64 KB chunk of K at a time and shared by the 8 waves; every
-//            wave decodes its own 16 W1 rows and 16 W3 rows straight into MFMA B fragments
-//            in registers (no LDS, no barrier for weights) and runs v_mfma_f32_16x16x32_f16;
-//            epilogue: silu(g) * u with the 1/s_t undone, the per-row max|h| of each
-//            128-column block, and h as f16 scaled by that max's power of two, stored in the
-//            down kernel's K order;
-//   down:    per (tile, 256 output rows) the same over K = inter (one chunk); each 128-column
+//   gate_up: per (tile, 64 gate/up column pairs; 128 when M > 1024) a workgroup of 8 waves,
+//            two per CU; the tile's token rows (gathered -- the reference's kernel skipped
+//            this gather) are resident in LDS one 64 KB chunk of K at a time and shared by the
+//            8 waves; each wave decodes 16 W1 rows and 16 W3 rows (with 64 columns, two waves
+//            share them and take alternate 128-K stages; their sums meet in LDS) straight
+//            into MFMA B fragments in registers (no LDS, no barrier for weights) and runs
+//            v_mfma_f32_16x16x32_f16; epilogue: silu(g) * u with the 1/s_t undone, the
+//            per-row max|h| of the item's column block, and h as f16 scaled by that max's
+//            power of two, stored in the down kernel's K order;
+//   down:    per (tile, 256 output rows) the same over K = inter (one chunk); each column
 //            block of the f16 h rows is rescaled to the power of two of the row's max (a
 //            factor 2^-j, exact for normal f16) as it is staged; epilogue multiplies by
 //            2^-s_row * c * slot weight and writes one f32 row per slot through LDS (16-byte
@@ -45,7 +46,6 @@ namespace moe {
 
 constexpr int PF_KC = 128;             // K per LDS stage
 constexpr int PF_WAVES = 8;
-constexpr int PF_NGU = 16 * PF_WAVES;  // gate/up columns per workgroup
 constexpr int PF_ND = 32 * PF_WAVES;   // down output rows per workgroup (2 N-tiles per wave)
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -331,6 +331,36 @@ __device__ __forceinline__ void gemm_resident(WStage<NR> (&ws)[RD], const uint8_
     });
 }
 
+// The same K loop with the stages split between two waves: the wave of parity p runs stages
+// 2c + p (half super-block p of super-block c), so each decodes half the weights of its
+// columns; chunk boundaries (KCH even) fall at the same loop index for both.  Half-length
+// work items: gate/up's items then fill the 512 workgroup slots in three rounds of half
+// length instead of two full ones (at M = 512, ~1140 items against ~570 of twice the length).
+template <int NCH, int RD, int NR, int MT, typename StageA>
+__device__ __forceinline__ void gemm_resident_split(WStage<NR> (&ws)[RD], const uint8_t *const (&rows)[NR],
+                                                    const _Float16 *As, int n, int g, int p,
+                                                    f32x4 (&acc)[MT][NR], StageA stage_a) {
+    constexpr int KCH = pf_kch<NCH, MT>();
+    constexpr int LK = pf_ldsr<NCH, MT>();
+    constexpr int NC2 = NCH / 2;
+    static_assert(NCH % KCH == 0 && KCH % 2 == 0 && 16 * MT * LK <= PF_AS_HALVES, "whole chunks of even length");
+    static_for<NC2>([&](auto Cc) __attribute__((always_inline)) {
+        constexpr int c = decltype(Cc)::value, S = c % RD, ch0 = 2 * c;
+        if constexpr (ch0 > 0 && ch0 % KCH == 0) {
+            lds_barrier();
+            stage_a(ch0 / KCH);
+            lds_barrier();
+        }
+        const int ch = ch0 + p;
+        uint32_t dl[NR][4];
+        wstage_dl(ws[S], ch, g, n, dl);
+        stage_mfma<NR, MT, LK>(ws[S], dl, As + (ch0 % KCH + p) * PF_KC, n, g, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (c + RD - 1 < NC2) wstage_load(ws[(c + RD - 1) % RD], rows, 2 * (c + RD - 1) + p, n + 16 * g);
+        __builtin_amdgcn_sched_barrier(0);
+    });
+}
+
 // A tile holds up to PF_BM slots of one expert and runs as 1, 2 or 4 M-tiles of 16 rows (one
 // instantiation each, picked per workgroup, so every inner loop is straight-line code).  Full
 // PF_BM tiles come first in the list, remainders after: the long work items start first and
@@ -347,11 +377,15 @@ __device__ __forceinline__ void by_mtiles(int nrows, F f) {
 }
 
 // ---------------------------------------------------------------- gate/up
-template <int H, int I>
+// SPLIT: PF_NGU columns per item, two waves per 16 columns on alternate stages; else
+// PF_NGU_WIDE columns, one wave per 16 columns on every stage.
+template <int H, int I, bool SPLIT>
 __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) {
+    constexpr int NGU = SPLIT ? PF_NGU : PF_NGU_WIDE;
+    static_assert(NGU == 16 * PF_WAVES / (SPLIT ? 2 : 1), "16 columns per wave (pair)");
     constexpr int NCH = H / PF_KC;
     constexpr int ROWB = (H / QK) * SB_BYTES;
-    static_assert(H % QK == 0 && I % PF_NGU == 0 && PF_KC * 2 == QK, "gate/up shape");
+    static_assert(H % QK == 0 && I % NGU == 0 && PF_KC * 2 == QK, "gate/up shape");
     __shared__ __attribute__((aligned(16))) _Float16 As[PF_AS_HALVES];
     __shared__ uint32_t rowmax[PF_BM];
     __shared__ float s_inv[PF_BM];
@@ -362,7 +396,8 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
     const int e = tl.expert, row0 = tl.row0, nrows = tl.nrows;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int n = lane & 15, g = lane >> 4;
-    const int c0 = blockIdx.x * PF_NGU + wv * 16; // this wave's h columns
+    const int cw = SPLIT ? (wv & 3) : wv, p = SPLIT ? (wv >> 2) : 0; // column group, stage parity
+    const int c0 = blockIdx.x * NGU + cw * 16; // this wave's h columns
     // the tile's tokens and their 1/scale (rows past nrows repeat the last token)
     if (tid < PF_BM) {
         const int t = a.sorted_tok[row0 + (tid < nrows ? tid : nrows - 1)];
@@ -405,7 +440,15 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
         constexpr int RD = 3; // weight ring depth: two stages ahead (register budget)
         WStage<2> ws[RD];
         load_a(0, 0, PER);
-        wring_prologue<NCH, RD>(ws, rows, lane);
+        if constexpr (SPLIT) {
+#pragma unroll
+            for (int c = 0; c < RD - 1; ++c) {
+                if (c < NCH / 2) wstage_load(ws[c], rows, 2 * c + p, lane);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+            wring_prologue<NCH, RD>(ws, rows, lane);
+        }
         store_a(0, PER);
         lds_barrier();
         f32x4 acc[MT][2];
@@ -414,14 +457,36 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
         // later chunks are moved in two halves while the weight ring and the accumulators
         // are live (fewer registers held at once)
         constexpr int HALF = (PER + 1) / 2;
-        gemm_resident<NCH, RD, 2, MT>(ws, rows, As, n, g, acc, [&](int c) __attribute__((always_inline)) {
+        auto stage_a = [&](int c) __attribute__((always_inline)) {
             load_a(c, 0, HALF);
             store_a(0, HALF);
             load_a(c, HALF, PER);
             store_a(HALF, PER);
-        });
+        };
+        if constexpr (SPLIT) {
+            gemm_resident_split<NCH, RD, 2, MT>(ws, rows, As, n, g, p, acc, stage_a);
+            // the odd-stage wave hands its sums to its partner through the (now free) A chunk
+            lds_barrier();
+            f32x4 *red = reinterpret_cast<f32x4 *>(As);
+            static_assert(4 * MT * 2 * 64 * 16 <= PF_AS_HALVES * 2, "the pair sums fit the A chunk");
+            if (p) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) red[((cw * MT + mt) * 2 + r) * 64 + lane] = acc[mt][r];
+            }
+            lds_barrier();
+            if (!p) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) acc[mt][r] += red[((cw * MT + mt) * 2 + r) * 64 + lane];
+            }
+        } else {
+            gemm_resident<NCH, RD, 2, MT>(ws, rows, As, n, g, acc, stage_a);
+        }
 
-        // epilogue: h = silu(g) * u with the token scale undone; per-row max|h| of the block,
+        // epilogue (even-stage waves): h = silu(g) * u with the token scale undone; per-row max|h| of the block,
         // then h as f16 scaled by the power of two that puts that max in [2^14, 2^15), stored
         // in the down kernel's K order (perm32_pos inside every 32-column block)
         float hv[MT][4];
@@ -431,12 +496,12 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
             for (int i = 0; i < 4; ++i) {
                 const int m = 16 * mt + 4 * g + i;
                 hv[mt][i] = 0.0f;
-                if (m < nrows) {
+                if (m < nrows && !p) {
                     const float inv = s_inv[m];
                     hv[mt][i] = silu(acc[mt][0][i] * inv) * (acc[mt][1][i] * inv);
                 }
                 const float rm = max16(fabsf(hv[mt][i]));
-                if (n == 0) atomicMax(&rowmax[m], __builtin_bit_cast(uint32_t, rm));
+                if (n == 0 && !p) atomicMax(&rowmax[m], __builtin_bit_cast(uint32_t, rm));
             }
         lds_barrier();
         const int col = c0 + n, hcol = (col & ~31) + perm32_pos(col & 31);
@@ -445,22 +510,23 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int m = 16 * mt + 4 * g + i;
-                if (m < nrows) {
+                if (m < nrows && !p) {
                     float unused;
                     const float sc = pow2_scale(__builtin_bit_cast(float, rowmax[m]), &unused);
                     a.hh[(size_t)(row0 + m) * I + hcol] = (_Float16)(hv[mt][i] * sc);
                 }
             }
     });
-    if (tid < nrows) a.hmax[(size_t)(row0 + tid) * (I / PF_NGU) + blockIdx.x] = __builtin_bit_cast(float, rowmax[tid]);
+    if (tid < nrows) a.hmax[(size_t)(row0 + tid) * (I / NGU) + blockIdx.x] = __builtin_bit_cast(float, rowmax[tid]);
 }
 
 // ---------------------------------------------------------------- down
-template <int H, int I>
+// NGU: the column width of h's scale blocks (the gate/up item width).
+template <int H, int I, int NGU>
 __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
     constexpr int NTW = 2, NCH = I / PF_KC;
     constexpr int ROWB = (I / QK) * SB_BYTES;
-    constexpr int NHB = I / PF_NGU; // h max blocks per row
+    constexpr int NHB = I / NGU; // h max blocks per row
     constexpr int BPR = I / 32;      // 32-blocks per row
     static_assert(I % QK == 0 && H % PF_ND == 0 && PF_KC * 2 == QK, "down shape");
     static_assert(pf_kch<NCH, 4>() == NCH, "all of K = inter resident in one chunk");
@@ -480,12 +546,12 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
         constexpr int MT = decltype(MTc)::value;
         constexpr int LK = pf_ldsr<NCH, MT>();
         // A: 16*MT rows x BPR 32-blocks; a thread takes blocks tid, tid + 512, ... -- each one
-        // 32 f16 of h, already in the weights' K order and scaled by its 128-column block's
+        // 32 f16 of h, already in the weights' K order and scaled by its NGU-column block's
         // power of two; rescaled here to the power of two of the row's max (a factor 2^-j,
         // exact for normal f16).  All loads (h and the row's max blocks) are issued before any
         // is used.
         constexpr int NIT = 16 * MT * BPR, IPT = (NIT + 64 * PF_WAVES - 1) / (64 * PF_WAVES);
-        static_assert(PF_NGU % 32 == 0, "max blocks of whole 32-blocks");
+        static_assert(NGU % 32 == 0, "max blocks of whole 32-blocks");
         u32x4 hq[IPT][4];
         float hm[IPT][NHB];
 #pragma unroll
@@ -514,7 +580,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
                 for (int b = 0; b < NHB; ++b) mx = fmaxf(mx, hm[j][b]);
                 float inv, inv_b;
                 const float sc = pow2_scale(ar < nrows ? mx : 0.0f, &inv);
-                (void)pow2_scale(hm[j][ab / (PF_NGU / 32)], &inv_b);
+                (void)pow2_scale(hm[j][ab / (NGU / 32)], &inv_b);
                 if (ab == 0) s_inv[ar] = inv;
                 const _Float16 f = (_Float16)(sc * inv_b); // 2^-j, j >= 0 for a real row
                 const f16x2 f2 = {f, f};
@@ -598,13 +664,16 @@ static hipError_t launch_prefill_t(const BucketArgs &b, const PrefillArgs &a, hi
     }
     // one launch over both tile lists (full and big remainder tiles, then small remainders)
     const int ntiles = a.tile_max + a.stile_max;
+    const bool split = a.M <= PF_SPLIT_MAX_M;
     {
         TimedLaunch tl(T, MOE_K_PREFILL_GATE_UP, st);
-        hipLaunchKernelGGL((k_pf_gate_up<H, I>), dim3(I / PF_NGU, ntiles), dim3(64 * PF_WAVES), 0, st, a);
+        if (split) hipLaunchKernelGGL((k_pf_gate_up<H, I, true>), dim3(I / PF_NGU, ntiles), dim3(64 * PF_WAVES), 0, st, a);
+        else hipLaunchKernelGGL((k_pf_gate_up<H, I, false>), dim3(I / PF_NGU_WIDE, ntiles), dim3(64 * PF_WAVES), 0, st, a);
     }
     {
         TimedLaunch tl(T, MOE_K_PREFILL_DOWN, st);
-        hipLaunchKernelGGL((k_pf_down<H, I>), dim3(H / PF_ND, ntiles), dim3(64 * PF_WAVES), 0, st, a);
+        if (split) hipLaunchKernelGGL((k_pf_down<H, I, PF_NGU>), dim3(H / PF_ND, ntiles), dim3(64 * PF_WAVES), 0, st, a);
+        else hipLaunchKernelGGL((k_pf_down<H, I, PF_NGU_WIDE>), dim3(H / PF_ND, ntiles), dim3(64 * PF_WAVES), 0, st, a);
     }
     {
         TimedLaunch tl(T, MOE_K_PREFILL_COMBINE, st);

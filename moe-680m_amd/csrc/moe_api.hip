@@ -31,7 +31,7 @@ struct moe_ctx {
     _Float16 *xh = nullptr;      // [m_max][H]
     float *xinv = nullptr;       // [m_max]
     _Float16 *hh = nullptr;      // [9 m_max][I]
-    float *hmax = nullptr;       // [9 m_max][I/128]
+    float *hmax = nullptr;       // [9 m_max][I/PF_NGU]
     float *part = nullptr;       // [9 m_max][H]
     uint32_t *ranges = nullptr;  // [E+2]
     uint16_t *stok = nullptr;    // [9 m_max]
@@ -139,7 +139,7 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
         {(void **)&c->xh, mm * H * 2},
         {(void **)&c->xinv, mm * 4},
         {(void **)&c->hh, SLOTS * mm * I * 2},
-        {(void **)&c->hmax, SLOTS * mm * (I / 128) * 4},
+        {(void **)&c->hmax, SLOTS * mm * (I / PF_NGU) * 4},
         {(void **)&c->part, SLOTS * mm * H * sizeof(float)},
         {(void **)&c->ranges, (E1 + 1) * 4},
         {(void **)&c->stok, SLOTS * mm * 2},

@@ -14,6 +14,12 @@ struct Tile {
 
 constexpr int PF_BM = 64;  // prefill big-tile rows (token slots of one expert)
 constexpr int PF_SMALL_MAX = 32; // remainders of at most this many slots are listed as small tiles
+// h columns per prefill gate/up work item, and per hmax block: 64 (two waves per 16 columns,
+// alternate K stages: half-length items, which fill the last round of workgroup slots better)
+// for M <= PF_SPLIT_MAX_M, else 128 (one wave per 16 columns: fewer items to stage A for).
+constexpr int PF_NGU = 64;
+constexpr int PF_NGU_WIDE = 128;
+constexpr int PF_SPLIT_MAX_M = 1024;
 
 struct DecodeArgs {
     LayerPtrs L;
@@ -52,10 +58,10 @@ struct PrefillArgs {
     const float *sorted_w;
     const uint32_t *pos; // [M][9]
     const Tile *tiles;
-    _Float16 *hh;        // [9M][I] h = silu(g) * u as f16, sorted slot order: each 128-column
+    _Float16 *hh;        // [9M][I] h = silu(g) * u as f16, sorted slot order: each PF_NGU-column
                          // block scaled by the power of two of its max (hmax), K order of the
                          // down kernel's A (perm32_pos inside 32-column blocks)
-    float *hmax;         // [9M][I/128] max |h| per row and 128-column block
+    float *hmax;         // [9M][I/PF_NGU] max |h| per row and PF_NGU-column block
     float *part;         // [9M][H] f32, c*w-scaled expert outputs, sorted slot order
     float *y;
     int M, E, accumulate, rmsnorm, tile_max, stile_max;
