@@ -9,7 +9,7 @@
 //            max|x| in [2^14, 2^15), stored as f16 with K permuted inside 32-blocks (the
 //            order the weight nibbles arrive in, see below); 1/s_t kept per token -- run in
 //            the same launch as the bucket fill (k_pf_route_prep), which does not need it;
-//   gate_up: per (tile, 64 gate/up column pairs; 128 when M > 1024) a workgroup of 8 waves,
+//   gate_up: per (tile, 64 gate/up column pairs; 128 when M > 768) a workgroup of 8 waves,
 //            two per CU; the tile's token rows (gathered -- the reference's kernel skipped
 //            this gather) are resident in LDS one 64 KB chunk of K at a time and shared by the
 //            8 waves; each wave decodes 16 W1 rows and 16 W3 rows (with 64 columns, two waves
