@@ -10,7 +10,8 @@ every step routes differently, so weights stream from HBM.  `value` is algorithm
 time is logged beside it).  The prefill leg (config 1: M=512, Zipf(1.1)-biased router) is reported in the
 same line, with tok/s and the MFMA fraction (f16 operands; the f16 and bf16 dense peaks are
 the same 2.5 PFLOP/s), and so are config 3 (one layer at M = 2, 4, 8: GB/s of the distinct
-experts selected) and config 4 (M = 4096: MFMA fraction).
+experts selected) and config 4 (M = 4096: MFMA fraction); prefill and config 3 steps are
+replayed five per graph.
 
     python bench.py [--steps K] [--warmup W]      # one JSON line on stdout
 """
@@ -284,13 +285,16 @@ def main():
 
             step3(0)
             torch.cuda.synchronize()
-            g3 = [capture(torch, lambda s=s, f=step3: f(s)) for s in range(n3)]
-            for s in range(3):
-                g3[s].replay()
+            # warm-up steps one per graph, timed steps PG per graph, as in the prefill leg
+            g3 = [capture(torch, lambda s=s, f=step3: f(s)) for s in range(3)]
+            g3 += [capture(torch, lambda b=b, f=step3: [f(s) for s in range(b, min(b + PG, n3))])
+                   for b in range(3, n3, PG)]
+            for g in g3[:3]:
+                g.replay()
             torch.cuda.synchronize()
             ev0.record()
-            for s in range(3, n3):
-                g3[s].replay()
+            for g in g3[3:]:
+                g.replay()
             ev1.record()
             torch.cuda.synchronize()
             us3 = ev0.elapsed_time(ev1) * 1e3 / (n3 - 3)
