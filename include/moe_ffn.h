@@ -47,7 +47,7 @@ typedef enum {
  *   MOE_W_RENORM: w renormalised over the 8 selected experts, scale 1. */
 typedef enum { MOE_W_REF = 0, MOE_W_RENORM = 1 } moe_wmode;
 
-enum { MOE_TOPK = 8, MOE_SLOTS = 9, MOE_DECODE_MAX_M = 8 };
+enum { MOE_TOPK = 8, MOE_SLOTS = 9, MOE_DECODE_MAX_M = 8, MOE_MAX_EXPERTS = 256 };
 
 /* moe_ffn flags */
 enum {
@@ -65,7 +65,7 @@ enum {
 typedef struct {
     int hidden;     /* 2048 for moe-680m (also 512 is compiled, for small tests) */
     int inter;      /* 512 for moe-680m (also 256 is compiled) */
-    int n_experts;  /* routed experts, 8..1024 (256 for moe-680m); shared id = n_experts */
+    int n_experts;  /* routed experts, 8..256 (256 for moe-680m); shared id = n_experts */
     int n_layers;   /* weight tables to hold (40 for moe-680m) */
     int m_max;      /* largest M any call will pass (<= 65535); sizes the workspaces */
     moe_wmode wmode;
@@ -90,10 +90,10 @@ typedef struct {
 moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out);
 moe_status moe_destroy(moe_ctx *ctx);
 
-/* Record one layer's weight table (device pointers; the single-layer decode path reads
- * them in place) and copy the layer into the context's decode-stack layout and, for a
- * prefill context, its prefill layout (same bytes, rearranged).  Synchronises the device;
- * rebinding a layer replaces its copies.
+/* Copy one layer's weights (device pointers, read only during this call) into the context's
+ * split layout, which the decode path and the decode stack read, and, for a prefill context,
+ * its prefill layout (same bytes, rearranged).  Synchronises the device; rebinding a layer
+ * replaces its copies.
  * Replaces LayerWeights::from_registry (src/memory.rs:227-291). */
 moe_status moe_bind_layer(moe_ctx *ctx, int layer, const moe_layer_weights *lw);
 
@@ -115,12 +115,25 @@ moe_status moe_bucket_fill(moe_ctx *ctx, const uint16_t *ids, const float *w, in
 /* The expert FFN of one layer for M tokens and the weighted combine:
  *   out_t = c * sum_{s<9} w[t][s] * W2_e (silu(W1_e xin_t) * (W3_e xin_t)),  e = ids[t][s]
  *   y_t   = (flags & ACCUMULATE ? y_t : 0) + out_t
- * c = 1/9 (MOE_W_REF) or 1 (MOE_W_RENORM).  x and y may be the same buffer.
- * M <= 8 runs the decode GEMV kernels (f32); larger M runs bucket fill + grouped
- * bf16-MFMA GEMMs + combine.  Replaces record_and_submit_moe (src/inference.rs:663-766):
- * shaders w1_w3_fused(_m1).comp, silu_mult.comp, w2(_scatter)(_m1).comp, moe_combine.comp. */
+ * c = 1/9 (MOE_W_REF) or 1 (MOE_W_RENORM).  x and y may be the same buffer.  A slot whose
+ * id exceeds n_experts, or repeats an id of an earlier slot of its token, is dropped
+ * (MOE_DEVFLAG_BAD_ID / MOE_DEVFLAG_DUP_ID), for every M.
+ * M <= 8 runs the decode path, one launch of IQ4_XS GEMVs (activations as two int8 planes
+ * per 32-element chunk, f32 accumulation; each selected expert's weights read once however
+ * many tokens chose it); larger M runs bucket fill + grouped f16-MFMA GEMMs (f32
+ * accumulate) + combine.  Replaces record_and_submit_moe (src/inference.rs:663-766): shaders
+ * w1_w3_fused(_m1).comp, silu_mult.comp, w2(_scatter)(_m1).comp, moe_combine.comp. */
 moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids, const float *w,
                    int M, float *y, int flags, void *stream);
+
+/* Router and expert FFN of one layer in one call: (ids, w) = top8(softmax(logits)) exactly
+ * as moe_router_topk computes them (written to ids/w, [M][9]), then moe_ffn with them.  For
+ * M <= 2 the routing runs inside the decode launch (no separate router launch).
+ * Replaces the RouterTopk dispatch (src/inference.rs:608-616), do_route's readback
+ * (src/inference.rs:622-659) and record_and_submit_moe (src/inference.rs:663-766) of one
+ * layer. */
+moe_status moe_ffn_route(moe_ctx *ctx, int layer, const float *x, const float *logits, int M,
+                         float *y, uint16_t *ids, float *w, int flags, void *stream);
 
 /* One token (M = 1) through n_layers consecutive MoE layers in one persistent launch:
  *   for l in layer0 .. layer0+n_layers-1:
@@ -130,7 +143,11 @@ moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids,
  * logits f32 [n_layers][n_experts]; ids u16 / w f32 [n_layers][9] receive the routing
  * (both may be NULL).  flags: MOE_FFN_RMSNORM (the residual is always added).
  * Needs n_experts <= 256 and every workgroup of the launch resident at once (one per CU;
- * checked at moe_create).  A bounded wait that expires sets MOE_DEVFLAG_TIMEOUT.
+ * checked at moe_create), hidden/8 workgroups spread evenly over the device's 8 XCDs.
+ * Every wait inside the launch is bounded: one that expires sets MOE_DEVFLAG_TIMEOUT, every
+ * workgroup then stops publishing and leaves, and y is left unwritten -- it is written only
+ * after every row of the last layer is complete -- so an x that y aliases keeps its value.
+ * Check the flag with moe_device_flags or, without a host sync, moe_device_flags_async.
  * Replaces, for the MoE path of one decode token, the per-layer sequence
  * record_and_submit_layer's RouterTopk dispatch -> do_route -> record_and_submit_moe of
  * InferenceEngine::forward_single (src/inference.rs:296-301, 608-616, 622-766). */
@@ -146,6 +163,18 @@ moe_status moe_dequant_iq4xs(const void *blocks, size_t n_superblocks, float *ou
  * No reference counterpart: the reference panics instead (src/router.rs:41). */
 moe_status moe_device_flags(moe_ctx *ctx, void *stream, uint32_t *flags);
 
+/* Stream-ordered variant for callers that cannot block (a serving loop, graph capture): one
+ * tiny launch on `stream` moves the sticky device flags into *dst (device memory, or pinned
+ * host memory from hipHostMalloc) and clears them; the host reads *dst once the stream has
+ * passed that point.  No reference counterpart (the reference panics, src/router.rs:41). */
+moe_status moe_device_flags_async(moe_ctx *ctx, uint32_t *dst, void *stream);
+
+/* Poll rounds after which a bounded wait inside moe_decode_stack expires (default 65536;
+ * a round is one reload of the awaited words).  0 makes every wait that is not satisfied at
+ * its first look expire at once -- a host-forced timeout for testing the failure path, in
+ * which every workgroup still exits normally.  No reference counterpart. */
+moe_status moe_stack_spin_limit(moe_ctx *ctx, uint32_t polls);
+
 /* Last error message of the calling thread ("" when none). */
 const char *moe_last_error(void);
 
@@ -157,18 +186,16 @@ const char *moe_last_error(void);
  * timed launches and their summed milliseconds, and starts a new window.  Events are
  * created here, never inside a hot call; capacity 0 disables and frees them. */
 enum {
-    MOE_K_ROUTER_TOPK = 0,
-    MOE_K_BUCKET_FILL = 1,
-    MOE_K_DECODE_GATE_UP = 2,
+    MOE_K_ROUTER_TOPK = 0,     /* moe_router_topk, and moe_ffn_route's router launch for M > 2 */
+    MOE_K_BUCKET_FILL = 1,     /* moe_bucket_fill; moe_ffn's first prefill launch (bucket fill + prep) */
+    MOE_K_DECODE_GATE_UP = 2,  /* moe_ffn / moe_ffn_route, M <= 8 */
     MOE_K_DECODE_DOWN = 3,
-    MOE_K_PREFILL_PREP = 4,          /* no longer launched: moe_ffn's prep runs in its BUCKET_FILL launch */
-    MOE_K_PREFILL_GATE_UP = 5,
-    MOE_K_PREFILL_DOWN = 6,
-    MOE_K_PREFILL_COMBINE = 7,
-    MOE_K_DECODE_STACK = 8,
-    MOE_K_PREFILL_GATE_UP_SMALL = 9, /* no longer launched (small tiles run in the kernels above); */
-    MOE_K_PREFILL_DOWN_SMALL = 10,   /* ids kept so the numbering stays stable; they count 0 */
-    MOE_K_COUNT = 11
+    MOE_K_PREFILL_GATE_UP = 4,
+    MOE_K_PREFILL_DOWN = 5,
+    MOE_K_PREFILL_COMBINE = 6,
+    MOE_K_DECODE_STACK = 7,    /* moe_decode_stack: the persistent launch */
+    MOE_K_STACK_PREP = 8,      /* moe_decode_stack: the routing + clearing launch before it */
+    MOE_K_COUNT = 9
 };
 moe_status moe_timing_enable(moe_ctx *ctx, int capacity);
 moe_status moe_timing_read(moe_ctx *ctx, int counts[MOE_K_COUNT], double total_ms[MOE_K_COUNT]);

@@ -13,6 +13,8 @@ Reference interfaces mirrored (path:line in the reference tree):
                               the GPU top-k read back by do_route (src/inference.rs:622-659)
   ``Context.bucket_fill``  -- router::build_expert_batches (src/router.rs:55-97)
   ``Context.ffn``          -- InferenceEngine::record_and_submit_moe (src/inference.rs:663-766)
+  ``Context.ffn_route``    -- the RouterTopk dispatch + do_route + record_and_submit_moe of one
+                              layer (src/inference.rs:608-616, 622-766)
 """
 import ctypes
 import os
@@ -38,14 +40,14 @@ DEVFLAG_BAD_ID, DEVFLAG_DUP_ID, DEVFLAG_TIMEOUT = 1, 2, 4
 # Every symbol include/moe_ffn.h declares (checked by the CPU test suite).
 EXPORTS = (
     "moe_create", "moe_destroy", "moe_bind_layer", "moe_router_topk", "moe_bucket_fill",
-    "moe_ffn", "moe_decode_stack", "moe_dequant_iq4xs", "moe_device_flags", "moe_last_error",
+    "moe_ffn", "moe_ffn_route", "moe_decode_stack", "moe_dequant_iq4xs", "moe_device_flags",
+    "moe_device_flags_async", "moe_stack_spin_limit", "moe_last_error",
     "moe_timing_enable", "moe_timing_read",
     "moe_gen_iq4xs", "moe_gen_normal", "moe_gen_logits",
 )
 
-KERNELS = ("router_topk", "bucket_fill", "decode_gate_up", "decode_down", "prefill_prep",
-           "prefill_gate_up", "prefill_down", "prefill_combine", "decode_stack",
-           "prefill_gate_up_small", "prefill_down_small")
+KERNELS = ("router_topk", "bucket_fill", "decode_gate_up", "decode_down", "prefill_gate_up",
+           "prefill_down", "prefill_combine", "decode_stack", "stack_prep")
 
 
 class MoeError(RuntimeError):
@@ -86,9 +88,12 @@ def lib():
         "moe_router_topk": [vp, vp, i, vp, vp, vp],
         "moe_bucket_fill": [vp, vp, vp, i, vp, vp, vp, vp],
         "moe_ffn": [vp, i, vp, vp, vp, i, vp, i, vp],
+        "moe_ffn_route": [vp, i, vp, vp, i, vp, vp, vp, i, vp],
         "moe_decode_stack": [vp, i, i, vp, vp, vp, vp, vp, i, vp],
         "moe_dequant_iq4xs": [vp, sz, vp, vp],
         "moe_device_flags": [vp, vp, ctypes.POINTER(ctypes.c_uint32)],
+        "moe_device_flags_async": [vp, vp, vp],
+        "moe_stack_spin_limit": [vp, ctypes.c_uint32],
         "moe_gen_iq4xs": [vp, sz, u64, u64, vp],
         "moe_gen_normal": [vp, sz, u64, u64, ctypes.c_float, ctypes.c_float, vp],
         "moe_gen_logits": [vp, i, i, u64, i, ctypes.c_double, ctypes.c_double, vp],
@@ -220,6 +225,21 @@ class Context:
                              _stream(stream)))
         return y
 
+    def ffn_route(self, layer, x, logits, y=None, ids=None, w=None, accumulate=False, rmsnorm=False,
+                  stream=None):
+        """Router + expert FFN in one call (moe_ffn_route); returns (y, ids, w)."""
+        M = x.shape[0]
+        if y is None:
+            y = torch.empty_like(x)
+        if ids is None:
+            ids = torch.empty((M, SLOTS), dtype=torch.uint16, device=x.device)
+        if w is None:
+            w = torch.empty((M, SLOTS), dtype=torch.float32, device=x.device)
+        flags = (FFN_ACCUMULATE if accumulate else 0) | (FFN_RMSNORM if rmsnorm else 0)
+        _check(lib().moe_ffn_route(self._h, layer, _ptr(x), _ptr(logits), M, _ptr(y), _ptr(ids), _ptr(w),
+                                   flags, _stream(stream)))
+        return y, ids, w
+
     def decode_stack(self, layer0, x, logits, y=None, ids=None, w=None, rmsnorm=True, stream=None):
         """One token through len(logits) consecutive layers starting at layer0:
         routing from logits[l], x <- x + MoE_l(RMSNorm(x)).  Returns y (= x if y is x)."""
@@ -235,6 +255,15 @@ class Context:
         v = ctypes.c_uint32()
         _check(lib().moe_device_flags(self._h, _stream(stream), ctypes.byref(v)))
         return v.value
+
+    def device_flags_async(self, dst, stream=None):
+        """Enqueue the move of the sticky flags into dst (a 1-element int32/uint32 tensor on
+        the device or in pinned host memory); no host synchronisation."""
+        _check(lib().moe_device_flags_async(self._h, _ptr(dst), _stream(stream)))
+        return dst
+
+    def stack_spin_limit(self, polls):
+        _check(lib().moe_stack_spin_limit(self._h, polls))
 
     def timing_enable(self, capacity=4096):
         _check(lib().moe_timing_enable(self._h, capacity))

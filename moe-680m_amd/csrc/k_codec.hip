@@ -273,6 +273,15 @@ hipError_t launch_repack_split(const void *src, uint64_t src_stride, const void 
     return hipGetLastError();
 }
 
+__global__ void k_flags_take(uint32_t *flags, uint32_t *dst) {
+    *dst = __hip_atomic_exchange((MOE_GLOBAL uint32_t *)flags, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+hipError_t launch_flags_take(uint32_t *flags, uint32_t *dst, hipStream_t st) {
+    hipLaunchKernelGGL(k_flags_take, dim3(1), dim3(1), 0, st, flags, dst);
+    return hipGetLastError();
+}
+
 hipError_t launch_dequant(const void *blocks, uint64_t n_sb, float *out, hipStream_t st) {
     uint64_t threads = n_sb * 8;
     if (threads == 0) return hipSuccess;

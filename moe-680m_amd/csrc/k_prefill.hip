@@ -580,9 +580,13 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
                 for (int b = 0; b < NHB; ++b) mx = fmaxf(mx, hm[j][b]);
                 float inv, inv_b;
                 const float sc = pow2_scale(ar < nrows ? mx : 0.0f, &inv);
-                (void)pow2_scale(hm[j][ab / (NGU / 32)], &inv_b);
+                const float hb = hm[j][ab / (NGU / 32)];
+                (void)pow2_scale(hb, &inv_b);
                 if (ab == 0) s_inv[ar] = inv;
-                const _Float16 f = (_Float16)(sc * inv_b); // 2^-j, j >= 0 for a real row
+                // 2^-j, j >= 0, for a block with a nonzero max; a block whose max is 0 holds
+                // only zeros, and its factor is 0 (sc alone can exceed the f16 range when the
+                // row's max is small: 0 * inf would be NaN)
+                const _Float16 f = hb > 0.0f ? (_Float16)(sc * inv_b) : (_Float16)0.0f;
                 const f16x2 f2 = {f, f};
                 u32x4 *d = reinterpret_cast<u32x4 *>(As + ar * LK + 32 * ab);
 #pragma unroll

@@ -59,14 +59,8 @@
 
 namespace moe {
 
-constexpr uint32_t STK_SPIN_MAX = 1u << 16;
 constexpr int STK_NX = 8;   // XCDs
 
-// Cross-XCD publish: an agent-scope store writes through this XCD's L2.
-__device__ __forceinline__ void tag_store(uint32_t *p, float v) {
-    __hip_atomic_store((MOE_GLOBAL uint32_t *)p, __builtin_bit_cast(uint32_t, v) | 1u, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-}
 // XCD-local publish: a plain store, which stays in this XCD's L2.
 __device__ __forceinline__ void tag_store_local(uint32_t *p, float v) {
     *(MOE_GLOBAL uint32_t *)p = __builtin_bit_cast(uint32_t, v) | 1u;
@@ -76,10 +70,9 @@ __device__ __forceinline__ void tag_store_local(uint32_t *p, float v) {
 // lane's 32-float chunk).
 __device__ __forceinline__ int padk(int k) { return k + ((k >> 5) << 2); }
 
-__device__ __forceinline__ uint32_t qtag(u32x4 v) { return v[0] & v[1] & v[2] & v[3] & 1u; }
 // Tag tests: LSB-tagged f32 words, or words that are never zero once published.
 struct LsbTag {
-    __device__ __forceinline__ uint32_t operator()(u32x4 v) const { return qtag(v); }
+    __device__ __forceinline__ uint32_t operator()(u32x4 v) const { return quad_tagged(v); }
 };
 struct NonzeroTag {
     __device__ __forceinline__ uint32_t operator()(u32x4 v) const {
@@ -94,12 +87,7 @@ struct NonzeroTag {
 // XCD's L2, where the plain stores of its workgroups land.
 struct RemoteQuads {
     const u32x4 *p;
-    __device__ __forceinline__ u32x4 operator()(int q) const {
-        const MOE_GLOBAL uint64_t *g = (const MOE_GLOBAL uint64_t *)(p + q);
-        const uint64_t lo = __hip_atomic_load(g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        const uint64_t hi = __hip_atomic_load(g + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        return u32x4{(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
-    }
+    __device__ __forceinline__ u32x4 operator()(int q) const { return remote_quad(p + q); }
 };
 struct LocalQuads {
     const uint64_t *p;
@@ -111,31 +99,43 @@ struct LocalQuads {
     }
 };
 
+typedef volatile __attribute__((address_space(3))) int lds_flag;
+
+// Expiry of a bounded wait: the sticky TIMEOUT flag, the launch's abort word (every other
+// waiter stops at its next check) and this workgroup's own abort flag.
+__device__ __forceinline__ void stack_abort(uint32_t *flags, lds_flag *s_abort) {
+    set_flag(flags, MOE_DEVFLAG_TIMEOUT);
+    set_flag(flags + 1, 1u);
+    *s_abort = 1;
+}
+
 // Bounded wait until every quad in v[] is tagged, reloading only the untagged ones.  All
-// loads of a round are in flight together; a round ends with one wave-wide test.  Returns
-// with the abort word set (and the caller's data invalid) when the wait fails.
+// loads of a round are in flight together; a round ends with one wave-wide test.  After
+// spin_max failed rounds (checked every 32 rounds, or every round once past the limit) the
+// wait expires; it also gives up when this workgroup or any other has aborted.  Either way
+// it returns with the abort flag set and the caller's data invalid -- and once it is set,
+// nothing more is published, so no other workgroup can receive data computed from it.
 template <int MAXQ, typename LD, typename TAG = LsbTag>
 __device__ __forceinline__ void poll_until_tagged(u32x4 (&v)[MAXQ], const int (&q)[MAXQ], const LD &ld,
-                                                  uint32_t *flags,
-                                                  volatile __attribute__((address_space(3))) int *s_abort,
+                                                  uint32_t *flags, uint32_t spin_max, lds_flag *s_abort,
                                                   TAG tag = TAG{}) {
+    if (*s_abort) return;
     uint32_t spins = 0;
     while (true) {
         uint32_t t = 1u;
 #pragma unroll
         for (int j = 0; j < MAXQ; ++j) t &= tag(v[j]);
         if (__all(t)) break;
-        if ((++spins & 31u) == 0) {
+        ++spins;
+        if ((spins & 31u) == 0 || spins > spin_max) {
             if (*s_abort) break;
             if (__hip_atomic_load((const MOE_GLOBAL uint32_t *)(flags + 1), __ATOMIC_RELAXED,
                                   __HIP_MEMORY_SCOPE_AGENT)) {
                 *s_abort = 1;
                 break;
             }
-            if (spins >= STK_SPIN_MAX) {
-                set_flag(flags, MOE_DEVFLAG_TIMEOUT);
-                set_flag(flags + 1, 1u);
-                *s_abort = 1;
+            if (spins > spin_max) {
+                stack_abort(flags, s_abort);
                 break;
             }
         }
@@ -145,11 +145,29 @@ __device__ __forceinline__ void poll_until_tagged(u32x4 (&v)[MAXQ], const int (&
     }
 }
 
-// Total of each group of G lanes, complete in lane 63 for G = 64 and in every lane otherwise.
-template <int G>
-__device__ __forceinline__ float row_total(float v) {
-    if constexpr (G == 64) return wave_sum_last(v);
-    else return group_sum<G>(v);
+// Bounded wait (same limits as poll_until_tagged) until the XCD-local counter reaches
+// target; false when the wait expired or the launch aborted.
+__device__ __forceinline__ bool wait_count(const uint32_t *ctr, uint32_t target, uint32_t *flags, uint32_t spin_max,
+                                           lds_flag *s_abort) {
+    uint32_t spins = 0;
+    while (true) {
+        const uint32_t c = (uint32_t)__builtin_amdgcn_readfirstlane((int)__hip_atomic_load(
+            (const MOE_GLOBAL uint32_t *)ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        if (c >= target) return !*s_abort;
+        ++spins;
+        if ((spins & 31u) == 0 || spins > spin_max) {
+            if (*s_abort) return false;
+            if (__hip_atomic_load((const MOE_GLOBAL uint32_t *)(flags + 1), __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT)) {
+                *s_abort = 1;
+                return false;
+            }
+            if (spins > spin_max) {
+                stack_abort(flags, s_abort);
+                return false;
+            }
+        }
+    }
 }
 
 // Sum over aligned groups of G adjacent lanes (G = 1, 2, 4, 8), result in every lane.
@@ -164,17 +182,11 @@ __device__ __forceinline__ float adjacent_sum(float v) {
 }
 
 // ---------------------------------------------------------------- int8 activations
-// Phase A reads x as two int8 planes per 32-element chunk c (one IQ4_XS sub-block of K):
-//     x_i ~= s_c * (xh_i + xl_i / 256),  s_c = max_c |x| / 127,  xh = rint(x / s_c),
-//     xl = rint(256 * (x / s_c - xh)),
-// so a sub-block dot is two integer dot products of the signed codebook bytes
-// (v_dot4_i32_i8) with f32 scaling once per sub-block.  Error per element <= s_c / 256,
-// i.e. <= 1.6e-5 of the chunk's largest |x|.  In the exchange, element pair (2w, 2w+1) is
-// one word [xl_2w, xh_2w ^ 0x80, xl_2w+1, xh_2w+1 ^ 0x80]: xh is never -128, so byte 1 is
-// never zero and a published word is never zero -- the exchange tag is "word != 0"
-// (the zero-cleared buffer), which costs no bit of precision.
-__device__ __forceinline__ float quant_ratio(float am) { return am > 1e-30f ? 127.0f * __builtin_amdgcn_rcpf(am) : 0.0f; }
-
+// Phase A reads x as the two int8 planes of moe_device.hpp (quant_ratio, subblock_idot).  In
+// the exchange, element pair (2w, 2w+1) is one word [xl_2w, xh_2w ^ 0x80, xl_2w+1,
+// xh_2w+1 ^ 0x80]: xh is never -128, so byte 1 is never zero and a published word is never
+// zero -- the exchange tag is "word != 0" (the zero-cleared buffer), which costs no bit of
+// precision.
 __device__ __forceinline__ uint32_t pack_pair(float xe, float xo, float r) {
     const float ue = xe * r, uo = xo * r;
     // the clamps also map a non-finite input to a finite byte, so the tag always holds
@@ -185,10 +197,6 @@ __device__ __forceinline__ uint32_t pack_pair(float xe, float xo, float r) {
             (((uint32_t)(int)ho & 0xFFu) << 24)) ^ 0x80008000u;
 }
 
-// LDS planes: chunk c at XQS * c: xh dwords 0..7 (elements 4d..4d+3), xl dwords 8..15,
-// 4 pad dwords (a lane's 128-bit reads of its chunk are conflict-free across lanes).
-constexpr int XQS = 20;
-
 // Exchange quad q (elements 8q..8q+7, four pair words) into the planes.
 __device__ __forceinline__ void store_quad(uint32_t *xq, int q, u32x4 v) {
     uint32_t *c = xq + XQS * (q >> 2) + 2 * (q & 3);
@@ -196,61 +204,6 @@ __device__ __forceinline__ void store_quad(uint32_t *xq, int q, u32x4 v) {
                                           __builtin_amdgcn_perm(v[3], v[2], 0x07050301u) ^ 0x80808080u};
     *reinterpret_cast<u32x2 *>(c + 8) =
         u32x2{__builtin_amdgcn_perm(v[1], v[0], 0x06040200u), __builtin_amdgcn_perm(v[3], v[2], 0x06040200u)};
-}
-
-// One qs dword (weights 4d..4d+3 low nibbles, 16+4d.. high nibbles) against the planes'
-// dwords of those elements: xh_lo = dword d, xh_hi = dword 4+d (and the same for xl).
-// lo, hi: the signed codebook bytes of the dword's low and high nibbles (kv_signed8).
-__device__ __forceinline__ void dword_idot(uint32_t lo, uint32_t hi, uint32_t xh_lo, uint32_t xh_hi, uint32_t xl_lo,
-                                           uint32_t xl_hi, int &ah, int &al) {
-    ah = __builtin_amdgcn_sdot4((int)lo, (int)xh_lo, ah, false);
-    ah = __builtin_amdgcn_sdot4((int)hi, (int)xh_hi, ah, false);
-    al = __builtin_amdgcn_sdot4((int)lo, (int)xl_lo, al, false);
-    al = __builtin_amdgcn_sdot4((int)hi, (int)xl_hi, al, false);
-}
-
-// Whole sub-block, already looked up (kv[2d], kv[2d+1] = kv_signed8 of qs dword d), against
-// chunk planes xh[8], xl[8]: sum kv * (xh + xl/256), unscaled.
-__device__ __forceinline__ float subblock_idot(const uint32_t (&kv)[8], const uint32_t (&xh)[8],
-                                               const uint32_t (&xl)[8]) {
-    int ah = 0, al = 0;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) dword_idot(kv[2 * d], kv[2 * d + 1], xh[d], xh[4 + d], xl[d], xl[4 + d], ah, al);
-    return __builtin_fmaf((float)al, 1.0f / 256.0f, (float)ah);
-}
-
-// 8 weights of one qs dword -- weights 4d..4d+3 (low nibbles) and 16+4d..16+4d+3 (high
-// nibbles) of a sub-block, as the biased codebook bytes lo, hi (kv_biased8) -- against their
-// activations xl[0..3], xh[0..3]; unscaled.
-__device__ __forceinline__ float dword_dot(uint32_t lo, uint32_t hi, const float *xl, const float *xh) {
-    float a0 = ubyte(lo, 0) * xl[0], a1 = ubyte(lo, 1) * xl[1];
-    a0 = __builtin_fmaf(ubyte(lo, 2), xl[2], a0);
-    a1 = __builtin_fmaf(ubyte(lo, 3), xl[3], a1);
-    a0 = __builtin_fmaf(ubyte(hi, 0), xh[0], a0);
-    a1 = __builtin_fmaf(ubyte(hi, 1), xh[1], a1);
-    a0 = __builtin_fmaf(ubyte(hi, 2), xh[2], a0);
-    a1 = __builtin_fmaf(ubyte(hi, 3), xh[3], a1);
-    const float xs = ((xl[0] + xl[1]) + (xl[2] + xl[3])) + ((xh[0] + xh[1]) + (xh[2] + xh[3]));
-    return (a0 + a1) - 128.f * xs;
-}
-
-// Whole sub-block, already looked up (kv[2d], kv[2d+1] = kv_biased8 of qs dword d), against
-// its 32 activations xv; xs = their sum.  Unscaled.
-__device__ __forceinline__ float subblock_dot(const uint32_t (&kv)[8], const float (&xv)[32], float xs) {
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        const uint32_t lo = kv[2 * d], hi = kv[2 * d + 1];
-        a0 = __builtin_fmaf(ubyte(lo, 0), xv[4 * d + 0], a0);
-        a1 = __builtin_fmaf(ubyte(lo, 1), xv[4 * d + 1], a1);
-        a2 = __builtin_fmaf(ubyte(lo, 2), xv[4 * d + 2], a2);
-        a3 = __builtin_fmaf(ubyte(lo, 3), xv[4 * d + 3], a3);
-        a0 = __builtin_fmaf(ubyte(hi, 0), xv[16 + 4 * d + 0], a0);
-        a1 = __builtin_fmaf(ubyte(hi, 1), xv[16 + 4 * d + 1], a1);
-        a2 = __builtin_fmaf(ubyte(hi, 2), xv[16 + 4 * d + 2], a2);
-        a3 = __builtin_fmaf(ubyte(hi, 3), xv[16 + 4 * d + 3], a3);
-    }
-    return ((a0 + a1) + (a2 + a3)) - 128.f * xs;
 }
 
 template <int H, int I>
@@ -308,15 +261,29 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     __shared__ float rt_w[3][2];        // per layer (ring of 3): weight of slot k, shared
     __shared__ const uint8_t *rt_p[3][2][3]; // W1, W3, W2 of the routed expert / shared
     __shared__ int s_abort;
+    __shared__ int s_j;
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     // HW_REG_XCC_ID (readfirstlane: the compiler then knows the value is wave-uniform)
     const int k = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & (NX - 1));
-    const int j = blockIdx.x / NX;
     const int n = a.n_layers;
-    if (tid == 0) s_abort = 0;
-    volatile __attribute__((address_space(3))) int *abort_lds =
-        (volatile __attribute__((address_space(3))) int *)&s_abort;
+    lds_flag *abort_lds = (lds_flag *)&s_abort;
+    // j: this workgroup's rank among the workgroups that started on XCD k, from a per-XCD
+    // ticket (not from blockIdx, so no assumption on the dispatch order).  An XCD that
+    // receives more than NJ workgroups leaves another XCD short: the surplus ones raise the
+    // timeout and leave, and the others' bounded waits end the launch with y untouched.
+    if (tid == 0) {
+        const uint32_t t = __hip_atomic_fetch_add((MOE_GLOBAL uint32_t *)(a.ctl + k), 1u, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+        s_j = t < (uint32_t)NJ ? (int)t : -1;
+        s_abort = 0;
+    }
+    __syncthreads();
+    const int j = s_j;
+    if (j < 0) {
+        if (tid == 0) stack_abort(a.flags, abort_lds);
+        return;
+    }
 
     // exchange buffers of (layer li, XCD k)
     auto hbuf = [&](int li) { return a.hx + ((size_t)li * NX + k) * HXG; };
@@ -416,7 +383,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                     q[m] = first ? I / 4 + 4 * lane + m : lane + 64 * m;
                     v[m] = ok ? ld(q[m]) : u32x4{1u, 1u, 1u, 1u};
                 }
-                poll_until_tagged<4>(v, q, ld, a.flags, abort_lds);
+                poll_until_tagged<4>(v, q, ld, a.flags, a.spin_max, abort_lds);
                 if (first) {
                     if (lane < I / NX) {
                         float g = 0.f, u = 0.f;
@@ -453,13 +420,13 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             if (first) {
                 // publish this XCD's partial of rows [64j, 64j+64) ...
                 uint32_t *pb = pbuf(li);
-                tag_store(pb + (size_t)k * H + ROWS * j + lane, part[0][lane] + part[1][lane]);
+                if (!*abort_lds) tag_store(pb + (size_t)k * H + ROWS * j + lane, part[0][lane] + part[1][lane]);
                 // ... gather all eight (lane: quad lane&15 of XCDs lane>>4 and (lane>>4)+4) ...
                 const RemoteQuads ld{reinterpret_cast<const u32x4 *>(pb + ROWS * j)};
                 const int m = lane >> 4, qq = lane & 15;
                 int q[2] = {m * (H / 4) + qq, (m + 4) * (H / 4) + qq};
                 u32x4 v[2] = {ld(q[0]), ld(q[1])};
-                poll_until_tagged<2>(v, q, ld, a.flags, abort_lds);
+                poll_until_tagged<2>(v, q, ld, a.flags, a.spin_max, abort_lds);
                 *reinterpret_cast<f32x4 *>(&ps[m][4 * qq]) = __builtin_bit_cast(f32x4, v[0]);
                 *reinterpret_cast<f32x4 *>(&ps[m + 4][4 * qq]) = __builtin_bit_cast(f32x4, v[1]);
                 // lanes read what other lanes of this wave wrote: LDS keeps a wave's
@@ -487,12 +454,21 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                     }
                     const float xo = dpp_mov<0xB1>(x1); // the odd partner of an even lane
                     const float ss = wave_sum(x1 * x1);
-                    if ((lane & 1) == 0)
-                        *(MOE_GLOBAL uint32_t *)(xb + (row >> 1)) = pack_pair(x1, xo, quant_ratio(am));
-                    if ((lane & 31) == 0) tag_store_local(xb + H / 2 + (row >> 5), am * (1.0f / 127.0f));
-                    if (lane == 0) tag_store_local(xb + H / 2 + H / 32 + j, ss);
-                } else if (k == 0) {
-                    *(MOE_GLOBAL float *)(a.y + row) = x1;
+                    if (!*abort_lds) {
+                        if ((lane & 1) == 0)
+                            *(MOE_GLOBAL uint32_t *)(xb + (row >> 1)) = pack_pair(x1, xo, quant_ratio(am));
+                        if ((lane & 31) == 0) tag_store_local(xb + H / 2 + (row >> 5), am * (1.0f / 127.0f));
+                        if (lane == 0) tag_store_local(xb + H / 2 + H / 32 + j, ss);
+                    }
+                } else if (k == 0 && !*abort_lds) {
+                    // y is written only once every reducer of XCD 0 holds its final rows (a
+                    // count in that XCD's L2): an expired wait anywhere in the launch leaves y
+                    // -- and an x it aliases -- as it was
+                    uint32_t *done = a.ctl + STK_CTL_DONE;
+                    if (lane == 0)
+                        __hip_atomic_fetch_add((MOE_GLOBAL uint32_t *)done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (wait_count(done, (uint32_t)NJ, a.flags, a.spin_max, abort_lds))
+                        *(MOE_GLOBAL float *)(a.y + row) = x1;
                 }
             }
             if (li + 1 < n) {
@@ -507,7 +483,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 }
                 // pair words are tagged by being nonzero; the scales and sums of squares
                 // are LSB-tagged f32 words, which are nonzero too
-                poll_until_tagged<XP>(v, q, ld, a.flags, abort_lds, NonzeroTag{});
+                poll_until_tagged<XP>(v, q, ld, a.flags, a.spin_max, abort_lds, NonzeroTag{});
 #pragma unroll
                 for (int m = 0; m < XP; ++m) {
                     if (q[m] < XD) {
@@ -749,14 +725,14 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 float u = (as3[st] * sx) * subblock_idot(ak3[st], xh, xl);
                 g = inv * row_total<LPR1>(g);
                 u = inv * row_total<LPR1>(u);
-                if (g1 == LPR1_LAST) tag_store_local(hb + rowA + st * RPS1 + rr1, silu_rcp(g) * u);
+                if (g1 == LPR1_LAST && !*abort_lds) tag_store_local(hb + rowA + st * RPS1 + rr1, silu_rcp(g) * u);
             }
             int sah_i = 0, sal_i = 0;
             dword_idot(sak[0], sak[1], sxh0[0], sxh1[0], sxl0[0], sxl1[0], sah_i, sal_i);
             dword_idot(sak[2], sak[3], sxh0[1], sxh1[1], sxl0[1], sxl1[1], sah_i, sal_i);
             float sp = (sas * ssx) * __builtin_fmaf((float)sal_i, 1.0f / 256.0f, (float)sah_i);
             sp = inv * adjacent_sum<LPRS>(sp);
-            if (lane % LPRS == 0 && lane < NSA)
+            if (lane % LPRS == 0 && lane < NSA && !*abort_lds)
                 tag_store_local(hb + I + ((j * SRP + pA) * NCW + w) * 2 + mA, sp);
         }
         __builtin_amdgcn_s_setprio(0);
@@ -838,15 +814,19 @@ __global__ void k_stack_prep(StackArgs a, uint64_t words) {
 }
 
 // Per layer and XCD: h (3I words), the XCD's partial of every row (H), and x' as int8
-// pair words + chunk scales + per-workgroup sums of squares (H/2 + H/32 + H/64).
+// pair words + chunk scales + per-workgroup sums of squares (H/2 + H/32 + H/64); then the
+// STK_CTL_WORDS control words (tickets, done count).
 size_t stack_exchange_words(int H, int I, int n_layers) {
-    return (size_t)n_layers * STK_NX * (3 * (size_t)I + (size_t)H + (size_t)(H / 2 + H / 32 + H / 64));
+    return (size_t)n_layers * STK_NX * (3 * (size_t)I + (size_t)H + (size_t)(H / 2 + H / 32 + H / 64)) + STK_CTL_WORDS;
 }
 
 template <int H, int I>
 static hipError_t launch_stack_t(const StackArgs &a, hipStream_t st, KernelTimer *T) {
     const uint64_t words = stack_exchange_words(H, I, a.n_layers);
-    hipLaunchKernelGGL(k_stack_prep, dim3(max(512, a.n_layers)), dim3(256), 0, st, a, words);
+    {
+        TimedLaunch tl(T, MOE_K_STACK_PREP, st);
+        hipLaunchKernelGGL(k_stack_prep, dim3(max(512, a.n_layers)), dim3(256), 0, st, a, words);
+    }
     {
         TimedLaunch tl(T, MOE_K_DECODE_STACK, st);
         hipLaunchKernelGGL((k_decode_stack<H, I>), dim3(H / 8), dim3(64 * STK_WAVES), 0, st, a);

@@ -16,10 +16,12 @@
 
 using namespace moe;
 
+
 struct moe_ctx {
     int device = 0;
     moe_config cfg{};
-    std::vector<LayerPtrs> layers;
+    std::vector<LayerPtrs> layers;  // the caller's tables as bound (read only by the repacks)
+    std::vector<LayerPtrs> slayers; // split copies (decode kernels and the stack)
     std::vector<LayerPtrs> rlayers; // R16 repacked copies (prefill)
     std::vector<char> bound;
     uint8_t *rpk = nullptr;         // [n_layers][E+1][W1|W3|W2] R16, when m_max > MOE_DECODE_MAX_M
@@ -27,7 +29,7 @@ struct moe_ctx {
     void *arena = nullptr; // one device allocation, carved below
     size_t arena_bytes = 0;
     uint32_t *flags = nullptr;
-    float *hbuf = nullptr;       // decode h: [8][9][I] f32
+    float *hbuf = nullptr;       // decode path h scratch [72][I]
     _Float16 *xh = nullptr;      // [m_max][H]
     float *xinv = nullptr;       // [m_max]
     _Float16 *hh = nullptr;      // [9 m_max][I]
@@ -44,6 +46,7 @@ struct moe_ctx {
     uint16_t *srid = nullptr;    // decode stack: routing of every layer
     float *srw = nullptr;
     int stack_ok = 0;            // all stack workgroups fit on the device at once
+    uint32_t spin_max = STK_SPIN_DEFAULT; // decode stack: poll rounds before a wait expires
     KernelTimer timer;
 };
 
@@ -106,7 +109,8 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
     const int H = cfg->hidden, I = cfg->inter, E = cfg->n_experts;
     if (!shape_compiled(H, I))
         return fail(MOE_EUNSUPPORTED, "moe_create: hidden=%d inter=%d not compiled (2048x512, 512x256)", H, I);
-    if (E < MOE_TOPK || E > 1024) return fail(MOE_EINVAL, "moe_create: n_experts=%d outside 8..1024", E);
+    if (E < MOE_TOPK || E > MOE_MAX_EXPERTS)
+        return fail(MOE_EINVAL, "moe_create: n_experts=%d outside %d..%d", E, MOE_TOPK, MOE_MAX_EXPERTS);
     if (cfg->n_layers < 1 || cfg->n_layers > 4096)
         return fail(MOE_EINVAL, "moe_create: n_layers=%d outside 1..4096", cfg->n_layers);
     if (cfg->m_max < 1 || cfg->m_max > 65535)
@@ -124,6 +128,7 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
     c->device = device;
     c->cfg = *cfg;
     c->layers.resize(cfg->n_layers);
+    c->slayers.resize(cfg->n_layers);
     c->rlayers.resize(cfg->n_layers);
     c->bound.assign(cfg->n_layers, 0);
 
@@ -135,7 +140,7 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
         size_t bytes;
     } parts[] = {
         {(void **)&c->flags, 256},
-        {(void **)&c->hbuf, (size_t)MOE_DECODE_MAX_M * SLOTS * I * sizeof(float)},
+        {(void **)&c->hbuf, decode_scratch_floats(I) * sizeof(float)},
         {(void **)&c->xh, mm * H * 2},
         {(void **)&c->xinv, mm * 4},
         {(void **)&c->hh, SLOTS * mm * I * 2},
@@ -194,6 +199,8 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
     if (he == hipSuccess) he = hipMemset(c->dlayers, 0, (size_t)cfg->n_layers * sizeof(LayerPtrs));
     if (he == hipSuccess) he = hipDeviceSynchronize();
     if (he != hipSuccess) {
+        if (c->rpk) (void)hipFree(c->rpk);
+        if (c->spk) (void)hipFree(c->spk);
         (void)hipFree(c->arena);
         delete c;
         return hip_fail(he, "moe_create: clearing workspace");
@@ -264,6 +271,7 @@ moe_status moe_bind_layer(moe_ctx *ctx, int layer, const moe_layer_weights *lw) 
         S.sw2 = S.sw1 + 2 * mat;
         he = hipMemcpy(ctx->dlayers + layer, &S, sizeof(LayerPtrs), hipMemcpyHostToDevice);
         if (he != hipSuccess) return hip_fail(he, "moe_bind_layer: copying the layer table");
+        ctx->slayers[layer] = S;
     }
     if (ctx->rpk) {
         const size_t es = 3 * mat;
@@ -328,39 +336,58 @@ moe_status moe_bucket_fill(moe_ctx *ctx, const uint16_t *ids, const float *w, in
     return ok();
 }
 
-moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids, const float *w, int M,
-                   float *y, int flags, void *stream) {
-    if (!ctx) return fail(MOE_EINVAL, "moe_ffn: null context");
+// The checks and launches shared by moe_ffn and moe_ffn_route.  logits == NULL: ids/w are
+// inputs; otherwise the tokens are routed first and ids/w receive the routing.  scr is the
+// decode path's h scratch (decode_scratch_floats(inter)).
+static moe_status ffn_call(const char *fn, moe_ctx *ctx, int layer, const float *x, const float *logits,
+                           uint16_t *ids, float *w, int M, float *y, int flags, void *stream, float *hbuf) {
+    if (!ctx) return fail(MOE_EINVAL, "%s: null context", fn);
     if (layer < 0 || layer >= ctx->cfg.n_layers)
-        return fail(MOE_EINVAL, "moe_ffn: layer %d outside 0..%d", layer, ctx->cfg.n_layers - 1);
-    if (!ctx->bound[layer]) return fail(MOE_EINVAL, "moe_ffn: layer %d has no bound weights", layer);
-    if (M < 0 || M > ctx->cfg.m_max) return fail(MOE_EINVAL, "moe_ffn: M=%d outside 0..m_max=%d", M, ctx->cfg.m_max);
-    if (flags & ~(MOE_FFN_ACCUMULATE | MOE_FFN_RMSNORM)) return fail(MOE_EINVAL, "moe_ffn: unknown flags 0x%x", flags);
+        return fail(MOE_EINVAL, "%s: layer %d outside 0..%d", fn, layer, ctx->cfg.n_layers - 1);
+    if (!ctx->bound[layer]) return fail(MOE_EINVAL, "%s: layer %d has no bound weights", fn, layer);
+    if (M < 0 || M > ctx->cfg.m_max) return fail(MOE_EINVAL, "%s: M=%d outside 0..m_max=%d", fn, M, ctx->cfg.m_max);
+    if (flags & ~(MOE_FFN_ACCUMULATE | MOE_FFN_RMSNORM)) return fail(MOE_EINVAL, "%s: unknown flags 0x%x", fn, flags);
     if (M == 0) return ok();
-    if (!x || !ids || !w || !y) return fail(MOE_EINVAL, "moe_ffn: null argument");
-    if (!aligned16(x) || !aligned16(y)) return fail(MOE_EINVAL, "moe_ffn: x and y must be 16-byte aligned");
-    if (((uintptr_t)w & 3u) || ((uintptr_t)ids & 1u)) return fail(MOE_EINVAL, "moe_ffn: misaligned routing");
+    if (!x || !ids || !w || !y) return fail(MOE_EINVAL, "%s: null argument", fn);
+    if (!aligned16(x) || !aligned16(y)) return fail(MOE_EINVAL, "%s: x and y must be 16-byte aligned", fn);
+    if (((uintptr_t)w & 3u) || ((uintptr_t)ids & 1u) || ((uintptr_t)logits & 3u))
+        return fail(MOE_EINVAL, "%s: misaligned routing", fn);
     const int H = ctx->cfg.hidden, I = ctx->cfg.inter, E = ctx->cfg.n_experts;
-    const float c = ctx->cfg.wmode == MOE_W_REF ? 1.0f / 9.0f : 1.0f;
+    const int renorm = ctx->cfg.wmode == MOE_W_RENORM;
+    const float c = renorm ? 1.0f : 1.0f / 9.0f;
     hipStream_t st = as_stream(stream);
+    KernelTimer *T = timer_for(ctx, st);
     hipError_t he;
     if (M <= MOE_DECODE_MAX_M) {
+        // Routing inside the decode launch repeats the top-8 in every workgroup: it pays for a
+        // separate router launch only while M is small.
+        if (logits && M > DEC_ROUTE_IN_KERNEL_MAX_M) {
+            he = launch_router_topk(logits, M, E, renorm, ids, w, st, T);
+            if (he != hipSuccess) return fail(MOE_EHIP, "%s: router launch: %s", fn, hipGetErrorString(he));
+            logits = nullptr;
+        }
         DecodeArgs a{};
-        a.L = ctx->layers[layer];
+        a.L = ctx->slayers[layer];
         a.x = x;
+        a.logits = logits;
         a.ids = ids;
         a.w = w;
         a.y = y;
-        a.hbuf = ctx->hbuf;
+        a.hbuf = hbuf;
         a.flags = ctx->flags;
         a.M = M;
         a.E = E;
         a.accumulate = (flags & MOE_FFN_ACCUMULATE) ? 1 : 0;
         a.rmsnorm = (flags & MOE_FFN_RMSNORM) ? 1 : 0;
+        a.renorm = renorm;
         a.c = c;
-        he = launch_decode(H, I, a, st, timer_for(ctx, st));
-        if (he != hipSuccess) return hip_fail(he, "moe_ffn: decode launch");
+        he = launch_decode(H, I, a, st, T);
+        if (he != hipSuccess) return fail(MOE_EHIP, "%s: decode launch: %s", fn, hipGetErrorString(he));
         return ok();
+    }
+    if (logits) {
+        he = launch_router_topk(logits, M, E, renorm, ids, w, st, T);
+        if (he != hipSuccess) return fail(MOE_EHIP, "%s: router launch: %s", fn, hipGetErrorString(he));
     }
     BucketArgs b{};
     b.ids = ids;
@@ -376,7 +403,6 @@ moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids,
     b.tile_max = tile_max_for(M, E + 1);
     b.stile_max = stile_max_for(E + 1);
     b.flags = ctx->flags;
-    KernelTimer *T = timer_for(ctx, st);
     PrefillArgs p{};
     p.L = ctx->rlayers[layer];
     p.x = x;
@@ -398,8 +424,35 @@ moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids,
     p.stile_max = b.stile_max;
     p.c = c;
     he = launch_prefill(H, I, b, p, st, T);
-    if (he != hipSuccess) return hip_fail(he, "moe_ffn: prefill launch");
+    if (he != hipSuccess) return fail(MOE_EHIP, "%s: prefill launch: %s", fn, hipGetErrorString(he));
     return ok();
+}
+
+} // extern "C"
+
+namespace moe {
+moe_status ffn_with_scratch(const char *fn, moe_ctx *ctx, int layer, const float *x, const uint16_t *ids,
+                            const float *w, int M, float *y, int flags, void *stream, float *hbuf) {
+    return ffn_call(fn, ctx, layer, x, nullptr, const_cast<uint16_t *>(ids), const_cast<float *>(w), M, y, flags,
+                    stream, hbuf);
+}
+int ctx_device(const moe_ctx *ctx) { return ctx->device; }
+int ctx_inter(const moe_ctx *ctx) { return ctx->cfg.inter; }
+moe_status set_error(moe_status st, const char *msg) { return fail(st, "%s", msg); }
+} // namespace moe
+
+extern "C" {
+
+moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids, const float *w, int M,
+                   float *y, int flags, void *stream) {
+    return ffn_call("moe_ffn", ctx, layer, x, nullptr, const_cast<uint16_t *>(ids), const_cast<float *>(w), M, y,
+                    flags, stream, ctx ? ctx->hbuf : nullptr);
+}
+
+moe_status moe_ffn_route(moe_ctx *ctx, int layer, const float *x, const float *logits, int M, float *y,
+                         uint16_t *ids, float *w, int flags, void *stream) {
+    if (M > 0 && !logits) return fail(MOE_EINVAL, "moe_ffn_route: null logits");
+    return ffn_call("moe_ffn_route", ctx, layer, x, logits, ids, w, M, y, flags, stream, ctx ? ctx->hbuf : nullptr);
 }
 
 moe_status moe_decode_stack(moe_ctx *ctx, int layer0, int n_layers, const float *x, const float *logits,
@@ -431,9 +484,11 @@ moe_status moe_decode_stack(moe_ctx *ctx, int layer0, int n_layers, const float 
     a.hx = ctx->xtag;
     a.px = a.hx + (size_t)n_layers * 8 * 3 * I;
     a.xx = a.px + (size_t)n_layers * 8 * H;
+    a.ctl = a.hx + stack_exchange_words(ctx->cfg.hidden, ctx->cfg.inter, n_layers) - STK_CTL_WORDS;
     a.rid = ctx->srid;
     a.rwt = ctx->srw;
     a.flags = ctx->flags;
+    a.spin_max = ctx->spin_max;
     a.E = ctx->cfg.n_experts;
     a.rmsnorm = (flags & MOE_FFN_RMSNORM) ? 1 : 0;
     a.renorm = ctx->cfg.wmode == MOE_W_RENORM;
@@ -519,6 +574,20 @@ moe_status moe_device_flags(moe_ctx *ctx, void *stream, uint32_t *flags) {
     if (he == hipSuccess) he = hipDeviceSynchronize();
     if (he != hipSuccess) return hip_fail(he, "moe_device_flags: clearing");
     *flags = v;
+    return ok();
+}
+
+moe_status moe_device_flags_async(moe_ctx *ctx, uint32_t *dst, void *stream) {
+    if (!ctx || !dst) return fail(MOE_EINVAL, "moe_device_flags_async: null argument");
+    if ((uintptr_t)dst & 3u) return fail(MOE_EINVAL, "moe_device_flags_async: dst not 4-byte aligned");
+    hipError_t he = launch_flags_take(ctx->flags, dst, as_stream(stream));
+    if (he != hipSuccess) return hip_fail(he, "moe_device_flags_async: launch");
+    return ok();
+}
+
+moe_status moe_stack_spin_limit(moe_ctx *ctx, uint32_t polls) {
+    if (!ctx) return fail(MOE_EINVAL, "moe_stack_spin_limit: null context");
+    ctx->spin_max = polls;
     return ok();
 }
 

@@ -106,24 +106,100 @@ __device__ __forceinline__ float sub_scale(u32x2 hdr, int ib) {
     return d * (float)(ls - 32);
 }
 
-// 16 qs bytes of one sub-block against its 32 activations: sum_j kv[q_j] * x_j,
-// returned unscaled (caller multiplies by dl).  xs = sum of the 32 activations.
-__device__ __forceinline__ float subblock_dot(u32x4 qs, const float *xv, float xs) {
+// ---------------------------------------------------------------- int8 activation planes
+// The decode kernels read activations as two int8 planes per 32-element chunk c (one IQ4_XS
+// sub-block of K):
+//     x_i ~= s_c * (xh_i + xl_i / 256),  s_c = max_c |x| / 127,  xh = rint(x / s_c),
+//     xl = rint(256 * (x / s_c - xh)),
+// so a sub-block dot is two integer dot products of the signed codebook bytes
+// (v_dot4_i32_i8) with f32 scaling once per sub-block.  Error per element <= s_c / 512,
+// i.e. <= 1.6e-5 of the chunk's largest |x|.
+__device__ __forceinline__ float quant_ratio(float am) { return am > 1e-30f ? 127.0f * __builtin_amdgcn_rcpf(am) : 0.0f; }
+
+// LDS planes: chunk c at XQS * c: xh dwords 0..7 (elements 4d..4d+3), xl dwords 8..15,
+// 4 pad dwords (a lane's 128-bit reads of its chunk are conflict-free across lanes).
+constexpr int XQS = 20;
+
+// Four consecutive activations (ratio r = 127 / chunk max) -> their xh and xl bytes.
+__device__ __forceinline__ void quant4(f32x4 v, float r, uint32_t &h, uint32_t &l) {
+    h = 0u;
+    l = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float u = v[i] * r;
+        const float hi = fminf(fmaxf(rintf(u), -127.0f), 127.0f);
+        const float lo = fminf(fmaxf(rintf((u - hi) * 256.0f), -127.0f), 127.0f);
+        h |= ((uint32_t)(int)hi & 0xFFu) << (8 * i);
+        l |= ((uint32_t)(int)lo & 0xFFu) << (8 * i);
+    }
+}
+
+// One qs dword (weights 4d..4d+3 low nibbles, 16+4d.. high nibbles) against the planes'
+// dwords of those elements: xh_lo = dword d, xh_hi = dword 4+d (and the same for xl).
+// lo, hi: the signed codebook bytes of the dword's low and high nibbles (kv_signed8).
+__device__ __forceinline__ void dword_idot(uint32_t lo, uint32_t hi, uint32_t xh_lo, uint32_t xh_hi, uint32_t xl_lo,
+                                           uint32_t xl_hi, int &ah, int &al) {
+    ah = __builtin_amdgcn_sdot4((int)lo, (int)xh_lo, ah, false);
+    ah = __builtin_amdgcn_sdot4((int)hi, (int)xh_hi, ah, false);
+    al = __builtin_amdgcn_sdot4((int)lo, (int)xl_lo, al, false);
+    al = __builtin_amdgcn_sdot4((int)hi, (int)xl_hi, al, false);
+}
+
+// Whole sub-block, already looked up (kv[2d], kv[2d+1] = kv_signed8 of qs dword d), against
+// chunk planes xh[8], xl[8]: sum kv * (xh + xl/256), unscaled.
+__device__ __forceinline__ float subblock_idot(const uint32_t (&kv)[8], const uint32_t (&xh)[8],
+                                               const uint32_t (&xl)[8]) {
+    int ah = 0, al = 0;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) dword_idot(kv[2 * d], kv[2 * d + 1], xh[d], xh[4 + d], xl[d], xl[4 + d], ah, al);
+    return __builtin_fmaf((float)al, 1.0f / 256.0f, (float)ah);
+}
+
+// 8 weights of one qs dword -- weights 4d..4d+3 (low nibbles) and 16+4d..16+4d+3 (high
+// nibbles) of a sub-block, as the biased codebook bytes lo, hi (kv_biased8) -- against their
+// activations xl[0..3], xh[0..3]; unscaled.
+__device__ __forceinline__ float dword_dot(uint32_t lo, uint32_t hi, const float *xl, const float *xh) {
+    float a0 = ubyte(lo, 0) * xl[0], a1 = ubyte(lo, 1) * xl[1];
+    a0 = __builtin_fmaf(ubyte(lo, 2), xl[2], a0);
+    a1 = __builtin_fmaf(ubyte(lo, 3), xl[3], a1);
+    a0 = __builtin_fmaf(ubyte(hi, 0), xh[0], a0);
+    a1 = __builtin_fmaf(ubyte(hi, 1), xh[1], a1);
+    a0 = __builtin_fmaf(ubyte(hi, 2), xh[2], a0);
+    a1 = __builtin_fmaf(ubyte(hi, 3), xh[3], a1);
+    const float xs = ((xl[0] + xl[1]) + (xl[2] + xl[3])) + ((xh[0] + xh[1]) + (xh[2] + xh[3]));
+    return (a0 + a1) - 128.f * xs;
+}
+
+// Whole sub-block, already looked up (kv[2d], kv[2d+1] = kv_biased8 of qs dword d), against
+// its 32 activations xv; xs = their sum.  Unscaled.
+__device__ __forceinline__ float subblock_dot(const uint32_t (&kv)[8], const float (&xv)[32], float xs) {
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        uint32_t lo, hi;
-        kv_biased8(qs[w], lo, hi);
-        a0 = __builtin_fmaf(ubyte(lo, 0), xv[4 * w + 0], a0);
-        a1 = __builtin_fmaf(ubyte(lo, 1), xv[4 * w + 1], a1);
-        a2 = __builtin_fmaf(ubyte(lo, 2), xv[4 * w + 2], a2);
-        a3 = __builtin_fmaf(ubyte(lo, 3), xv[4 * w + 3], a3);
-        a0 = __builtin_fmaf(ubyte(hi, 0), xv[16 + 4 * w + 0], a0);
-        a1 = __builtin_fmaf(ubyte(hi, 1), xv[16 + 4 * w + 1], a1);
-        a2 = __builtin_fmaf(ubyte(hi, 2), xv[16 + 4 * w + 2], a2);
-        a3 = __builtin_fmaf(ubyte(hi, 3), xv[16 + 4 * w + 3], a3);
+    for (int d = 0; d < 4; ++d) {
+        const uint32_t lo = kv[2 * d], hi = kv[2 * d + 1];
+        a0 = __builtin_fmaf(ubyte(lo, 0), xv[4 * d + 0], a0);
+        a1 = __builtin_fmaf(ubyte(lo, 1), xv[4 * d + 1], a1);
+        a2 = __builtin_fmaf(ubyte(lo, 2), xv[4 * d + 2], a2);
+        a3 = __builtin_fmaf(ubyte(lo, 3), xv[4 * d + 3], a3);
+        a0 = __builtin_fmaf(ubyte(hi, 0), xv[16 + 4 * d + 0], a0);
+        a1 = __builtin_fmaf(ubyte(hi, 1), xv[16 + 4 * d + 1], a1);
+        a2 = __builtin_fmaf(ubyte(hi, 2), xv[16 + 4 * d + 2], a2);
+        a3 = __builtin_fmaf(ubyte(hi, 3), xv[16 + 4 * d + 3], a3);
     }
     return ((a0 + a1) + (a2 + a3)) - 128.f * xs;
+}
+
+// ---------------------------------------------------------------- split weight layout
+// The library's one resident copy of every bound matrix (k_repack_split): for a matrix of
+// `rows` rows of SBR super-blocks each,
+//     [rows * SBR qs blocks of 128 bytes, row-major] [rows * SBR headers of 8 bytes, same order]
+// -- the bytes of the GGML layout (136 per super-block) split in two, so that every 16-byte
+// qs read is aligned and a row's headers are 8*SBR contiguous bytes.
+template <int SBR>
+__device__ __forceinline__ uint32_t split_qs(int row, int sb) { return (uint32_t)((row * SBR + sb) * 128); }
+template <int ROWS, int SBR>
+__device__ __forceinline__ uint32_t split_hdr(int row, int sb) {
+    return (uint32_t)(ROWS * SBR * 128 + (row * SBR + sb) * 8);
 }
 
 // ---------------------------------------------------------------- cross-lane sums
@@ -207,6 +283,17 @@ __device__ __forceinline__ float wave_sum_last(float v) {
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false));
     return v;
 }
+
+// Total of each group of G lanes, complete in lane 63 for G = 64 (DPP only, no readlane on
+// the dependency chain) and in every lane otherwise.
+template <int G>
+__device__ __forceinline__ float row_total(float v) {
+    if constexpr (G == 64) return wave_sum_last(v);
+    else return group_sum<G>(v);
+}
+// The lane of a G-lane group that holds row_total's result.
+template <int G>
+constexpr int row_total_lane() { return G == 64 ? 63 : 0; }
 
 // Total over each group of G lanes (G = 64: wave-uniform value through readlane).
 template <int G>
@@ -341,6 +428,25 @@ __device__ __forceinline__ const uint8_t *expert_w(const uint8_t *base, uint64_t
     return e == E ? shared : base + (uint64_t)e * stride;
 }
 
+
+// ---------------------------------------------------------------- cross-XCD exchange
+// Each XCD has its own L2.  A word published for workgroups on other XCDs is stored at agent
+// scope, which writes through the producer's L2; consumers read it with system-scope loads,
+// which miss their own L2 and see memory.  The buffer starts zeroed and a published f32
+// carries its mantissa LSB forced to 1 (<= 1 ulp), so "LSB set" marks a written word.
+__device__ __forceinline__ void tag_store(uint32_t *p, float v) {
+    __hip_atomic_store((MOE_GLOBAL uint32_t *)p, __builtin_bit_cast(uint32_t, v) | 1u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+// 16 bytes as two relaxed 8-byte system-scope atomic loads (atomic, so a poll loop re-issues
+// them every round; relaxed, so the compiler does not wait for each one).
+__device__ __forceinline__ u32x4 remote_quad(const u32x4 *p) {
+    const MOE_GLOBAL uint64_t *g = (const MOE_GLOBAL uint64_t *)p;
+    const uint64_t lo = __hip_atomic_load(g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    const uint64_t hi = __hip_atomic_load(g + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    return u32x4{(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
+}
+__device__ __forceinline__ uint32_t quad_tagged(u32x4 v) { return v[0] & v[1] & v[2] & v[3] & 1u; }
 
 // Workgroup barrier for LDS traffic only.  __syncthreads() also waits for every global
 // load the wave has in flight (the barrier's release fence needs vmcnt(0)), which would

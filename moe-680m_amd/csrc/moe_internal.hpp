@@ -23,16 +23,20 @@ constexpr int PF_NGU_WIDE = 128;
 constexpr int PF_SPLIT_MAX_M = 768;
 
 struct DecodeArgs {
-    LayerPtrs L;
+    LayerPtrs L;          // split copy of the layer (k_repack_split)
     const float *x;
-    const uint16_t *ids;
-    const float *w;
+    const float *logits;  // non-null: the gate/up launch routes the tokens and publishes ids, w
+    uint16_t *ids;        // [M][9] (read, or written when logits is set)
+    float *w;             // [M][9]
     float *y;
-    float *hbuf;     // [M][9][I] f32
-    uint32_t *flags; // sticky device flags
-    int M, E, accumulate, rmsnorm;
+    float *hbuf;          // [9M][I] f32 h scratch
+    uint32_t *flags;      // sticky device flags
+    int M, E, accumulate, rmsnorm, renorm;
     float c;
 };
+constexpr int DEC_ROUTE_IN_KERNEL_MAX_M = 2; // moe_ffn_route: larger M launches the router first
+// Floats of the decode path's h scratch for inter size I.
+inline size_t decode_scratch_floats(int I) { return (size_t)MOE_DECODE_MAX_M * SLOTS * I; }
 
 struct BucketArgs {
     const uint16_t *ids;
@@ -84,12 +88,20 @@ struct StackArgs {
     uint32_t *hx;            // [n_layers][8 XCDs][3I] h of each XCD's rows (shared rows as partials)
     uint32_t *px;            // [n_layers][8 XCDs][H] each XCD's partial of the layer output
     uint32_t *xx;            // [n_layers][8 XCDs][H] x_{l+1}, one copy per XCD
+    uint32_t *ctl;           // control words: per-XCD workgroup tickets, the done count
     uint16_t *rid;           // [n_layers][9] routing of every layer (k_stack_prep)
     float *rwt;              // [n_layers][9]
     uint32_t *flags;         // [0] sticky device flags, [1] abort word
+    uint32_t spin_max;       // poll rounds before a bounded wait expires
     int E, rmsnorm, renorm;
     float c;
 };
+
+constexpr uint32_t STK_SPIN_DEFAULT = 1u << 16;
+// Control words after the stack's exchange buffers: one workgroup ticket counter per XCD,
+// then the count of last-layer reducers done (cleared with the buffers before every launch).
+constexpr int STK_CTL_WORDS = 16;
+constexpr int STK_CTL_DONE = 8;
 
 // Optional per-kernel timing (moe_timing_enable): each launch is bracketed by two HIP
 // events recorded on the launch's own stream.  Events are created when timing is enabled,
@@ -139,6 +151,8 @@ hipError_t launch_decode(int H, int I, const DecodeArgs &a, hipStream_t st, Kern
 // Bucket fill and prep (one launch), gate/up, down, combine.
 hipError_t launch_prefill(int H, int I, const BucketArgs &b, const PrefillArgs &a, hipStream_t st, KernelTimer *T);
 hipError_t launch_stack(int H, int I, const StackArgs &a, hipStream_t st, KernelTimer *T);
+// *dst = the sticky device flags, which are cleared (one thread, stream ordered).
+hipError_t launch_flags_take(uint32_t *flags, uint32_t *dst, hipStream_t st);
 hipError_t stack_occupancy(int H, int I, int *blocks_per_cu);
 int stack_blocks(int H);
 size_t stack_exchange_words(int H, int I, int n_layers);
@@ -148,4 +162,16 @@ size_t stack_exchange_words(int H, int I, int n_layers);
 inline int tile_max_for(int M, int E1) { return (9 * M + PF_BM - 1) / PF_BM + E1; }
 inline int stile_max_for(int E1) { return E1; }
 
+} // namespace moe
+
+// Internal services of moe_api.hip for the entry points defined in other files.
+namespace moe {
+// moe_ffn with ids/w given, its decode path (M <= MOE_DECODE_MAX_M) using hbuf
+// (decode_scratch_floats(inter)) as its h scratch.
+moe_status ffn_with_scratch(const char *fn, moe_ctx *ctx, int layer, const float *x, const uint16_t *ids,
+                            const float *w, int M, float *y, int flags, void *stream, float *hbuf);
+int ctx_device(const moe_ctx *ctx);
+int ctx_inter(const moe_ctx *ctx);
+// Sets the calling thread's moe_last_error message and returns st.
+moe_status set_error(moe_status st, const char *msg);
 } // namespace moe

@@ -249,6 +249,13 @@ static const uint8_t *expert_ptr(const uint8_t *base, size_t stride, const uint8
  * is scaled by its weight times the dispatch scale (1/9 there, c here) and summed onto
  * the hidden state; the shared expert enters with weight 1.  Experts are evaluated once
  * each for all tokens that chose them, then summed per token in slot order. */
+/* Slot s of a token repeats an id of one of its earlier slots (such a slot is dropped). */
+static int repeats_earlier_slot(const uint16_t *tok_ids, int s) {
+    for (int s2 = 0; s2 < s; ++s2)
+        if (tok_ids[s2] == tok_ids[s]) return 1;
+    return 0;
+}
+
 void orc_moe_ffn(const orc_layer *L, int H, int I, int E, const float *x, const uint16_t *ids,
                  const float *w, int M, double c, int flags, float *y) {
     int nb = E + 1;
@@ -282,7 +289,7 @@ void orc_moe_ffn(const orc_layer *L, int H, int I, int E, const float *x, const 
             orc_dequant_iq4xs(expert_ptr(L->w2, L->w2_stride, L->shared_w2, e, E), nw / ORC_QK, W2);
             for (int t = 0; t < M; ++t)
                 for (int s = 0; s < ORC_SLOTS; ++s)
-                    if (ids[(size_t)t * ORC_SLOTS + s] == e)
+                    if (ids[(size_t)t * ORC_SLOTS + s] == e && !repeats_earlier_slot(ids + (size_t)t * ORC_SLOTS, s))
                         expert_rows(W1, W3, W2, H, I, xin + (size_t)t * H, h,
                                     ys + ((size_t)t * ORC_SLOTS + s) * H);
         }

@@ -75,7 +75,9 @@ typedef struct {
  *   y_e = W2_e (silu(W1_e xin) * (W3_e xin))
  *   out = c * sum_{s<9} w[s] * y_{ids[s]}
  *   y   = flags&ACCUMULATE ? y + out : out
- * x and y may alias.  Accumulation in f64. */
+ * A slot whose id is above E, or repeats an id of an earlier slot of the same token, adds
+ * nothing (the rule the product's bucket fill and decode kernels apply; the reference's
+ * router never produces either).  x and y may alias.  Accumulation in f64. */
 void orc_moe_ffn(const orc_layer *L, int H, int I, int E, const float *x, const uint16_t *ids,
                  const float *w, int M, double c, int flags, float *y);
 

@@ -27,11 +27,12 @@ def elementwise_err(got, ref):
 class Layer:
     """One generated layer, resident on the GPU, with a lazily copied host view."""
 
-    def __init__(self, pkg, orc, seed, hidden=H, inter=I, n_experts=E):
+    def __init__(self, pkg, orc, seed, hidden=H, inter=I, n_experts=E, dev=None):
+        """The layer of generator stream `seed`, or the packed device buffer `dev`."""
         import torch
         self.pkg, self.orc = pkg, orc
         self.H, self.I, self.E = hidden, inter, n_experts
-        self.dev = pkg.gen_layer(hidden, inter, n_experts, seed)
+        self.dev = dev if dev is not None else pkg.gen_layer(hidden, inter, n_experts, seed)
         torch.cuda.synchronize()
         self._host = None
 

@@ -52,7 +52,8 @@ def test_host_validation_without_gpu(pkg):
     h = vp()
     assert L.moe_create(0, ctypes.byref(cfg), ctypes.byref(h)) == pkg.MOE_EUNSUPPORTED
     assert b"not compiled" in L.moe_last_error()
-    for bad in [pkg._Config(2048, 512, 4, 1, 16, 0), pkg._Config(2048, 512, 256, 0, 16, 0),
+    for bad in [pkg._Config(2048, 512, 4, 1, 16, 0), pkg._Config(2048, 512, 257, 1, 16, 0),
+                pkg._Config(2048, 512, 1024, 1, 16, 0), pkg._Config(2048, 512, 256, 0, 16, 0),
                 pkg._Config(2048, 512, 256, 1, 0, 0), pkg._Config(2048, 512, 256, 1, 70000, 0),
                 pkg._Config(2048, 512, 256, 1, 16, 7)]:
         assert L.moe_create(0, ctypes.byref(bad), ctypes.byref(h)) == pkg.MOE_EINVAL

@@ -107,6 +107,84 @@ def test_config2_forty_layers(gpu, orc, full):
     assert err <= TOL
 
 
+def test_config2_forty_layers_renorm(gpu, orc, full):
+    """Config 2 under BASELINE's renormalised top-8 (c = 1): a context in MOE_W_RENORM bound
+    to the same 40 layers."""
+    import torch
+    _, layers = full
+    ctx = gpu.Context(H, I, E, 40, 8, gpu.W_RENORM)
+    try:
+        for l, buf in enumerate(layers):
+            ctx.bind_packed(l, buf)
+        log("config 2 RENORM: 40-layer stack, M=1")
+        x = gpu.gen_normal(H, gpu.seed_for(2, 0, gpu.TAG_X) + 1)
+        logits = gpu.gen_logits(40, E, gpu.seed_for(2, 0, gpu.TAG_L) + 1)
+        ids = torch.empty((40, 9), dtype=torch.uint16, device="cuda")
+        w = torch.empty((40, 9), dtype=torch.float32, device="cuda")
+        y = ctx.decode_stack(0, x, logits, ids=ids, w=w)
+        torch.cuda.synchronize()
+        assert ctx.device_flags() == 0
+        ref, rid, rw = oracle_chain(orc, gpu, layers, H, I, E, x.cpu().numpy(), logits.cpu().numpy(), mode=1)
+        assert np.array_equal(ids.cpu().numpy(), rid)
+        assert np.allclose(w.cpu().numpy(), rw, rtol=1e-5)
+        assert np.allclose(w.cpu().numpy()[:, :8].sum(axis=1), 1.0, rtol=1e-5)
+        err = normwise_err(y.cpu().numpy(), ref)
+        log(f"  normwise err {err:.3e}")
+        assert err <= TOL
+    finally:
+        ctx.close()
+
+
+def test_stack_timeout_leaves_x(gpu, full):
+    """A host-forced timeout (spin limit 0: every wait not satisfied at its first look
+    expires): TIMEOUT is raised, every workgroup exits, and the in-place x is untouched.
+    The same context then runs normally again."""
+    import torch
+    ctx, _ = full
+    n = 4
+    x = gpu.gen_normal(H, 1101)
+    logits = gpu.gen_logits(n, E, 1102)
+    x0 = x.clone()
+    good = ctx.decode_stack(0, x0, logits).clone()
+    torch.cuda.synchronize()
+    assert ctx.device_flags() == 0
+    ctx.stack_spin_limit(0)
+    try:
+        log("stack with spin limit 0 (forced timeout), in place")
+        ctx.decode_stack(0, x, logits, y=x)
+        torch.cuda.synchronize()
+        f = ctx.device_flags()
+        assert f & gpu.DEVFLAG_TIMEOUT
+        assert torch.equal(x.view(torch.int32), x0.view(torch.int32))
+    finally:
+        ctx.stack_spin_limit(65536)
+    ctx.decode_stack(0, x, logits, y=x)
+    torch.cuda.synchronize()
+    assert ctx.device_flags() == 0
+    assert torch.equal(x.view(torch.int32), good.view(torch.int32))
+
+
+def test_device_flags_async(gpu, full):
+    """moe_device_flags_async moves and clears the sticky flags in stream order, into device
+    memory or pinned host memory, without a host synchronisation."""
+    import torch
+    ctx, _ = full
+    dst = torch.full((1,), 0x7F, dtype=torch.int32, device="cuda")
+    pinned = torch.full((1,), 0x7F, dtype=torch.int32).pin_memory()
+    ctx.device_flags_async(dst)
+    ctx.stack_spin_limit(0)
+    try:
+        ctx.decode_stack(0, gpu.gen_normal(H, 1201), gpu.gen_logits(2, E, 1202))
+    finally:
+        ctx.stack_spin_limit(65536)
+    ctx.device_flags_async(pinned)
+    ctx.device_flags_async(dst)   # cleared by the previous move
+    torch.cuda.synchronize()
+    assert int(pinned[0]) & gpu.DEVFLAG_TIMEOUT
+    assert int(dst[0]) == 0
+    assert ctx.device_flags() == 0
+
+
 def test_stack_matches_per_layer_path(gpu, full):
     import torch
     ctx, _ = full

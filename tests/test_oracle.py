@@ -254,6 +254,27 @@ def test_moe_ffn_composition(orc):
         assert np.allclose(got_norm[t], c * refn, rtol=1e-5, atol=1e-5 * np.abs(refn).max())
 
 
+def test_moe_ffn_drops_repeated_and_bad_slots(orc):
+    """A slot naming an id above E, or an id its token already named in an earlier slot, adds
+    nothing: the result equals the composition of single experts over the remaining slots."""
+    H, I, E = 512, 256, 16
+    L = small_layer(orc, H, I, E)
+    rng = np.random.default_rng(19)
+    x = rng.standard_normal((2, H)).astype(np.float32)
+    ids, w = orc.router_topk(rng.standard_normal((2, E)).astype(np.float32), 0)
+    ids[0, 6] = ids[0, 1]      # repeat of slot 1: dropped
+    ids[1, 3] = E + 5          # out of range: dropped
+    ids[1, 7] = ids[1, 0]      # repeat of slot 0: dropped
+    got = orc.moe_ffn(L, x, ids, w, 1.0, 0)
+    kept = {0: [s for s in range(9) if s != 6], 1: [s for s in range(9) if s not in (3, 7)]}
+    for t in range(2):
+        ref = np.zeros(H)
+        for s in kept[t]:
+            w1, w3, w2 = L.expert(int(ids[t, s]))
+            ref += w[t, s] * orc.expert_forward(w1, w3, w2, H, I, x[t])
+        assert np.allclose(got[t], ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
+
+
 # ---------------------------------------------------------------- generator
 
 def test_generator_math(orc):
