@@ -135,6 +135,16 @@ moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids,
 moe_status moe_ffn_route(moe_ctx *ctx, int layer, const float *x, const float *logits, int M,
                          float *y, uint16_t *ids, float *w, int flags, void *stream);
 
+/* moe_ffn for M <= MOE_DECODE_MAX_M whose h scratch is a static device array of the library
+ * (147,456 bytes per GPU, held until the process ends) instead of the context's workspace:
+ * nothing in this call allocates, frees or calls an allocating library routine.  No
+ * counterpart in the reference; it is for callers that cannot allocate device memory
+ * (work under graph capture, tight serving loops, harnesses that forbid allocation).
+ * Refuses M > MOE_DECODE_MAX_M and inter > 512 (MOE_EINVAL / MOE_EUNSUPPORTED).  Every call
+ * on a GPU shares that GPU's array: calls that overlap on one GPU (two streams) race. */
+moe_status moe_ffn_noalloc(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids, const float *w,
+                           int M, float *y, int flags, void *stream);
+
 /* One token (M = 1) through n_layers consecutive MoE layers in one persistent launch:
  *   for l in layer0 .. layer0+n_layers-1:
  *       (ids_l, w_l) = top8(softmax(logits[l - layer0]))      (as moe_router_topk)

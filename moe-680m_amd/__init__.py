@@ -40,7 +40,7 @@ DEVFLAG_BAD_ID, DEVFLAG_DUP_ID, DEVFLAG_TIMEOUT = 1, 2, 4
 # Every symbol include/moe_ffn.h declares (checked by the CPU test suite).
 EXPORTS = (
     "moe_create", "moe_destroy", "moe_bind_layer", "moe_router_topk", "moe_bucket_fill",
-    "moe_ffn", "moe_ffn_route", "moe_decode_stack", "moe_dequant_iq4xs", "moe_device_flags",
+    "moe_ffn", "moe_ffn_route", "moe_ffn_noalloc", "moe_decode_stack", "moe_dequant_iq4xs", "moe_device_flags",
     "moe_device_flags_async", "moe_stack_spin_limit", "moe_last_error",
     "moe_timing_enable", "moe_timing_read",
     "moe_gen_iq4xs", "moe_gen_normal", "moe_gen_logits",
@@ -89,6 +89,7 @@ def lib():
         "moe_bucket_fill": [vp, vp, vp, i, vp, vp, vp, vp],
         "moe_ffn": [vp, i, vp, vp, vp, i, vp, i, vp],
         "moe_ffn_route": [vp, i, vp, vp, i, vp, vp, vp, i, vp],
+        "moe_ffn_noalloc": [vp, i, vp, vp, vp, i, vp, i, vp],
         "moe_decode_stack": [vp, i, i, vp, vp, vp, vp, vp, i, vp],
         "moe_dequant_iq4xs": [vp, sz, vp, vp],
         "moe_device_flags": [vp, vp, ctypes.POINTER(ctypes.c_uint32)],
@@ -223,6 +224,15 @@ class Context:
         flags = (FFN_ACCUMULATE if accumulate else 0) | (FFN_RMSNORM if rmsnorm else 0)
         _check(lib().moe_ffn(self._h, layer, _ptr(x), _ptr(ids), _ptr(w), M, _ptr(y), flags,
                              _stream(stream)))
+        return y
+
+    def ffn_noalloc(self, layer, x, ids, w, y=None, accumulate=False, rmsnorm=False, stream=None):
+        """moe_ffn_noalloc: the decode path (M <= 8) with the library's static scratch."""
+        if y is None:
+            y = torch.empty_like(x)
+        flags = (FFN_ACCUMULATE if accumulate else 0) | (FFN_RMSNORM if rmsnorm else 0)
+        _check(lib().moe_ffn_noalloc(self._h, layer, _ptr(x), _ptr(ids), _ptr(w), x.shape[0], _ptr(y), flags,
+                                     _stream(stream)))
         return y
 
     def ffn_route(self, layer, x, logits, y=None, ids=None, w=None, accumulate=False, rmsnorm=False,
