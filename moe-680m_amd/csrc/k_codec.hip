@@ -200,48 +200,8 @@ __global__ __launch_bounds__(256) void k_gen_logits(float *__restrict__ dst, int
 }
 
 // ---------------------------------------------------------------- launchers
-// ---------------------------------------------------------------- R16 repack (prefill)
-// One-time copy of a bound layer into the layout the prefill GEMMs read: within every group
-// of 16 consecutive rows of a matrix, each super-block column (16 rows x 136 bytes) becomes
-// one 2176-byte block  [16 headers of 8 bytes, row order] [qs half 0: 1024 B] [qs half 1]
-// where qs half h holds, at byte 16*L (lane L = 16g + n), dword g of sub-blocks 4h..4h+3
-// of row n -- the 16 bytes that lane needs for four MFMA K-steps.  The bytes are those of
-// the natural layout, permuted; the decoded values do not change.
-__global__ __launch_bounds__(256) void k_repack_r16(const uint8_t *__restrict__ src, uint64_t src_stride,
-                                                    const uint8_t *__restrict__ shared, uint8_t *__restrict__ dst,
-                                                    uint64_t dst_stride, int E, int rowb, int sbr) {
-    const int e = blockIdx.y;
-    const int grp = blockIdx.x / sbr, sb = blockIdx.x % sbr;
-    const uint8_t *m = (e == E) ? shared : src + (uint64_t)e * src_stride;
-    const uint8_t *in = m + (uint64_t)grp * 16 * rowb + (uint64_t)sb * SB_BYTES;
-    uint32_t *out = reinterpret_cast<uint32_t *>(dst + (uint64_t)e * dst_stride + (uint64_t)grp * 16 * rowb +
-                                                 (uint64_t)sb * 16 * SB_BYTES);
-    for (int o = threadIdx.x; o < 16 * SB_BYTES / 4; o += blockDim.x) {
-        uint32_t off; // byte offset inside the source super-block column of row `row`
-        int row;
-        if (o < 32) {
-            row = o >> 1;
-            off = 4u * (o & 1);
-        } else {
-            const int q = o - 32, h = q >> 8, lane = (q & 255) >> 2, j = q & 3;
-            row = lane & 15;
-            off = 8u + 16u * (4 * h + j) + 4u * (lane >> 4);
-        }
-        out[o] = *reinterpret_cast<const uint32_t *>(in + (uint64_t)row * rowb + off);
-    }
-}
-
-hipError_t launch_repack_r16(const void *src, uint64_t src_stride, const void *shared, void *dst, uint64_t dst_stride,
-                             int E, int rows, int cols, hipStream_t st) {
-    const int sbr = cols / QK, rowb = sbr * SB_BYTES;
-    dim3 grid((unsigned)(rows / 16 * sbr), (unsigned)(E + 1));
-    hipLaunchKernelGGL(k_repack_r16, grid, dim3(256), 0, st, (const uint8_t *)src, src_stride, (const uint8_t *)shared,
-                       (uint8_t *)dst, dst_stride, E, rowb, sbr);
-    return hipGetLastError();
-}
-
-// ---------------------------------------------------------------- split repack (decode stack)
-// One-time copy of a bound layer into the layout the decode stack reads.  Per matrix of nsb
+// ---------------------------------------------------------------- split repack
+// One-time copy of a bound layer into the layout every kernel family reads.  Per matrix of nsb
 // super-blocks (row-major: rows x super-blocks per row):
 //     [nsb x 128-byte qs] [nsb x 8-byte header (d, scales_h, scales_l)]
 // -- the bytes of the natural layout (136 per super-block) split in two, so that every

@@ -33,9 +33,10 @@
 //
 // Weight decode into a B fragment.  v_mfma_f32_16x16x32_f16 takes from lane (g, n) of the
 // B operand 8 K values of column n; the K order inside one 32-wide MFMA step is free as long
-// as A uses the same one.  Lane group g takes qs bytes 4g..4g+3 of the sub-block: low
-// nibbles are K = 4g..4g+3, high nibbles K = 16+4g..16+4g+3, so one 32-bit qs load gives
-// the lane its 8 weights.  The activations are stored in that order (perm32 below).
+// as A uses the same one.  A lane takes one qs dword d of a sub-block: low nibbles are
+// K = 4d..4d+3, high nibbles K = 16+4d..16+4d+3 of that sub-block, so one 32-bit qs word
+// gives the lane its 8 weights (which sub-block and dword each lane group takes in each
+// step: wstage_load).  The activations are stored in that order (perm32 below).
 // Codebook bytes come from the v_perm lookup (kv + 128, see moe_device.hpp); a second
 // v_perm places each byte under an 0x64 high byte, which is the f16 1024 + byte, exactly;
 // one packed f16 add of -1152 gives kv exactly and one packed multiply applies dl.
@@ -198,11 +199,23 @@ __device__ __forceinline__ const T *uniform_ptr(const T *p) {
 }
 
 // Raw IQ4_XS data of one K stage (PF_KC = 128 K = 4 sub-blocks, half a super-block) for NR
-// 16-row weight groups, read from the R16 layout (k_repack_r16): lane (g, n) gets the
-// header of row n and, in one 16-byte load, dword g of each of the stage's 4 sub-blocks of
-// row n -- exactly its B-fragment bytes for 4 MFMA K-steps.  A wave's load is 1 KB of
-// contiguous memory.  Stages live in a ring of 4 so each is requested three stages ahead.
-constexpr int R16_BLOCK = 16 * SB_BYTES; // one super-block column of a 16-row group
+// 16-row weight groups, read from the split layout (k_repack_split): lane (g, n) gets the
+// header of row n and, in one 16-byte load, the 16 qs bytes of sub-block 4h + g of row n (h =
+// the stage's half of the super-block).  MFMA K-step ks of the stage then takes dword ks of
+// every lane's sub-block: lane group g supplies K positions 32 g + 8 ks .. + 7 of the stage (in
+// the 32-block permuted K order of xh), and its sub-block scale is the same in all 4 steps.
+// Stages live in a ring so each is requested a few stages ahead.
+struct WRows {
+    const uint8_t *q; // qs of the group's first row (matrix base + row * SBR * 128)
+    const uint8_t *h; // header of the group's first row (header array + row * SBR * 8)
+};
+
+// Rows row0 .. row0 + 15 of a split matrix of `rows` rows and SBR super-blocks per row.
+template <int SBR>
+__device__ __forceinline__ WRows split_rows(const uint8_t *m, int rows, int row0) {
+    return WRows{uniform_ptr(m + (size_t)row0 * SBR * 128),
+                 uniform_ptr(m + (size_t)rows * SBR * 128 + (size_t)row0 * SBR * 8)};
+}
 
 template <int NR>
 struct WStage {
@@ -210,33 +223,25 @@ struct WStage {
     u32x4 q[NR];
 };
 
-// groups[r]: first byte of the 16-row group (= matrix base + first row * row bytes).
-template <int NR>
-__device__ __forceinline__ void wstage_load(WStage<NR> &s, const uint8_t *const (&groups)[NR], int ch, int lane) {
+template <int SBR, int NR>
+__device__ __forceinline__ void wstage_load(WStage<NR> &s, const WRows (&groups)[NR], int ch, int lane) {
     const int sb = ch >> 1, h = ch & 1;
-    // unsigned lane offsets (zero-extended) on a wave-uniform block base that goes through
-    // readfirstlane: the loads then take an SGPR base and one 32-bit lane offset; past the
-    // immediate-offset range the compiler would otherwise rebuild a 64-bit VGPR address
-    const uint32_t oh = 8u * (uint32_t)(lane & 15), oq = 16u * (uint32_t)lane;
+    // unsigned lane offsets (zero-extended) on wave-uniform bases that go through
+    // readfirstlane: the loads then take an SGPR base and one 32-bit lane offset
+    const uint32_t n = (uint32_t)(lane & 15), g = (uint32_t)(lane >> 4);
+    const uint32_t oh = n * (SBR * 8u), oq = n * (SBR * 128u) + 16u * g;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-        const uint8_t *blk = uniform_ptr(groups[r] + (size_t)sb * R16_BLOCK);
-        s.hdr[r] = ldg<u32x2>(blk + oh);
-        s.q[r] = ldg<u32x4>(blk + 128 + 1024 * h + oq);
+        s.hdr[r] = ldg<u32x2>(uniform_ptr(groups[r].h + (size_t)sb * 8) + oh);
+        s.q[r] = ldg<u32x4>(uniform_ptr(groups[r].q + (size_t)sb * 128 + 64 * h) + oq);
     }
 }
 
-// dl pairs of the stage's 4 sub-blocks: lane group g computes sub-block kb0 + g and every
-// lane fetches the one of K-step ks from lane ks*16 + n.
+// dl pair of the lane's sub-block (4h + g of the stage's super-block) for each row group.
 template <int NR>
-__device__ __forceinline__ void wstage_dl(const WStage<NR> &s, int ch, int g, int n, uint32_t (&dl)[NR][4]) {
-    const int kb0 = (ch & 1) * 4;
+__device__ __forceinline__ void wstage_dl(const WStage<NR> &s, int ch, int g, uint32_t (&dl)[NR]) {
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
-        const uint32_t mine = dl_pair(s.hdr[r], kb0 + g);
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) dl[r][ks] = (uint32_t)__builtin_amdgcn_ds_bpermute((ks * 16 + n) * 4, (int)mine);
-    }
+    for (int r = 0; r < NR; ++r) dl[r] = dl_pair(s.hdr[r], 4 * (ch & 1) + g);
 }
 
 // One stage of MFMAs: NR B fragments (dequantized here) against the MT M-tiles of the LDS
@@ -244,17 +249,17 @@ __device__ __forceinline__ void wstage_dl(const WStage<NR> &s, int ch, int g, in
 // (which covers their LDS latency), then the MFMAs, reading the next A fragment two M-tiles
 // ahead (A fragments are held two at a time, not MT at a time: fewer live registers).
 template <int NR, int MT, int LK>
-__device__ __forceinline__ void stage_mfma(const WStage<NR> &s0, const uint32_t (&dl)[NR][4], const _Float16 *As,
+__device__ __forceinline__ void stage_mfma(const WStage<NR> &s0, const uint32_t (&dl)[NR], const _Float16 *As,
                                            int n, int g, f32x4 (&acc)[MT][NR]) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-        const _Float16 *ap = As + n * LK + 32 * ks + 8 * g;
+        const _Float16 *ap = As + n * LK + 32 * g + 8 * ks;
         u32x4 av[2];
 #pragma unroll
         for (int mt = 0; mt < (MT < 2 ? MT : 2); ++mt) av[mt] = *reinterpret_cast<const u32x4 *>(ap + 16 * mt * LK);
         u32x4 b[NR];
 #pragma unroll
-        for (int r = 0; r < NR; ++r) b[r] = dq8_f16(s0.q[r][ks], dl[r][ks]);
+        for (int r = 0; r < NR; ++r) b[r] = dq8_f16(s0.q[r][ks], dl[r]);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             const u32x4 cur = av[mt & 1];
@@ -295,19 +300,19 @@ __device__ __forceinline__ void static_for(F &&f) {
 }
 
 // Weight ring of RD register stages: the prologue requests stages 0..RD-2.
-template <int NCH, int RD, int NR>
-__device__ __forceinline__ void wring_prologue(WStage<NR> (&ws)[RD], const uint8_t *const (&rows)[NR], int lane) {
+template <int NCH, int RD, int SBR, int NR>
+__device__ __forceinline__ void wring_prologue(WStage<NR> (&ws)[RD], const WRows (&rows)[NR], int lane) {
 #pragma unroll
     for (int c = 0; c < RD - 1; ++c) {
-        if (c < NCH) wstage_load(ws[c], rows, c, lane);
+        if (c < NCH) wstage_load<SBR>(ws[c], rows, c, lane);
         __builtin_amdgcn_sched_barrier(0);
     }
 }
 
 // stage_a(c) moves chunk c of A into LDS; chunk 0 is expected in LDS on entry (its loads were
 // issued before the weight ring's, so waiting for them did not wait for the weights).
-template <int NCH, int RD, int NR, int MT, typename StageA>
-__device__ __forceinline__ void gemm_resident(WStage<NR> (&ws)[RD], const uint8_t *const (&rows)[NR],
+template <int NCH, int RD, int SBR, int NR, int MT, typename StageA>
+__device__ __forceinline__ void gemm_resident(WStage<NR> (&ws)[RD], const WRows (&rows)[NR],
                                               const _Float16 *As, int n, int g, f32x4 (&acc)[MT][NR],
                                               StageA stage_a) {
     constexpr int KCH = pf_kch<NCH, MT>();
@@ -320,13 +325,13 @@ __device__ __forceinline__ void gemm_resident(WStage<NR> (&ws)[RD], const uint8_
             stage_a(ch / KCH);
             lds_barrier();
         }
-        uint32_t dl[NR][4];
-        wstage_dl(ws[S], ch, g, n, dl);
+        uint32_t dl[NR];
+        wstage_dl(ws[S], ch, g, dl);
         stage_mfma<NR, MT, LK>(ws[S], dl, As + (ch % KCH) * PF_KC, n, g, acc);
         // keep the scheduler from moving loads across stages: each stage's weights are
         // requested RD-1 stages ahead, in the order they are consumed
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (ch + RD - 1 < NCH) wstage_load(ws[(ch + RD - 1) % RD], rows, ch + RD - 1, n + 16 * g);
+        if constexpr (ch + RD - 1 < NCH) wstage_load<SBR>(ws[(ch + RD - 1) % RD], rows, ch + RD - 1, n + 16 * g);
         __builtin_amdgcn_sched_barrier(0);
     });
 }
@@ -336,8 +341,8 @@ __device__ __forceinline__ void gemm_resident(WStage<NR> (&ws)[RD], const uint8_
 // columns; chunk boundaries (KCH even) fall at the same loop index for both.  Half-length
 // work items: gate/up's items then fill the 512 workgroup slots in three rounds of half
 // length instead of two full ones (at M = 512, ~1140 items against ~570 of twice the length).
-template <int NCH, int RD, int NR, int MT, typename StageA>
-__device__ __forceinline__ void gemm_resident_split(WStage<NR> (&ws)[RD], const uint8_t *const (&rows)[NR],
+template <int NCH, int RD, int SBR, int NR, int MT, typename StageA>
+__device__ __forceinline__ void gemm_resident_split(WStage<NR> (&ws)[RD], const WRows (&rows)[NR],
                                                     const _Float16 *As, int n, int g, int p,
                                                     f32x4 (&acc)[MT][NR], StageA stage_a) {
     constexpr int KCH = pf_kch<NCH, MT>();
@@ -352,11 +357,11 @@ __device__ __forceinline__ void gemm_resident_split(WStage<NR> (&ws)[RD], const 
             lds_barrier();
         }
         const int ch = ch0 + p;
-        uint32_t dl[NR][4];
-        wstage_dl(ws[S], ch, g, n, dl);
+        uint32_t dl[NR];
+        wstage_dl(ws[S], ch, g, dl);
         stage_mfma<NR, MT, LK>(ws[S], dl, As + (ch0 % KCH + p) * PF_KC, n, g, acc);
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (c + RD - 1 < NC2) wstage_load(ws[(c + RD - 1) % RD], rows, 2 * (c + RD - 1) + p, n + 16 * g);
+        if constexpr (c + RD - 1 < NC2) wstage_load<SBR>(ws[(c + RD - 1) % RD], rows, 2 * (c + RD - 1) + p, n + 16 * g);
         __builtin_amdgcn_sched_barrier(0);
     });
 }
@@ -384,7 +389,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
     constexpr int NGU = SPLIT ? PF_NGU : PF_NGU_WIDE;
     static_assert(NGU == 16 * PF_WAVES / (SPLIT ? 2 : 1), "16 columns per wave (pair)");
     constexpr int NCH = H / PF_KC;
-    constexpr int ROWB = (H / QK) * SB_BYTES;
+    constexpr int SBR = H / QK;
     static_assert(H % QK == 0 && I % NGU == 0 && PF_KC * 2 == QK, "gate/up shape");
     __shared__ __attribute__((aligned(16))) _Float16 As[PF_AS_HALVES];
     __shared__ uint32_t rowmax[PF_BM];
@@ -407,8 +412,8 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
     }
     lds_barrier();
     // Weights: rows c0 + n of W1 (gate) and W3 (up).
-    const uint8_t *rows[2] = {uniform_ptr(expert_w(a.L.w1, a.L.s1, a.L.sw1, e, a.E) + (size_t)c0 * ROWB),
-                              uniform_ptr(expert_w(a.L.w3, a.L.s3, a.L.sw3, e, a.E) + (size_t)c0 * ROWB)};
+    const WRows rows[2] = {split_rows<SBR>(expert_w(a.L.w1, a.L.s1, a.L.sw1, e, a.E), I, c0),
+                           split_rows<SBR>(expert_w(a.L.w3, a.L.s3, a.L.sw3, e, a.E), I, c0)};
 
     by_mtiles(nrows, [&](auto MTc) __attribute__((always_inline)) {
         constexpr int MT = decltype(MTc)::value;
@@ -443,11 +448,11 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
         if constexpr (SPLIT) {
 #pragma unroll
             for (int c = 0; c < RD - 1; ++c) {
-                if (c < NCH / 2) wstage_load(ws[c], rows, 2 * c + p, lane);
+                if (c < NCH / 2) wstage_load<SBR>(ws[c], rows, 2 * c + p, lane);
                 __builtin_amdgcn_sched_barrier(0);
             }
         } else {
-            wring_prologue<NCH, RD>(ws, rows, lane);
+            wring_prologue<NCH, RD, SBR>(ws, rows, lane);
         }
         store_a(0, PER);
         lds_barrier();
@@ -464,7 +469,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
             store_a(HALF, PER);
         };
         if constexpr (SPLIT) {
-            gemm_resident_split<NCH, RD, 2, MT>(ws, rows, As, n, g, p, acc, stage_a);
+            gemm_resident_split<NCH, RD, SBR, 2, MT>(ws, rows, As, n, g, p, acc, stage_a);
             // the odd-stage wave hands its sums to its partner through the (now free) A chunk
             lds_barrier();
             f32x4 *red = reinterpret_cast<f32x4 *>(As);
@@ -483,7 +488,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
                     for (int r = 0; r < 2; ++r) acc[mt][r] += red[((cw * MT + mt) * 2 + r) * 64 + lane];
             }
         } else {
-            gemm_resident<NCH, RD, 2, MT>(ws, rows, As, n, g, acc, stage_a);
+            gemm_resident<NCH, RD, SBR, 2, MT>(ws, rows, As, n, g, acc, stage_a);
         }
 
         // epilogue (even-stage waves): h = silu(g) * u with the token scale undone; per-row max|h| of the block,
@@ -525,7 +530,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
 template <int H, int I, int NGU>
 __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
     constexpr int NTW = 2, NCH = I / PF_KC;
-    constexpr int ROWB = (I / QK) * SB_BYTES;
+    constexpr int SBR = I / QK;
     constexpr int NHB = I / NGU; // h max blocks per row
     constexpr int BPR = I / 32;      // 32-blocks per row
     static_assert(I % QK == 0 && H % PF_ND == 0 && PF_KC * 2 == QK, "down shape");
@@ -540,7 +545,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
     const int n = lane & 15, g = lane >> 4;
     const int r0 = blockIdx.x * PF_ND + wv * 32; // this wave's output rows r0 .. r0+31
     const uint8_t *w2 = expert_w(a.L.w2, a.L.s2, a.L.sw2, e, a.E);
-    const uint8_t *rows[NTW] = {uniform_ptr(w2 + (size_t)r0 * ROWB), uniform_ptr(w2 + (size_t)(r0 + 16) * ROWB)};
+    const WRows rows[NTW] = {split_rows<SBR>(w2, H, r0), split_rows<SBR>(w2, H, r0 + 16)};
 
     by_mtiles(nrows, [&](auto MTc) __attribute__((always_inline)) {
         constexpr int MT = decltype(MTc)::value;
@@ -569,7 +574,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
         }
         constexpr int RD = 4; // weight ring depth: three stages ahead
         WStage<NTW> ws[RD];
-        wring_prologue<NCH, RD>(ws, rows, lane);
+        wring_prologue<NCH, RD, SBR>(ws, rows, lane);
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
             const int it = j * 64 * PF_WAVES + tid;
@@ -605,7 +610,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
         for (int i = 0; i < MT; ++i)
 #pragma unroll
             for (int t = 0; t < NTW; ++t) acc[i][t] = f32x4{0, 0, 0, 0};
-        gemm_resident<NCH, RD, NTW, MT>(ws, rows, As, n, g, acc, [](int) {});
+        gemm_resident<NCH, RD, SBR, NTW, MT>(ws, rows, As, n, g, acc, [](int) {});
 
         // epilogue: the scaled results through LDS (As is free once every wave is done with
         // it), so that each lane stores whole 16-byte row pieces -- 8 store instructions per

@@ -20,12 +20,9 @@ using namespace moe;
 struct moe_ctx {
     int device = 0;
     moe_config cfg{};
-    std::vector<LayerPtrs> layers;  // the caller's tables as bound (read only by the repacks)
-    std::vector<LayerPtrs> slayers; // split copies (decode kernels and the stack)
-    std::vector<LayerPtrs> rlayers; // R16 repacked copies (prefill)
+    std::vector<LayerPtrs> slayers; // the library's split copy of each bound layer (every kernel)
     std::vector<char> bound;
-    uint8_t *rpk = nullptr;         // [n_layers][E+1][W1|W3|W2] R16, when m_max > MOE_DECODE_MAX_M
-    uint8_t *spk = nullptr;         // [n_layers][E+1][W1|W3|W2] split layout (decode stack)
+    uint8_t *spk = nullptr;         // [n_layers][E+1][W1|W3|W2] split layout: the one resident copy
     void *arena = nullptr; // one device allocation, carved below
     size_t arena_bytes = 0;
     uint32_t *flags = nullptr;
@@ -127,9 +124,7 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
     if (!c) return fail(MOE_ENOMEM, "moe_create: host allocation");
     c->device = device;
     c->cfg = *cfg;
-    c->layers.resize(cfg->n_layers);
     c->slayers.resize(cfg->n_layers);
-    c->rlayers.resize(cfg->n_layers);
     c->bound.assign(cfg->n_layers, 0);
 
     const size_t mm = (size_t)cfg->m_max, E1 = (size_t)E + 1;
@@ -170,28 +165,16 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
         *p.dst = (char *)c->arena + off;
         off += align_up(p.bytes, 256);
     }
-    if (cfg->m_max > MOE_DECODE_MAX_M) {
-        // the prefill GEMMs read a repacked copy of every bound layer (see k_repack_r16)
-        const size_t mat = (size_t)H * I / QK * SB_BYTES;
-        const size_t rbytes = (size_t)cfg->n_layers * E1 * 3 * mat;
-        he = hipMalloc((void **)&c->rpk, rbytes);
-        if (he != hipSuccess) {
-            (void)hipFree(c->arena);
-            delete c;
-            return fail(MOE_ENOMEM, "moe_create: hipMalloc(%zu) for the prefill weight layout: %s", rbytes,
-                        hipGetErrorString(he));
-        }
-    }
     {
-        // the decode stack reads a split copy of every bound layer (see k_repack_split)
+        // every kernel family reads the library's own split copy of each bound layer
+        // (k_repack_split); the caller's buffers are not read after moe_bind_layer returns
         const size_t mat = (size_t)H * I / QK * SB_BYTES;
         const size_t sbytes = (size_t)cfg->n_layers * E1 * 3 * mat;
         he = hipMalloc((void **)&c->spk, sbytes);
         if (he != hipSuccess) {
-            if (c->rpk) (void)hipFree(c->rpk);
             (void)hipFree(c->arena);
             delete c;
-            return fail(MOE_ENOMEM, "moe_create: hipMalloc(%zu) for the decode-stack weight layout: %s", sbytes,
+            return fail(MOE_ENOMEM, "moe_create: hipMalloc(%zu) for the weight copies: %s", sbytes,
                         hipGetErrorString(he));
         }
     }
@@ -199,7 +182,6 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
     if (he == hipSuccess) he = hipMemset(c->dlayers, 0, (size_t)cfg->n_layers * sizeof(LayerPtrs));
     if (he == hipSuccess) he = hipDeviceSynchronize();
     if (he != hipSuccess) {
-        if (c->rpk) (void)hipFree(c->rpk);
         if (c->spk) (void)hipFree(c->spk);
         (void)hipFree(c->arena);
         delete c;
@@ -219,7 +201,6 @@ moe_status moe_destroy(moe_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipDeviceSynchronize();
     timer_free(ctx->timer);
-    if (ctx->rpk) (void)hipFree(ctx->rpk);
     if (ctx->spk) (void)hipFree(ctx->spk);
     hipError_t he = hipFree(ctx->arena);
     delete ctx;
@@ -260,7 +241,7 @@ moe_status moe_bind_layer(moe_ctx *ctx, int layer, const moe_layer_weights *lw) 
         if (he == hipSuccess) he = launch_repack_split(L.w3, L.s3, L.sw3, base + mat, es, E, I, H, nullptr);
         if (he == hipSuccess) he = launch_repack_split(L.w2, L.s2, L.sw2, base + 2 * mat, es, E, H, I, nullptr);
         if (he == hipSuccess) he = hipDeviceSynchronize();
-        if (he != hipSuccess) return hip_fail(he, "moe_bind_layer: repacking for the decode stack");
+        if (he != hipSuccess) return hip_fail(he, "moe_bind_layer: repacking into the split layout");
         LayerPtrs S;
         S.w1 = base;
         S.w3 = base + mat;
@@ -273,25 +254,6 @@ moe_status moe_bind_layer(moe_ctx *ctx, int layer, const moe_layer_weights *lw) 
         if (he != hipSuccess) return hip_fail(he, "moe_bind_layer: copying the layer table");
         ctx->slayers[layer] = S;
     }
-    if (ctx->rpk) {
-        const size_t es = 3 * mat;
-        uint8_t *base = ctx->rpk + (size_t)layer * (E + 1) * es;
-        he = launch_repack_r16(L.w1, L.s1, L.sw1, base, es, E, I, H, nullptr);
-        if (he == hipSuccess) he = launch_repack_r16(L.w3, L.s3, L.sw3, base + mat, es, E, I, H, nullptr);
-        if (he == hipSuccess) he = launch_repack_r16(L.w2, L.s2, L.sw2, base + 2 * mat, es, E, H, I, nullptr);
-        if (he == hipSuccess) he = hipDeviceSynchronize();
-        if (he != hipSuccess) return hip_fail(he, "moe_bind_layer: repacking for prefill");
-        LayerPtrs R;
-        R.w1 = base;
-        R.w3 = base + mat;
-        R.w2 = base + 2 * mat;
-        R.s1 = R.s3 = R.s2 = es;
-        R.sw1 = base + (size_t)E * es;
-        R.sw3 = R.sw1 + mat;
-        R.sw2 = R.sw1 + 2 * mat;
-        ctx->rlayers[layer] = R;
-    }
-    ctx->layers[layer] = L;
     ctx->bound[layer] = 1;
     return ok();
 }
@@ -404,7 +366,7 @@ static moe_status ffn_call(const char *fn, moe_ctx *ctx, int layer, const float 
     b.stile_max = stile_max_for(E + 1);
     b.flags = ctx->flags;
     PrefillArgs p{};
-    p.L = ctx->rlayers[layer];
+    p.L = ctx->slayers[layer];
     p.x = x;
     p.xh = ctx->xh;
     p.xinv = ctx->xinv;

@@ -52,8 +52,7 @@ struct BucketArgs {
     uint32_t *flags;
 };
 
-// Prefill reads the R16 repacked copy of a layer (k_repack_r16): same matrix bases and
-// sizes as the natural layout, bytes permuted within every 16-row group.
+// Prefill reads the split copy of a layer (k_repack_split), as the decode kernels do.
 struct PrefillArgs {
     LayerPtrs L;
     const float *x;
@@ -132,8 +131,6 @@ struct TimedLaunch {
 };
 
 hipError_t launch_dequant(const void *blocks, uint64_t n_sb, float *out, hipStream_t st);
-hipError_t launch_repack_r16(const void *src, uint64_t src_stride, const void *shared, void *dst, uint64_t dst_stride,
-                             int E, int rows, int cols, hipStream_t st);
 // Decode-stack copy of a layer: per matrix, the 128-byte qs of every super-block, then its
 // 8-byte headers, same order (k_repack_split).
 hipError_t launch_repack_split(const void *src, uint64_t src_stride, const void *shared, void *dst,
