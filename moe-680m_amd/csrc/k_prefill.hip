@@ -175,19 +175,28 @@ __device__ __forceinline__ void prep_token(const PrefillArgs &a, int t, int lane
     if (lane == 0) a.xinv[t] = inv_s;
 }
 
-// The chain's first launch: workgroup 0 runs the bucket fill (one CU, latency-bound), the
-// others the prep of 16 tokens each (one wave per token) -- independent work that would
-// otherwise be two launches in a row.
-template <int H, bool KEEP>
-__global__ __launch_bounds__(BF_THREADS) void k_pf_route_prep(BucketArgs b, PrefillArgs a) {
+// The chain's first launch: the first workgroups run the bucket fill, the others the prep of
+// one token per wave -- independent work that would otherwise be two launches in a row.
+// ONE: 1024-thread workgroups, workgroup 0 runs the one-workgroup fill (M <= 1024), the
+// others 16 tokens each; else 64-thread workgroups, the first ceil(M/64) count one chunk
+// each (the scan and the scatter follow as their own launches), the others one token each.
+template <int H, bool ONE>
+__global__ __launch_bounds__(ONE ? BF_THREADS : BF_CHUNK_THREADS) void k_pf_route_prep(BucketArgs b, PrefillArgs a) {
     static_assert(H % (32 * 64) == 0 || H == 512, "prep shape");
-    if (blockIdx.x == 0) {
-        bucket_fill_body<KEEP>(b);
+    constexpr int TPW = (ONE ? BF_THREADS : BF_CHUNK_THREADS) / 64; // tokens per prep workgroup
+    const int nfill = ONE ? 1 : (b.M + 63) / 64;
+    if ((int)blockIdx.x < nfill) {
+        if constexpr (ONE) bucket_fill_one_wg(b);
+        else bucket_count_chunk(b, blockIdx.x);
         return;
     }
-    const int t = (blockIdx.x - 1) * (BF_THREADS / 64) + (int)(threadIdx.x >> 6);
+    const int t = ((int)blockIdx.x - nfill) * TPW + (int)(threadIdx.x >> 6);
     if (t < a.M) prep_token<H>(a, t, threadIdx.x & 63); // whole waves
 }
+
+// The many-workgroup fill's scan and scatter (after k_pf_route_prep's counts).
+__global__ __launch_bounds__(BF_THREADS) void k_pf_bucket_scan(BucketArgs b) { bucket_scan_wg(b); }
+__global__ __launch_bounds__(BF_CHUNK_THREADS) void k_pf_scatter(BucketArgs b) { bucket_scatter_chunk(b, blockIdx.x); }
 
 // ---------------------------------------------------------------- shared pipeline pieces
 // A wave-uniform pointer moved to SGPRs (loads then take a scalar base and a lane offset).
@@ -665,11 +674,17 @@ template <int H, int I>
 static hipError_t launch_prefill_t(const BucketArgs &b, const PrefillArgs &a, hipStream_t st, KernelTimer *T) {
     {
         TimedLaunch tl(T, MOE_K_BUCKET_FILL, st);
-        const bool keep = (b.M + 63) / 64 <= bucket_cw(b.E1);
-        const dim3 grid((unsigned)(1 + (a.M + BF_THREADS / 64 - 1) / (BF_THREADS / 64)));
-        const size_t smem = bucket_smem(b.E1, keep);
-        if (keep) hipLaunchKernelGGL((k_pf_route_prep<H, true>), grid, dim3(BF_THREADS), smem, st, b, a);
-        else hipLaunchKernelGGL((k_pf_route_prep<H, false>), grid, dim3(BF_THREADS), smem, st, b, a);
+        if (bucket_one_wg(b.M, b.E1)) {
+            const dim3 grid((unsigned)(1 + (a.M + BF_THREADS / 64 - 1) / (BF_THREADS / 64)));
+            hipLaunchKernelGGL((k_pf_route_prep<H, true>), grid, dim3(BF_THREADS), bucket_smem(b.E1, true), st, b, a);
+        } else {
+            const int nch = (b.M + 63) / 64;
+            const size_t smem = bucket_chunk_smem(b.E1);
+            hipLaunchKernelGGL((k_pf_route_prep<H, false>), dim3((unsigned)(nch + a.M)), dim3(BF_CHUNK_THREADS), smem,
+                               st, b, a);
+            hipLaunchKernelGGL(k_pf_bucket_scan, dim3(1), dim3(BF_THREADS), bucket_smem(b.E1, false), st, b);
+            hipLaunchKernelGGL(k_pf_scatter, dim3((unsigned)nch), dim3(BF_CHUNK_THREADS), smem, st, b);
+        }
     }
     // one launch over both tile lists (full and big remainder tiles, then small remainders)
     const int ntiles = a.tile_max + a.stile_max;

@@ -52,19 +52,22 @@ hipError_t launch_router_topk(const float *logits, int M, int E, int renorm, uin
 }
 
 // ---------------------------------------------------------------- bucket fill
-template <bool KEEP>
-__global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) {
-    bucket_fill_body<KEEP>(a);
-}
+__global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) { bucket_fill_one_wg(a); }
+__global__ __launch_bounds__(BF_CHUNK_THREADS) void k_bucket_count(BucketArgs a) { bucket_count_chunk(a, blockIdx.x); }
+__global__ __launch_bounds__(BF_THREADS) void k_bucket_scan(BucketArgs a) { bucket_scan_wg(a); }
+__global__ __launch_bounds__(BF_CHUNK_THREADS) void k_bucket_scatter(BucketArgs a) { bucket_scatter_chunk(a, blockIdx.x); }
 
 hipError_t launch_bucket_fill(const BucketArgs &a, hipStream_t st, KernelTimer *T) {
     if (a.M < 0) return hipSuccess; // M == 0 still writes all-zero ranges
-    const bool keep = (a.M + 63) / 64 <= bucket_cw(a.E1);
-    const size_t smem = bucket_smem(a.E1, keep);
-    {
-        TimedLaunch tl(T, MOE_K_BUCKET_FILL, st);
-        if (keep) hipLaunchKernelGGL(k_bucket_fill<true>, dim3(1), dim3(BF_THREADS), smem, st, a);
-        else hipLaunchKernelGGL(k_bucket_fill<false>, dim3(1), dim3(BF_THREADS), smem, st, a);
+    TimedLaunch tl(T, MOE_K_BUCKET_FILL, st);
+    if (bucket_one_wg(a.M, a.E1)) {
+        hipLaunchKernelGGL(k_bucket_fill, dim3(1), dim3(BF_THREADS), bucket_smem(a.E1, true), st, a);
+    } else {
+        const dim3 grid((unsigned)((a.M + 63) / 64));
+        const size_t smem = bucket_chunk_smem(a.E1);
+        hipLaunchKernelGGL(k_bucket_count, grid, dim3(BF_CHUNK_THREADS), smem, st, a);
+        hipLaunchKernelGGL(k_bucket_scan, dim3(1), dim3(BF_THREADS), bucket_smem(a.E1, false), st, a);
+        hipLaunchKernelGGL(k_bucket_scatter, grid, dim3(BF_CHUNK_THREADS), smem, st, a);
     }
     return hipGetLastError();
 }

@@ -46,7 +46,7 @@ struct BucketArgs {
     uint16_t *sorted_tok; // [9M]
     float *sorted_w;      // [9M]
     uint32_t *pos;        // [M][9] or null
-    uint32_t *chunk_cnt;  // workspace [ceil(M/64)][E1]
+    uint32_t *chunk_cnt;  // workspace: ceil(M/64) * E1 chunk counts
     Tile *tiles;          // [tile_max] big tiles (full first), then [stile_max] small tiles; or null
     int tile_max, stile_max;
     uint32_t *flags;

@@ -59,7 +59,7 @@ def test_router_empty(gpu, ctx):
     assert ids.numel() == 0
 
 
-@pytest.mark.parametrize("M", [0, 1, 9, 63, 64, 65, 512, 4096])
+@pytest.mark.parametrize("M", [0, 1, 9, 63, 64, 65, 512, 1024, 1025, 3000, 4096])
 def test_bucket_fill_matches_oracle(gpu, orc, ctx, M):
     import torch
     log(f"bucket fill M={M}")
