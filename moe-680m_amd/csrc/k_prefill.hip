@@ -21,10 +21,10 @@
 //   down:    per (tile, 256 output rows) the same over K = inter (one chunk); each column
 //            block of the f16 h rows is rescaled to the power of two of the row's max (a
 //            factor 2^-j, exact for normal f16) as it is staged; epilogue multiplies by
-//            2^-s_row * c * slot weight and writes one f32 row per slot through LDS (16-byte
-//            pieces per lane);
-//   combine: y_t (+)= sum over t's 9 slots in slot order -- deterministic, no atomics, no
-//            f16 read-modify-write race (the reference's w2_scatter.comp:77-86 RMW).
+//            2^-s_row * c * slot weight and writes each slot row as f16, every 32 columns
+//            scaled by the power of two of their max (the exponent kept in a byte);
+//   combine: y_t (+)= sum over t's 9 slots in slot order, in f32 -- deterministic, no
+//            atomics, no f16 read-modify-write race (the reference's w2_scatter.comp:77-86).
 //
 // Operand precision: the weight dl*kv (exact in f32, up to 23 significant bits) is rounded
 // once to f16 (dl itself is rounded to f16 first: <= 2^-10 relative in all); activations
@@ -106,6 +106,16 @@ __device__ __forceinline__ float pow2_scale(float mx, float *inv) {
     sh = sh > 120 ? 120 : (sh < -120 ? -120 : sh);
     *inv = ldexpf(1.0f, -sh);
     return ldexpf(1.0f, sh);
+}
+
+// The exponent of pow2_scale: max * 2^sh in [2^14, 2^15) (0 when max is 0 or not finite),
+// sh in [-120, 120].
+__device__ __forceinline__ int pow2_shift(float mx) {
+    if (!(mx > 0.0f) || !(mx < INFINITY)) return 0;
+    int e = 0;
+    (void)frexpf(mx, &e);
+    const int sh = 15 - e;
+    return sh > 120 ? 120 : (sh < -120 ? -120 : sh);
 }
 
 template <int CTRL>
@@ -621,52 +631,83 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
             for (int t = 0; t < NTW; ++t) acc[i][t] = f32x4{0, 0, 0, 0};
         gemm_resident<NCH, RD, SBR, NTW, MT>(ws, rows, As, n, g, acc, [](int) {});
 
-        // epilogue: the scaled results through LDS (As is free once every wave is done with
-        // it), so that each lane stores whole 16-byte row pieces -- 8 store instructions per
-        // wave for 64 rows instead of 32 four-byte ones
-        static_assert(PF_WAVES * PF_BM * 32 * 4 <= PF_AS_HALVES * 2, "transpose fits in As");
+        // epilogue: v = c * w * 2^-s_row * acc per slot row; each row's 32 values of this
+        // wave are stored as f16 times a power of two 2^sh that puts their max in
+        // [2^14, 2^15), sh kept beside them (one byte per row and 32 columns), column n and
+        // 16 + n of the block side by side (stored position 2n, 2n + 1).  Through LDS
+        // (As is free once every wave is done with it) so that each lane stores whole 16-byte
+        // row pieces.
+        static_assert(PF_WAVES * PF_BM * 32 * 2 <= PF_AS_HALVES * 2, "transpose fits in As");
         lds_barrier();
-        float *T = reinterpret_cast<float *>(As) + wv * (16 * MT * 32); // [16 MT rows][32 columns]
+        _Float16 *T = As + wv * (16 * MT * 32); // [16 MT rows][32 columns]
+        const int cb = r0 / 32;                 // this wave's 32-column block
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int m = 16 * mt + 4 * g + i;
                 const float sc = m < nrows ? a.c * a.sorted_w[row0 + m] * s_inv[m] : 0.0f;
+                float v[NTW], mx = 0.0f;
 #pragma unroll
-                for (int t = 0; t < NTW; ++t) T[m * 32 + 16 * t + n] = sc * acc[mt][t][i];
+                for (int t = 0; t < NTW; ++t) {
+                    v[t] = sc * acc[mt][t][i];
+                    mx = fmaxf(mx, fabsf(v[t]));
+                }
+                mx = max16(mx); // the row's 32 columns: 16 lanes x NTW
+                const int sh = pow2_shift(mx);
+                static_assert(NTW == 2, "columns n and 16 + n of a block stored as one f16 pair");
+                *reinterpret_cast<uint32_t *>(T + m * 32 + 2 * n) =
+                    pack_f16x2(__builtin_amdgcn_ldexpf(v[0], sh), __builtin_amdgcn_ldexpf(v[1], sh));
+                if (n == 0 && m < nrows) a.pexp[(size_t)(row0 + m) * (H / 32) + cb] = (int8_t)sh;
             }
         // lanes read what other lanes of this wave wrote: LDS keeps a wave's accesses in
         // order, the compiler must too
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-        for (int k = lane; k < 16 * MT * 8; k += 64) {
-            const int r = k >> 3, q = k & 7;
+        for (int k = lane; k < 16 * MT * 4; k += 64) {
+            const int r = k >> 2, q = k & 3;
             if (r < nrows)
-                *reinterpret_cast<f32x4 *>(a.part + (size_t)(row0 + r) * H + r0 + 4 * q) =
-                    *reinterpret_cast<const f32x4 *>(T + r * 32 + 4 * q);
+                *reinterpret_cast<u32x4 *>(a.part + (size_t)(row0 + r) * H + r0 + 8 * q) =
+                    *reinterpret_cast<const u32x4 *>(T + r * 32 + 8 * q);
         }
     });
 }
 
 // ---------------------------------------------------------------- combine
-// y_t (+)= sum_{s=0..8} part[pos[t][s]]; restates the weighted sum that the reference's
-// w2_scatter epilogue accumulates into the hidden state (shaders/w2_scatter.comp:77-86),
-// in a fixed order.
+// y_t (+)= sum_{s=0..8} part[pos[t][s]] * 2^-pexp; restates the weighted sum that the
+// reference's w2_scatter epilogue accumulates into the hidden state
+// (shaders/w2_scatter.comp:77-86), in a fixed order, in f32.  A thread owns 8 stored f16:
+// in 32-column block b, pairs j = 4 (c8 % 4) .. + 3, i.e. columns 32 b + j and 32 b + 16 + j.
 template <int H>
 __global__ __launch_bounds__(256) void k_pf_combine(PrefillArgs a) {
     const int t = blockIdx.x;
     uint32_t ps[SLOTS];
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) ps[s] = a.pos[(size_t)t * SLOTS + s];
-    for (int n4 = threadIdx.x; n4 < H / 4; n4 += 256) {
-        f32x4 acc = f32x4{0, 0, 0, 0};
+    for (int c8 = threadIdx.x; c8 < H / 8; c8 += 256) {
+        u32x4 q[SLOTS];
+        float f[SLOTS];
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) { // all loads first; dropped slots read slot 0 and add 0
+            const uint32_t p = ps[s] != 0xFFFFFFFFu ? ps[s] : 0u;
+            q[s] = ldg<u32x4>(a.part + (size_t)p * H + 8 * c8);
+            f[s] = ps[s] != 0xFFFFFFFFu ? __builtin_amdgcn_ldexpf(1.0f, -(int)a.pexp[(size_t)p * (H / 32) + c8 / 4]) : 0.0f;
+        }
+        f32x4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
 #pragma unroll
         for (int s = 0; s < SLOTS; ++s)
-            if (ps[s] != 0xFFFFFFFFu) acc += ldg<f32x4>(a.part + (size_t)ps[s] * H + 4 * n4);
-        f32x4 *yp = reinterpret_cast<f32x4 *>(a.y + (size_t)t * H) + n4;
-        f32x4 base = a.accumulate ? *yp : f32x4{0, 0, 0, 0};
-        *yp = base + acc;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f16x2 h2 = __builtin_bit_cast(f16x2, (uint32_t)q[s][j]);
+                lo[j] += (float)h2[0] * f[s];
+                hi[j] += (float)h2[1] * f[s];
+            }
+        float *yb = a.y + (size_t)t * H + 32 * (c8 / 4) + 4 * (c8 % 4);
+        f32x4 *y0 = reinterpret_cast<f32x4 *>(yb), *y1 = reinterpret_cast<f32x4 *>(yb + 16);
+        const f32x4 b0 = a.accumulate ? *y0 : f32x4{0, 0, 0, 0};
+        const f32x4 b1 = a.accumulate ? *y1 : f32x4{0, 0, 0, 0};
+        *y0 = b0 + lo;
+        *y1 = b1 + hi;
     }
 }
 

@@ -31,7 +31,8 @@ struct moe_ctx {
     float *xinv = nullptr;       // [m_max]
     _Float16 *hh = nullptr;      // [9 m_max][I]
     float *hmax = nullptr;       // [9 m_max][I/PF_NGU]
-    float *part = nullptr;       // [9 m_max][H]
+    _Float16 *part = nullptr;    // [9 m_max][H]
+    int8_t *pexp = nullptr;      // [9 m_max][H/32]
     uint32_t *ranges = nullptr;  // [E+2]
     uint16_t *stok = nullptr;    // [9 m_max]
     float *sw = nullptr;         // [9 m_max]
@@ -140,7 +141,8 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
         {(void **)&c->xinv, mm * 4},
         {(void **)&c->hh, SLOTS * mm * I * 2},
         {(void **)&c->hmax, SLOTS * mm * (I / PF_NGU) * 4},
-        {(void **)&c->part, SLOTS * mm * H * sizeof(float)},
+        {(void **)&c->part, SLOTS * mm * H * 2},
+        {(void **)&c->pexp, SLOTS * mm * (H / 32)},
         {(void **)&c->ranges, (E1 + 1) * 4},
         {(void **)&c->stok, SLOTS * mm * 2},
         {(void **)&c->sw, SLOTS * mm * 4},
@@ -377,6 +379,7 @@ static moe_status ffn_call(const char *fn, moe_ctx *ctx, int layer, const float 
     p.hh = ctx->hh;
     p.hmax = ctx->hmax;
     p.part = ctx->part;
+    p.pexp = ctx->pexp;
     p.y = y;
     p.M = M;
     p.E = E;

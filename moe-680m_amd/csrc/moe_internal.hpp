@@ -66,7 +66,10 @@ struct PrefillArgs {
                          // block scaled by the power of two of its max (hmax), K order of the
                          // down kernel's A (perm32_pos inside 32-column blocks)
     float *hmax;         // [9M][I/PF_NGU] max |h| per row and PF_NGU-column block
-    float *part;         // [9M][H] f32, c*w-scaled expert outputs, sorted slot order
+    _Float16 *part;      // [9M][H] c*w-scaled expert outputs in sorted slot order, as f16
+                         // times 2^pexp per 32-column block; columns n and 16 + n of a block
+                         // stored side by side
+    int8_t *pexp;        // [9M][H/32] those exponents
     float *y;
     int M, E, accumulate, rmsnorm, tile_max, stile_max;
     float c;
