@@ -105,6 +105,18 @@ moe_status moe_bind_layer(moe_ctx *ctx, int layer, const moe_layer_weights *lw);
 moe_status moe_router_topk(moe_ctx *ctx, const float *logits, int M, uint16_t *ids, float *w,
                            void *stream);
 
+/* Router gate GEMV fused with the top-8: logits[t][e] = sum_k xin[t][k] * Wg[e][k], xin = x_t
+ * or, with flags = MOE_FFN_RMSNORM, RMSNorm(x_t) (eps 1e-6, no gain); then ids/w exactly as
+ * moe_router_topk computes them from those logits.  wg: IQ4_XS [n_experts][hidden] in the
+ * GGML layout (rows = experts, 16-byte aligned device memory, read in place -- no binding);
+ * x f32 [M][hidden]; logits f32 [M][n_experts] or NULL (then M <= m_max and the context's
+ * workspace holds them); ids u16 / w f32 [M][9], or both NULL for logits only.  f32
+ * arithmetic throughout (exact weights).  Replaces the Router GEMV dispatch
+ * (shaders/router.comp:21-61 at src/inference.rs:598-605) and, with ids/w, the RouterTopk
+ * dispatch and do_route (src/inference.rs:608-659). */
+moe_status moe_router_gemv_topk(moe_ctx *ctx, const void *wg, const float *x, int M, int flags,
+                                float *logits, uint16_t *ids, float *w, void *stream);
+
 /* Prefix-sum expert bucket fill over n_experts+1 buckets (bucket n_experts = shared):
  * ranges u32 [n_experts+2], sorted_tok u16 [9M], sorted_w f32 [9M]; tokens ascend inside
  * a bucket.  Replaces router::build_expert_batches (src/router.rs:55-97) and the upload
@@ -205,7 +217,8 @@ enum {
     MOE_K_PREFILL_COMBINE = 6,
     MOE_K_DECODE_STACK = 7,    /* moe_decode_stack: the persistent launch */
     MOE_K_STACK_PREP = 8,      /* moe_decode_stack: the routing + clearing launch before it */
-    MOE_K_COUNT = 9
+    MOE_K_ROUTER_GEMV = 9,     /* moe_router_gemv_topk: the GEMV launch (its top-8 is ROUTER_TOPK) */
+    MOE_K_COUNT = 10
 };
 moe_status moe_timing_enable(moe_ctx *ctx, int capacity);
 moe_status moe_timing_read(moe_ctx *ctx, int counts[MOE_K_COUNT], double total_ms[MOE_K_COUNT]);

@@ -39,7 +39,7 @@ DEVFLAG_BAD_ID, DEVFLAG_DUP_ID, DEVFLAG_TIMEOUT = 1, 2, 4
 
 # Every symbol include/moe_ffn.h declares (checked by the CPU test suite).
 EXPORTS = (
-    "moe_create", "moe_destroy", "moe_bind_layer", "moe_router_topk", "moe_bucket_fill",
+    "moe_create", "moe_destroy", "moe_bind_layer", "moe_router_topk", "moe_router_gemv_topk", "moe_bucket_fill",
     "moe_ffn", "moe_ffn_route", "moe_ffn_noalloc", "moe_decode_stack", "moe_dequant_iq4xs", "moe_device_flags",
     "moe_device_flags_async", "moe_stack_spin_limit", "moe_last_error",
     "moe_timing_enable", "moe_timing_read",
@@ -47,7 +47,7 @@ EXPORTS = (
 )
 
 KERNELS = ("router_topk", "bucket_fill", "decode_gate_up", "decode_down", "prefill_gate_up",
-           "prefill_down", "prefill_combine", "decode_stack", "stack_prep")
+           "prefill_down", "prefill_combine", "decode_stack", "stack_prep", "router_gemv")
 
 
 class MoeError(RuntimeError):
@@ -86,6 +86,7 @@ def lib():
         "moe_destroy": [vp],
         "moe_bind_layer": [vp, i, ctypes.POINTER(_LayerWeights)],
         "moe_router_topk": [vp, vp, i, vp, vp, vp],
+        "moe_router_gemv_topk": [vp, vp, vp, i, i, vp, vp, vp, vp],
         "moe_bucket_fill": [vp, vp, vp, i, vp, vp, vp, vp],
         "moe_ffn": [vp, i, vp, vp, vp, i, vp, i, vp],
         "moe_ffn_route": [vp, i, vp, vp, i, vp, vp, vp, i, vp],
@@ -206,6 +207,26 @@ class Context:
             w = torch.empty((M, SLOTS), dtype=torch.float32, device=logits.device)
         _check(lib().moe_router_topk(self._h, _ptr(logits), M, _ptr(ids), _ptr(w), _stream(stream)))
         return ids, w
+
+    def router_gemv_topk(self, wg, x, rmsnorm=False, logits=None, ids=None, w=None, want_logits=True,
+                         want_ids=True, stream=None):
+        """Router gate GEMV + top-8: wg = IQ4_XS bytes of [n_experts][hidden] (device uint8),
+        x [M][hidden] f32.  Returns (logits or None, ids or None, w or None)."""
+        M = x.shape[0]
+        if x.shape[-1] != self.hidden:
+            raise ValueError("x last dimension must be hidden")
+        if wg.numel() != matrix_bytes(self.hidden, self.n_experts):
+            raise ValueError("wg must hold n_experts x hidden IQ4_XS weights")
+        dev = x.device
+        if want_logits and logits is None:
+            logits = torch.empty((M, self.n_experts), dtype=torch.float32, device=dev)
+        if want_ids and ids is None:
+            ids = torch.empty((M, SLOTS), dtype=torch.uint16, device=dev)
+        if want_ids and w is None:
+            w = torch.empty((M, SLOTS), dtype=torch.float32, device=dev)
+        _check(lib().moe_router_gemv_topk(self._h, _ptr(wg), _ptr(x), M, FFN_RMSNORM if rmsnorm else 0,
+                                          _ptr(logits), _ptr(ids), _ptr(w), _stream(stream)))
+        return logits, ids, w
 
     def bucket_fill(self, ids, w, stream=None):
         M = ids.shape[0]

@@ -51,6 +51,79 @@ hipError_t launch_router_topk(const float *logits, int M, int E, int renorm, uin
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- router gate GEMV
+// logits[t][e] = sum_k xin[t][k] * Wg[e][k], xin = x or RMSNorm(x); Wg IQ4_XS [E][H] in the
+// caller's (GGML) layout, rows = experts.  Replaces shaders/router.comp:21-61 (dispatched at
+// src/inference.rs:598-605), whose 64x8 f32 tiles re-dequantized every weight per tile.
+// One wave per (expert row, group of RG_TM tokens), four waves per workgroup: lane l owns
+// sub-block l of the row (32 weights; H = 2048 is one sub-block per lane), decodes it once
+// into biased codebook bytes and one f32 scale, then for each token takes one f32 dot of 32
+// against x (loaded for all the group's tokens before any is used) and a wave sum.  All f32:
+// the weights are exact, so the logits differ from an f64 sum by f32 rounding only.
+constexpr int RG_TM = 4;    // tokens per wave
+constexpr int RG_WAVES = 4; // experts per workgroup
+
+template <int H>
+__global__ __launch_bounds__(64 * RG_WAVES) void k_router_gemv(const uint8_t *__restrict__ wg,
+                                                               const float *__restrict__ x, int M, int E,
+                                                               int rmsnorm, float *__restrict__ logits) {
+    constexpr int NSB = H / 32, SBR = H / QK;
+    static_assert(H % QK == 0 && NSB <= 64, "one sub-block per lane");
+    const int lane = threadIdx.x & 63;
+    const int e = blockIdx.x * RG_WAVES + (int)(threadIdx.x >> 6);
+    const int t0 = blockIdx.y * RG_TM;
+    if (e >= E) return; // whole wave
+    const bool on = lane < NSB;
+    const int sl = on ? lane : 0; // idle lanes (H < 2048) read sub-block 0 and add nothing
+    const uint8_t *blk = wg + ((size_t)e * SBR + sl / 8) * SB_BYTES;
+    const u32x2 hdr = ldg<u32x2>(blk);
+    const int j = sl % 8;
+    uint32_t q[4];
+    {
+        const u32x2 q01 = ldg<u32x2>(blk + 8 + 16 * j), q23 = ldg<u32x2>(blk + 16 + 16 * j);
+        q[0] = q01.x; q[1] = q01.y; q[2] = q23.x; q[3] = q23.y;
+    }
+    float xv[RG_TM][32];
+#pragma unroll
+    for (int i = 0; i < RG_TM; ++i) {
+        const int t = t0 + i < M ? t0 + i : M - 1; // rows past M repeat the last; not stored
+        load32(x + (size_t)t * H + 32 * sl, xv[i]);
+    }
+    uint32_t kv[8];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) kv_biased8(q[d], kv[2 * d], kv[2 * d + 1]);
+    const float dl = on ? sub_scale(hdr, j) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < RG_TM; ++i) {
+        float xs = 0.f, ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            xs += xv[i][k];
+            ss = __builtin_fmaf(xv[i][k], xv[i][k], ss);
+        }
+        const float dot = wave_sum(dl * subblock_dot(kv, xv[i], xs));
+        float inv = 1.0f;
+        if (rmsnorm) inv = 1.0f / sqrtf(wave_sum(on ? ss : 0.0f) * (1.0f / (float)H) + 1e-6f);
+        if (lane == 0 && t0 + i < M) logits[(size_t)(t0 + i) * E + e] = dot * inv;
+    }
+}
+
+hipError_t launch_router_gemv(int H, const void *wg, const float *x, int M, int E, int rmsnorm, float *logits,
+                              hipStream_t st, KernelTimer *T) {
+    if (M <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((E + RG_WAVES - 1) / RG_WAVES), (unsigned)((M + RG_TM - 1) / RG_TM));
+    TimedLaunch tl(T, MOE_K_ROUTER_GEMV, st);
+    if (H == 2048)
+        hipLaunchKernelGGL(k_router_gemv<2048>, grid, dim3(64 * RG_WAVES), 0, st, (const uint8_t *)wg, x, M, E, rmsnorm,
+                           logits);
+    else if (H == 512)
+        hipLaunchKernelGGL(k_router_gemv<512>, grid, dim3(64 * RG_WAVES), 0, st, (const uint8_t *)wg, x, M, E, rmsnorm,
+                           logits);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------- bucket fill
 __global__ __launch_bounds__(BF_THREADS) void k_bucket_fill(BucketArgs a) { bucket_fill_one_wg(a); }
 __global__ __launch_bounds__(BF_CHUNK_THREADS) void k_bucket_count(BucketArgs a) { bucket_count_chunk(a, blockIdx.x); }

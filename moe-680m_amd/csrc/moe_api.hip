@@ -33,6 +33,7 @@ struct moe_ctx {
     float *hmax = nullptr;       // [9 m_max][I/PF_NGU]
     _Float16 *part = nullptr;    // [9 m_max][H]
     int8_t *pexp = nullptr;      // [9 m_max][H/32]
+    float *logits = nullptr;     // [m_max][E] router GEMV output when the caller gives none
     uint32_t *ranges = nullptr;  // [E+2]
     uint16_t *stok = nullptr;    // [9 m_max]
     float *sw = nullptr;         // [9 m_max]
@@ -143,6 +144,7 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
         {(void **)&c->hmax, SLOTS * mm * (I / PF_NGU) * 4},
         {(void **)&c->part, SLOTS * mm * H * 2},
         {(void **)&c->pexp, SLOTS * mm * (H / 32)},
+        {(void **)&c->logits, mm * (size_t)E * 4},
         {(void **)&c->ranges, (E1 + 1) * 4},
         {(void **)&c->stok, SLOTS * mm * 2},
         {(void **)&c->sw, SLOTS * mm * 4},
@@ -271,6 +273,30 @@ moe_status moe_router_topk(moe_ctx *ctx, const float *logits, int M, uint16_t *i
     hipError_t he = launch_router_topk(logits, M, ctx->cfg.n_experts, ctx->cfg.wmode == MOE_W_RENORM, ids,
                                        w, as_stream(stream), timer_for(ctx, as_stream(stream)));
     if (he != hipSuccess) return hip_fail(he, "moe_router_topk: launch");
+    return ok();
+}
+
+moe_status moe_router_gemv_topk(moe_ctx *ctx, const void *wg, const float *x, int M, int flags, float *logits,
+                                uint16_t *ids, float *w, void *stream) {
+    static const char *fn = "moe_router_gemv_topk";
+    if (!ctx) return fail(MOE_EINVAL, "%s: null context", fn);
+    if (M < 0 || M > 65535) return fail(MOE_EINVAL, "%s: M=%d outside 0..65535", fn, M);
+    if (flags & ~MOE_FFN_RMSNORM) return fail(MOE_EINVAL, "%s: flags 0x%x (only MOE_FFN_RMSNORM)", fn, flags);
+    if (!ids != !w) return fail(MOE_EINVAL, "%s: ids and w must both be given or both be NULL", fn);
+    if (!logits && !ids) return fail(MOE_EINVAL, "%s: no output (logits, ids and w all NULL)", fn);
+    if (!logits && M > ctx->cfg.m_max)
+        return fail(MOE_EINVAL, "%s: M=%d above m_max=%d with no logits buffer", fn, M, ctx->cfg.m_max);
+    if (M == 0) return ok();
+    if (!wg || !x) return fail(MOE_EINVAL, "%s: null argument", fn);
+    if (!aligned16(wg) || !aligned16(x) || ((uintptr_t)logits & 3u) || ((uintptr_t)w & 3u) || ((uintptr_t)ids & 1u))
+        return fail(MOE_EINVAL, "%s: misaligned pointer (wg and x need 16 bytes)", fn);
+    const hipStream_t st = as_stream(stream);
+    KernelTimer *T = timer_for(ctx, st);
+    float *lg = logits ? logits : ctx->logits;
+    const int E = ctx->cfg.n_experts;
+    hipError_t he = launch_router_gemv(ctx->cfg.hidden, wg, x, M, E, (flags & MOE_FFN_RMSNORM) ? 1 : 0, lg, st, T);
+    if (he == hipSuccess && ids) he = launch_router_topk(lg, M, E, ctx->cfg.wmode == MOE_W_RENORM, ids, w, st, T);
+    if (he != hipSuccess) return hip_fail(he, "moe_router_gemv_topk: launch");
     return ok();
 }
 

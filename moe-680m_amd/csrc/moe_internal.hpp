@@ -146,6 +146,8 @@ hipError_t launch_gen_logits(float *dst, int M, int E, uint64_t seed, int kind, 
 hipError_t launch_router_topk(const float *logits, int M, int E, int renorm, uint16_t *ids,
                               float *w, hipStream_t st, KernelTimer *T);
 hipError_t launch_bucket_fill(const BucketArgs &a, hipStream_t st, KernelTimer *T);
+hipError_t launch_router_gemv(int H, const void *wg, const float *x, int M, int E, int rmsnorm, float *logits,
+                              hipStream_t st, KernelTimer *T);
 hipError_t launch_decode(int H, int I, const DecodeArgs &a, hipStream_t st, KernelTimer *T);
 // prep, one gate/up and one down launch over both tile lists, combine -- all on st.
 // Bucket fill and prep (one launch), gate/up, down, combine.

@@ -215,6 +215,30 @@ void orc_rmsnorm(const float *x, int H, double *out) {
     for (int k = 0; k < H; ++k) out[k] = x[k] * inv;
 }
 
+/* Router gate GEMV, restating shaders/router.comp:21-61 (logits = x . Wg, dispatched at
+ * src/inference.rs:598-605) with Wg rows = experts (the [out][in] convention of the expert
+ * matrices): logits[t][e] = sum_k xin[t][k] * Wg[e][k], xin = x or RMSNorm(x).  f64 sums of
+ * exact f32 weights; the output is the f64 value rounded to f32. */
+void orc_router_gemv(const uint8_t *wg, int H, int E, const float *x, int M, int flags, float *logits) {
+    size_t nw = (size_t)E * H;
+    float *W = (float *)malloc(nw * 4);
+    orc_dequant_iq4xs(wg, nw / ORC_QK, W);
+#pragma omp parallel
+    {
+        double *xin = (double *)malloc((size_t)H * sizeof(double));
+#pragma omp for schedule(static)
+        for (int t = 0; t < M; ++t) {
+            if (flags & ORC_FFN_RMSNORM)
+                orc_rmsnorm(x + (size_t)t * H, H, xin);
+            else
+                for (int k = 0; k < H; ++k) xin[k] = x[(size_t)t * H + k];
+            for (int e = 0; e < E; ++e) logits[(size_t)t * E + e] = (float)dot_f32_f64(W + (size_t)e * H, xin, H);
+        }
+        free(xin);
+    }
+    free(W);
+}
+
 /* gate||up then SiLU*up then down, restating w1_w3_fused_m1.comp:30-52 (gate from W1,
  * up from W3), w2_scatter.comp:31-42 (A = silu(gate)*up) and :44-57 (down product). */
 static void expert_rows(const float *W1, const float *W3, const float *W2, int H, int I,

@@ -6,6 +6,7 @@
  * it, and only as the checker (or as the timed CPU baseline), never as a product path.
  *
  * What it restates (citations are path:line in the reference tree):
+ *   - router gate GEMV            shaders/router.comp:21-61, src/inference.rs:598-605
  *   - router softmax + top-8      shaders/router_topk.comp:31-92, src/router.rs:23-51
  *   - prefix-sum bucket fill      src/router.rs:55-97
  *   - gate||up GEMV, fused SiLU   shaders/w1_w3_fused_m1.comp:30-52, shaders/w1_w3_fused.comp:47-48,
@@ -80,6 +81,10 @@ typedef struct {
  * router never produces either).  x and y may alias.  Accumulation in f64. */
 void orc_moe_ffn(const orc_layer *L, int H, int I, int E, const float *x, const uint16_t *ids,
                  const float *w, int M, double c, int flags, float *y);
+
+/* Router gate GEMV: logits[t][e] = sum_k xin[t][k] * Wg[e][k] (f64 sum, rounded to f32),
+ * xin = flags & ORC_FFN_RMSNORM ? RMSNorm(x_t) : x_t.  wg: IQ4_XS [E][H], rows = experts. */
+void orc_router_gemv(const uint8_t *wg, int H, int E, const float *x, int M, int flags, float *logits);
 
 /* Single expert on one row, f64 out (for fine-grained tests). */
 void orc_expert_forward(const uint8_t *w1, const uint8_t *w3, const uint8_t *w2, int H, int I,

@@ -38,6 +38,7 @@ def lib():
         L.orc_bucket_fill.argtypes = [vp, vp, i, i, vp, vp, vp, vp]
         L.orc_moe_ffn.argtypes = [vp, i, i, i, vp, vp, vp, i, d, i, vp]
         L.orc_expert_forward.argtypes = [vp, vp, vp, i, i, vp, vp]
+        L.orc_router_gemv.argtypes = [vp, i, i, vp, i, i, vp]
         L.orc_mix64.argtypes = [u64]
         L.orc_mix64.restype = u64
         L.orc_rng.argtypes = [u64, u64]
@@ -86,6 +87,17 @@ def router_topk(logits, mode=W_REF):
     w = np.empty((M, SLOTS), dtype=np.float32)
     lib().orc_router_topk(_p(logits), M, E, mode, _p(ids), _p(w))
     return ids, w
+
+
+def router_gemv(wg, x, E, flags=0):
+    """logits [M][E] f32 = (x or RMSNorm(x)) . Wg^T; wg: IQ4_XS bytes of [E][H]."""
+    wg = np.ascontiguousarray(wg, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, H = x.shape
+    assert wg.size == E * H // QK * SB_BYTES
+    out = np.empty((M, E), dtype=np.float32)
+    lib().orc_router_gemv(_p(wg), H, E, _p(x), M, flags, _p(out))
+    return out
 
 
 def bucket_fill(ids, w, E):

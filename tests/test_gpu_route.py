@@ -90,3 +90,77 @@ def test_bucket_fill_flags_invalid_ids(gpu, ctx):
     assert r[-1] == 9 * M - 2 and np.all(np.diff(r) >= 0)
     ranges, stok, sw = ctx.bucket_fill(ids, w)
     assert ctx.device_flags() == 0
+
+
+# ---------------------------------------------------------------- router gate GEMV
+
+def _router_gemv_case(gpu, orc, c, E_, H_, M, seed, rmsnorm):
+    import torch
+    wg = gpu.gen_iq4xs(E_ * H_ // 256, seed)
+    x = gpu.gen_normal(M * H_, seed ^ 0x58, 0, 0.0, 1.0).view(M, H_)
+    lg, ids, w = c.router_gemv_topk(wg, x, rmsnorm=rmsnorm)
+    torch.cuda.synchronize()
+    ref = orc.router_gemv(wg.cpu().numpy(), x.cpu().numpy(), E_, flags=2 if rmsnorm else 0)
+    got = lg.cpu().numpy()
+    # f32 sums of exact weights: within 1e-5 of each row's logit scale
+    scale = np.maximum(np.abs(ref).max(axis=1, keepdims=True), 1.0)
+    assert np.all(np.abs(got - ref) <= 1e-5 * scale)
+    # the fused top-8 is moe_router_topk of the GEMV's own logits, bit for bit
+    ids2, w2 = c.router_topk(lg)
+    torch.cuda.synchronize()
+    assert np.array_equal(ids.cpu().numpy(), ids2.cpu().numpy())
+    assert np.array_equal(w.cpu().numpy().view(np.uint32), w2.cpu().numpy().view(np.uint32))
+    # against the oracle's routing of the oracle's logits, on every token whose sorted top-9
+    # logits are separated by more than the logits' tolerance: ids exact; weights within what
+    # the logit error allows (w_i = exp(l_i - l_max) / sum: a logit error d moves w_i by at most
+    # 2 max|d| relative, to first order) plus the softmax's own 1e-5
+    rid, rw = orc.router_topk(ref, c.wmode)
+    top9 = -np.sort(-ref, axis=1)[:, :9]
+    clear = np.all(-np.diff(top9, axis=1) > 2e-5 * scale, axis=1)
+    assert clear.mean() > 0.9
+    gi, gw = ids.cpu().numpy(), w.cpu().numpy()
+    assert np.array_equal(gi[clear], rid[clear])
+    d = np.abs(got - ref).max(axis=1, keepdims=True).astype(np.float64)
+    rtol = 2.5 * d + 1e-5
+    err = np.abs(gw.astype(np.float64) - rw)
+    assert np.all((err <= rtol * np.abs(rw) + 1e-37)[clear])
+    return got
+
+
+@pytest.mark.parametrize("M", [1, 5, 64, 300])
+@pytest.mark.parametrize("rmsnorm", [False, True])
+def test_router_gemv_matches_oracle(gpu, orc, ctx, ctx_renorm, M, rmsnorm):
+    log(f"router gemv E={E} H=2048 M={M} rmsnorm={rmsnorm}")
+    _router_gemv_case(gpu, orc, ctx if M % 2 else ctx_renorm, E, 2048, M, 0x52470000 + M, rmsnorm)
+
+
+@pytest.mark.parametrize("M", [1, 7])
+def test_router_gemv_small_shape(gpu, orc, M):
+    log(f"router gemv E=16 H=512 M={M}")
+    c = gpu.Context(512, 256, 16, 1, 64, gpu.W_RENORM)
+    try:
+        _router_gemv_case(gpu, orc, c, 16, 512, M, 0x52471000 + M, True)
+    finally:
+        c.close()
+
+
+def test_router_gemv_outputs_and_errors(gpu, orc, ctx):
+    import torch
+    log("router gemv: logits-only, ids-only, bad flags")
+    wg = gpu.gen_iq4xs(E * 2048 // 256, 0x5247AAAA)
+    x = gpu.gen_normal(3 * 2048, 0x5247AAAB).view(3, 2048)
+    lg, ids, w = ctx.router_gemv_topk(wg, x)
+    lg1, n1, n2 = ctx.router_gemv_topk(wg, x, want_ids=False)
+    n3, ids1, w1 = ctx.router_gemv_topk(wg, x, want_logits=False)
+    torch.cuda.synchronize()
+    assert n1 is None and n2 is None and n3 is None
+    assert np.array_equal(lg.cpu().numpy(), lg1.cpu().numpy())
+    assert np.array_equal(ids.cpu().numpy(), ids1.cpu().numpy())
+    assert np.array_equal(w.cpu().numpy(), w1.cpu().numpy())
+    L = gpu.lib()
+    for flags in (1, 4):
+        assert L.moe_router_gemv_topk(ctx._h, wg.data_ptr(), x.data_ptr(), 3, flags, lg.data_ptr(), None, None,
+                                      None) == gpu.MOE_EINVAL
+    assert L.moe_router_gemv_topk(ctx._h, wg.data_ptr(), x.data_ptr(), 3, 0, None, None, None, None) == gpu.MOE_EINVAL
+    assert L.moe_router_gemv_topk(ctx._h, wg.data_ptr() + 4, x.data_ptr(), 3, 0, lg.data_ptr(), None, None,
+                                  None) == gpu.MOE_EINVAL

@@ -275,6 +275,48 @@ def test_moe_ffn_drops_repeated_and_bad_slots(orc):
         assert np.allclose(got[t], ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
 
 
+# ---------------------------------------------------------------- router gate GEMV
+
+def router_weights(orc, E, H, seed):
+    return orc.gen_iq4xs(seed, 0, E * H // 256)
+
+
+def test_router_gemv_matches_numpy(orc):
+    """Against numpy's f64 product of the dequantised matrix (rows = experts): a transposed
+    operand, a dropped sub-block or a wrong row stride would all differ by O(1)."""
+    E, H = 16, 512
+    wg = router_weights(orc, E, H, 0x5267)
+    W = orc.dequant(wg).astype(np.float64).reshape(E, H)
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal((6, H)).astype(np.float32)
+    got = orc.router_gemv(wg, x, E)
+    ref = x.astype(np.float64) @ W.T
+    assert np.allclose(got, ref, rtol=2e-7, atol=1e-7 * np.abs(ref).max())
+    xn = x / np.sqrt((x.astype(np.float64) ** 2).mean(axis=1, keepdims=True) + 1e-6)
+    got_n = orc.router_gemv(wg, x, E, flags=2)
+    ref_n = xn @ W.T
+    assert np.allclose(got_n, ref_n, rtol=2e-7, atol=1e-7 * np.abs(ref_n).max())
+
+
+def test_router_gemv_closed_forms(orc):
+    """x = unit vector e_k gives column k of Wg exactly (as values: a -0 weight sums to +0);
+    a constant row under RMSNorm gives the row sums times 1/sqrt(1 + 1e-6/c^2)."""
+    E, H = 16, 512
+    wg = router_weights(orc, E, H, 0x5268)
+    W = orc.dequant(wg).reshape(E, H)
+    ks = [0, 1, 31, 32, 255, 256, 511]
+    x = np.zeros((len(ks), H), dtype=np.float32)
+    for i, k in enumerate(ks):
+        x[i, k] = 1.0
+    got = orc.router_gemv(wg, x, E)
+    for i, k in enumerate(ks):
+        assert np.array_equal(got[i], W[:, k])
+    c = 3.0
+    got_c = orc.router_gemv(wg, np.full((1, H), c, dtype=np.float32), E, flags=2)
+    ref_c = W.astype(np.float64).sum(axis=1) / math.sqrt(1.0 + 1e-6 / c ** 2)
+    assert np.allclose(got_c[0], ref_c, rtol=1e-6, atol=1e-6 * np.abs(ref_c).max())
+
+
 # ---------------------------------------------------------------- generator
 
 def test_generator_math(orc):
