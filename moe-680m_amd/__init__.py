@@ -159,7 +159,6 @@ class Context:
         h = ctypes.c_void_p()
         _check(lib().moe_create(device, ctypes.byref(cfg), ctypes.byref(h)))
         self._h = h
-        self._keep = {}
 
     @property
     def handle(self):
@@ -177,16 +176,14 @@ class Context:
             pass
 
     def bind_layer(self, layer, w1, w3, w2, w1_stride, w3_stride, w2_stride,
-                   shared_w1, shared_w3, shared_w2, keep=None):
+                   shared_w1, shared_w3, shared_w2):
         lw = _LayerWeights(_ptr(w1), _ptr(w3), _ptr(w2), w1_stride, w3_stride, w2_stride,
                            _ptr(shared_w1), _ptr(shared_w3), _ptr(shared_w2))
         _check(lib().moe_bind_layer(self._h, layer, ctypes.byref(lw)))
-        if keep is not None:
-            self._keep[layer] = keep
 
     def bind_packed(self, layer, buf):
         """Bind a uint8 device tensor laid out as [n_experts+1][w1|w3|w2]; the shared
-        expert is the last one."""
+        expert is the last one.  The library keeps its own copy: buf may be freed after."""
         mb = matrix_bytes(self.hidden, self.inter)
         eb = 3 * mb
         need = (self.n_experts + 1) * eb
@@ -195,7 +192,7 @@ class Context:
         base = buf.data_ptr()
         sh = base + self.n_experts * eb
         self.bind_layer(layer, base, base + mb, base + 2 * mb, eb, eb, eb,
-                        sh, sh + mb, sh + 2 * mb, keep=buf)
+                        sh, sh + mb, sh + 2 * mb)
 
     def router_topk(self, logits, ids=None, w=None, stream=None):
         M = logits.shape[0]
