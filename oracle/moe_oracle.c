@@ -330,6 +330,75 @@ void orc_moe_ffn(const orc_layer *L, int H, int I, int E, const float *x, const 
     free(xin); free(ys); free(used); free(list);
 }
 
+/* The same layer in f32 (f32 products and sums) with OpenMP over the output rows of each
+ * expert, rows decoded as they are used: the CPU baseline's timed path.  Checked against
+ * orc_moe_ffn (f64) by the CPU tests; not a checker itself. */
+static void dequant_row(const uint8_t *row, int n_sb, float *out) { orc_dequant_iq4xs(row, (size_t)n_sb, out); }
+
+void orc_moe_ffn_f32(const orc_layer *L, int H, int I, int E, const float *x, const uint16_t *ids,
+                     const float *w, int M, float c, int flags, float *y) {
+    const int nb = E + 1;
+    const size_t rb1 = (size_t)H / ORC_QK * ORC_SB_BYTES, rb2 = (size_t)I / ORC_QK * ORC_SB_BYTES;
+    float *xin = (float *)malloc((size_t)M * H * sizeof(float));
+    float *out = (float *)calloc((size_t)M * H, sizeof(float));
+    float *h = (float *)malloc((size_t)M * I * sizeof(float));
+    int *tok = (int *)malloc((size_t)M * sizeof(int));
+    float *tw = (float *)malloc((size_t)M * sizeof(float));
+    for (int t = 0; t < M; ++t) {
+        const float *xt = x + (size_t)t * H;
+        float inv = 1.0f;
+        if (flags & ORC_FFN_RMSNORM) {
+            float ss = 0.f;
+            for (int k = 0; k < H; ++k) ss += xt[k] * xt[k];
+            inv = 1.0f / sqrtf(ss / (float)H + 1e-6f);
+        }
+        for (int k = 0; k < H; ++k) xin[(size_t)t * H + k] = xt[k] * inv;
+    }
+    for (int e = 0; e < nb; ++e) {
+        int nt = 0;
+        for (int t = 0; t < M; ++t)
+            for (int s = 0; s < ORC_SLOTS; ++s)
+                if (ids[(size_t)t * ORC_SLOTS + s] == e && !repeats_earlier_slot(ids + (size_t)t * ORC_SLOTS, s)) {
+                    tok[nt] = t;
+                    tw[nt++] = w[(size_t)t * ORC_SLOTS + s];
+                }
+        if (!nt) continue;
+        const uint8_t *W1 = expert_ptr(L->w1, L->w1_stride, L->shared_w1, e, E);
+        const uint8_t *W3 = expert_ptr(L->w3, L->w3_stride, L->shared_w3, e, E);
+        const uint8_t *W2 = expert_ptr(L->w2, L->w2_stride, L->shared_w2, e, E);
+#pragma omp parallel
+        {
+            float *r1 = (float *)malloc((size_t)H * 4), *r3 = (float *)malloc((size_t)H * 4);
+#pragma omp for schedule(static)
+            for (int n = 0; n < I; ++n) {
+                dequant_row(W1 + (size_t)n * rb1, H / ORC_QK, r1);
+                dequant_row(W3 + (size_t)n * rb1, H / ORC_QK, r3);
+                for (int j = 0; j < nt; ++j) {
+                    const float *xt = xin + (size_t)tok[j] * H;
+                    float g = 0.f, u = 0.f;
+                    for (int k = 0; k < H; ++k) {
+                        g += r1[k] * xt[k];
+                        u += r3[k] * xt[k];
+                    }
+                    h[(size_t)j * I + n] = g / (1.0f + expf(-g)) * u;
+                }
+            }
+#pragma omp for schedule(static)
+            for (int n = 0; n < H; ++n) {
+                dequant_row(W2 + (size_t)n * rb2, I / ORC_QK, r1);
+                for (int j = 0; j < nt; ++j) {
+                    float a = 0.f;
+                    for (int k = 0; k < I; ++k) a += r1[k] * h[(size_t)j * I + k];
+                    out[(size_t)tok[j] * H + n] += c * tw[j] * a;
+                }
+            }
+            free(r1); free(r3);
+        }
+    }
+    for (size_t i = 0; i < (size_t)M * H; ++i) y[i] = ((flags & ORC_FFN_ACCUMULATE) ? y[i] : 0.f) + out[i];
+    free(xin); free(out); free(h); free(tok); free(tw);
+}
+
 /* ------------------------------------------------------------------ generator */
 /* Counter-based, so any slice of any stream can be produced independently.  The device
  * generator (moe-680m_amd/csrc) implements the same specification separately; tests

@@ -82,6 +82,11 @@ typedef struct {
 void orc_moe_ffn(const orc_layer *L, int H, int I, int E, const float *x, const uint16_t *ids,
                  const float *w, int M, double c, int flags, float *y);
 
+/* orc_moe_ffn in f32 arithmetic with OpenMP over each expert's output rows: the timed CPU
+ * baseline (a port of the same algorithm), checked against orc_moe_ffn; not a checker. */
+void orc_moe_ffn_f32(const orc_layer *L, int H, int I, int E, const float *x, const uint16_t *ids,
+                     const float *w, int M, float c, int flags, float *y);
+
 /* Router gate GEMV: logits[t][e] = sum_k xin[t][k] * Wg[e][k] (f64 sum, rounded to f32),
  * xin = flags & ORC_FFN_RMSNORM ? RMSNorm(x_t) : x_t.  wg: IQ4_XS [E][H], rows = experts. */
 void orc_router_gemv(const uint8_t *wg, int H, int E, const float *x, int M, int flags, float *logits);

@@ -39,6 +39,7 @@ def lib():
         L.orc_moe_ffn.argtypes = [vp, i, i, i, vp, vp, vp, i, d, i, vp]
         L.orc_expert_forward.argtypes = [vp, vp, vp, i, i, vp, vp]
         L.orc_router_gemv.argtypes = [vp, i, i, vp, i, i, vp]
+        L.orc_moe_ffn_f32.argtypes = [vp, i, i, i, vp, vp, vp, i, ctypes.c_float, i, vp]
         L.orc_mix64.argtypes = [u64]
         L.orc_mix64.restype = u64
         L.orc_rng.argtypes = [u64, u64]
@@ -143,6 +144,18 @@ def moe_ffn(layer, x, ids, w, c, flags=0, y=None):
         y = np.array(y, dtype=np.float32, copy=True)
     lib().orc_moe_ffn(ctypes.byref(layer.s), layer.H, layer.I, layer.E, _p(x), _p(ids), _p(w), M,
                       float(c), flags, _p(y))
+    return y
+
+
+def moe_ffn_f32(layer, x, ids, w, c, flags=0, y=None):
+    """The f32, all-core port of moe_ffn used as the timed CPU baseline.  Returns y."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    ids = np.ascontiguousarray(ids, dtype=np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    M = x.shape[0]
+    y = np.zeros_like(x) if y is None else np.array(y, dtype=np.float32, copy=True)
+    lib().orc_moe_ffn_f32(ctypes.byref(layer.s), layer.H, layer.I, layer.E, _p(x), _p(ids), _p(w), M,
+                          float(c), flags, _p(y))
     return y
 
 

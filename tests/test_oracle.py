@@ -275,6 +275,22 @@ def test_moe_ffn_drops_repeated_and_bad_slots(orc):
         assert np.allclose(got[t], ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
 
 
+def test_moe_ffn_f32_port_matches_oracle(orc):
+    """The f32 port timed as the CPU baseline computes the same layer as the f64 oracle (to
+    f32 rounding), for every flag combination, repeated ids included."""
+    H, I, E = 512, 256, 16
+    L = small_layer(orc, H, I, E, seed=29)
+    rng = np.random.default_rng(29)
+    x = rng.standard_normal((5, H)).astype(np.float32)
+    ids, w = orc.router_topk(rng.standard_normal((5, E)).astype(np.float32), 1)
+    ids[2, 5] = ids[2, 0]
+    y0 = rng.standard_normal((5, H)).astype(np.float32)
+    for flags in (0, 1, 2, 3):
+        ref = orc.moe_ffn(L, x, ids, w, 1.0, flags, y=y0)
+        got = orc.moe_ffn_f32(L, x, ids, w, 1.0, flags, y=y0)
+        assert np.abs(got - ref).max() <= 1e-4 * np.abs(ref).max(), flags
+
+
 # ---------------------------------------------------------------- router gate GEMV
 
 def router_weights(orc, E, H, seed):
