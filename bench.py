@@ -39,7 +39,7 @@ ROUTER_BYTES = E * H // 256 * 136                            # 278,528 (the gate
 PREFILL_M = 512
 PREFILL_FLOPS = 2 * (9 * PREFILL_M) * 3 * I * H             # 28,991,029,248
 HBM_PEAK_GBS = 8000.0
-BF16_PEAK_TFLOPS = 2500.0  # dense bf16 and f16 MFMA peak
+F16_PEAK_TFLOPS = 2500.0  # dense f16 MFMA peak (the bf16 figure is the same)
 # HBM bytes per decode-stack launch measured by rocprofv3 (FETCH_SIZE and WRITE_SIZE runs,
 # calibrated on a plain copy); the summary and its commands are in this file:
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_stack_config2.md")
@@ -266,7 +266,7 @@ def leg_prefill(torch, pkg, ctx, PK, eager):
     tflops = PREFILL_FLOPS / (us * 1e-6) / 1e12
     active = [int(torch.unique(pids[s].view(-1).to(torch.int32)).numel()) for s in range(pw, pn)]
     log(f"prefill M={PREFILL_M}: {us:.1f} us/step, {PREFILL_M / (us * 1e-6):.0f} tok/s, "
-        f"{tflops:.1f} TFLOP/s = {100 * tflops / BF16_PEAK_TFLOPS:.2f}% of the f16/bf16 MFMA peak; "
+        f"{tflops:.1f} TFLOP/s = {100 * tflops / F16_PEAK_TFLOPS:.2f}% of the f16 MFMA peak; "
         f"active experts {min(active)}-{max(active)}")
     pkern = kernel_times(ctx, lambda: [prefill(s) for s in range(pw, min(pn, pw + 8))], 8 * 64)
     log(f"prefill kernels: {pkern}")
@@ -276,11 +276,11 @@ def leg_prefill(torch, pkg, ctx, PK, eager):
                         "(cycling the 40 resident layers)",
             "dtype": "f16 MFMA (operands scaled by exact powers of two), f32 accumulate",
             "ms_per_step": round(p_ms, 5), "tok_per_s": round(PREFILL_M / (us * 1e-6), 1),
-            "tflops": round(tflops, 2), "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+            "tflops": round(tflops, 2), "mfma_frac": round(tflops / F16_PEAK_TFLOPS, 4),
             "active_experts": [min(active), max(active)],
             "roofline": {"bound": "mfma", "kernel": "prefill_gate_up", "achieved": round(pgu_tflops, 2),
-                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(pgu_tflops / BF16_PEAK_TFLOPS, 4), "avg_us": pgu_us},
+                         "peak": F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(pgu_tflops / F16_PEAK_TFLOPS, 4), "avg_us": pgu_us},
             "kernels": pkern}
 
 
@@ -352,11 +352,11 @@ def leg_config4(torch, pkg, layer0, eager):
     fl4 = 2 * (9 * M4) * 3 * I * H
     tf4 = fl4 / (us4 * 1e-6) / 1e12
     log(f"config 4, M={M4}: {us4:.1f} us/step, {M4 / (us4 * 1e-6):.0f} tok/s, {tf4:.1f} TFLOP/s = "
-        f"{100 * tf4 / BF16_PEAK_TFLOPS:.2f}% of the f16/bf16 MFMA peak; kernels {kern4}")
+        f"{100 * tf4 / F16_PEAK_TFLOPS:.2f}% of the f16 MFMA peak; kernels {kern4}")
     return {"workload": "config 4: one layer, M=4096, N(0,1) logits with 5% of tokens forced onto one hot "
                         "expert; router + moe_ffn per step",
             "us_per_step": round(us4, 1), "tok_per_s": round(M4 / (us4 * 1e-6), 1),
-            "tflops": round(tf4, 2), "mfma_frac": round(tf4 / BF16_PEAK_TFLOPS, 4), "kernels": kern4}
+            "tflops": round(tf4, 2), "mfma_frac": round(tf4 / F16_PEAK_TFLOPS, 4), "kernels": kern4}
 
 
 def main():

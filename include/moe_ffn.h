@@ -82,18 +82,18 @@ typedef struct {
 } moe_layer_weights;
 
 /* Create a context on HIP device `device`: validates the shape, allocates every
- * workspace for m_max tokens and the device copies of the weights that moe_bind_layer
- * fills (nothing is allocated later): a decode-stack layout of every layer, and for
- * m_max > MOE_DECODE_MAX_M a prefill layout -- each n_layers x (E+1) x 3 matrices.
+ * workspace for m_max tokens and the one device copy of the weights that moe_bind_layer
+ * fills (nothing is allocated later): n_layers x (E+1) x 3 matrices in the library's split
+ * layout, which every kernel family reads.
  * Replaces the MoE slice of InferenceEngine::new (src/inference.rs:85-126) and the
  * scratch / routing regions of ArenaLayout::compute (src/memory.rs:32-96). */
 moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out);
 moe_status moe_destroy(moe_ctx *ctx);
 
 /* Copy one layer's weights (device pointers, read only during this call) into the context's
- * split layout, which the decode path and the decode stack read, and, for a prefill context,
- * its prefill layout (same bytes, rearranged).  Synchronises the device; rebinding a layer
- * replaces its copies.
+ * split layout (same bytes, qs and headers of each super-block apart).  Synchronises the
+ * device: the caller's buffers may be freed when it returns.  Rebinding a layer replaces its
+ * copy.
  * Replaces LayerWeights::from_registry (src/memory.rs:227-291). */
 moe_status moe_bind_layer(moe_ctx *ctx, int layer, const moe_layer_weights *lw);
 
