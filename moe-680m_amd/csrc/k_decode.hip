@@ -54,6 +54,40 @@ __device__ __forceinline__ bool pair_valid(const DecodePlan &P, int q) { return 
 __device__ __forceinline__ uint32_t build_plan(const DecodeArgs &a, DecodePlan &P, bool publish) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
     const int np = a.M * SLOTS;
+    if (a.logits && a.M == 1) {
+        // One token routed here: its 8 ids are distinct and below E and the shared id is E,
+        // so every slot is valid and the only pair naming its expert -- no validity pass,
+        // and one LDS-only barrier (the published ids/w are for the next launch).
+        if (wv == 0) {
+            for (int e = lane; e < DEC_EMAX; e += 64) P.owner[e] = 0xFFFFFFFFu;
+            int sel[TOPK];
+            float ws[TOPK];
+            route_wave<4>(a.logits, a.E, a.renorm, lane, sel, ws);
+            if (lane < SLOTS) {
+                int id = a.E;
+                float wt = 1.0f;
+#pragma unroll
+                for (int r = 0; r < TOPK; ++r)
+                    if (lane == r) {
+                        id = sel[r];
+                        wt = ws[r];
+                    }
+                P.id[lane] = (uint16_t)id;
+                P.wt[lane] = wt;
+                P.owner[id] = (uint32_t)lane; // after the clear: one wave's LDS writes stay in order
+                if (publish) {
+                    a.ids[lane] = (uint16_t)id;
+                    a.w[lane] = wt;
+                }
+            }
+            if (lane == 0) {
+                P.valid[0] = (1ull << SLOTS) - 1;
+                P.valid[1] = 0;
+            }
+        }
+        lds_barrier();
+        return 0u;
+    }
     for (int e = tid; e < DEC_EMAX; e += blockDim.x) P.owner[e] = 0xFFFFFFFFu;
     if (a.logits) {
         for (int t = wv; t < a.M; t += nw) {
@@ -353,6 +387,63 @@ __device__ __forceinline__ void down_item(const DecodeArgs &a, const DecodePlan 
     }
 }
 
+// ---------------------------------------------------------------- down, M = 1
+// Wave s takes slot s: it reads the 9 ids itself (no plan, no barrier before the weight
+// loads), drops its slot by the rule of build_plan (an id above n_experts, or one an earlier
+// slot names), and writes c * w_s * (W2_e h_s) for the workgroup's 8 output rows to LDS; the
+// 9 contributions are then summed in slot order with the residual.
+template <int H, int I>
+__global__ __launch_bounds__(64 * SLOTS) void k_dec_down_m1(DecodeArgs a) {
+    using S = DecShape<H, I>;
+    constexpr int SBR = S::SBR2, LPR = S::LPR2, RPS = S::RPS2, STEPS = S::STEPS;
+    __shared__ float part[SLOTS][DEC_ROWS];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n0 = blockIdx.x * DEC_ROWS;
+    float yres = 0.f;
+    if (a.accumulate && tid < DEC_ROWS) yres = a.y[n0 + tid];
+    const int idl = lane < SLOTS ? (int)a.ids[lane] : 0;
+    const int e = __builtin_amdgcn_readlane(idl, wv);
+    bool ok = e <= a.E;
+    for (int s2 = 0; s2 < wv; ++s2) ok = ok && __builtin_amdgcn_readlane(idl, s2) != e;
+    const int gsb = lane % LPR, rr = lane / LPR, sb = gsb >> 3, ib = gsb & 7;
+    if (ok) {
+        const float wq = a.c * a.w[wv];
+        const uint8_t *W2 = expert_w(a.L.w2, a.L.s2, a.L.sw2, e, a.E);
+        u32x4 qs[STEPS];
+        u32x2 hd[STEPS];
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) {
+            const int row = n0 + st * RPS + rr;
+            qs[st] = ldg<u32x4>(W2 + split_qs<SBR>(row, sb) + 16 * ib);
+            hd[st] = ldg<u32x2>(W2 + split_hdr<H, SBR>(row, sb));
+        }
+        float hv[32];
+        load32(a.hbuf + (size_t)wv * I + 32 * gsb, hv);
+        float hs = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) hs += hv[i];
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) {
+            uint32_t kv[8];
+#pragma unroll
+            for (int d = 0; d < 4; ++d) kv_biased8(qs[st][d], kv[2 * d], kv[2 * d + 1]);
+            float d = sub_scale(hd[st], ib) * subblock_dot(kv, hv, hs);
+            d = group_sum<LPR>(d);
+            if (gsb == 0) part[wv][st * RPS + rr] = wq * d;
+        }
+    } else if (lane < DEC_ROWS) {
+        part[wv][lane] = 0.f;
+    }
+    lds_barrier();
+    if (tid < DEC_ROWS) {
+        float sum = 0.f;
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) sum += part[s][tid];
+        a.y[n0 + tid] = yres + sum;
+    }
+}
+
 // ---------------------------------------------------------------- the launches
 // MT: the most tokens one expert can serve in this call (M rounded up to 1, 2, 4, 8).
 template <int H, int I, int MT, int RP>
@@ -393,7 +484,7 @@ static hipError_t launch_decode_t(const DecodeArgs &a, hipStream_t st, KernelTim
     b.logits = nullptr;
     {
         TimedLaunch tl(T, MOE_K_DECODE_DOWN, st);
-        if (a.M == 1) hipLaunchKernelGGL((k_dec_down<H, I, SLOTS>), dim3(H / DEC_ROWS), dim3(64 * SLOTS), 0, st, b);
+        if (a.M == 1) hipLaunchKernelGGL((k_dec_down_m1<H, I>), dim3(H / DEC_ROWS), dim3(64 * SLOTS), 0, st, b);
         else hipLaunchKernelGGL((k_dec_down<H, I, 16>), dim3(H / DEC_ROWS), dim3(1024), 0, st, b);
     }
     return hipGetLastError();
