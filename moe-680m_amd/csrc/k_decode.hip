@@ -60,18 +60,10 @@ __device__ __forceinline__ uint32_t build_plan(const DecodeArgs &a, DecodePlan &
         // and one LDS-only barrier (the published ids/w are for the next launch).
         if (wv == 0) {
             for (int e = lane; e < DEC_EMAX; e += 64) P.owner[e] = 0xFFFFFFFFu;
-            int sel[TOPK];
-            float ws[TOPK];
-            route_wave<4>(a.logits, a.E, a.renorm, lane, sel, ws);
+            int id;
+            float wt;
+            route_wave<4>(a.logits, a.E, a.renorm, lane, id, wt);
             if (lane < SLOTS) {
-                int id = a.E;
-                float wt = 1.0f;
-#pragma unroll
-                for (int r = 0; r < TOPK; ++r)
-                    if (lane == r) {
-                        id = sel[r];
-                        wt = ws[r];
-                    }
                 P.id[lane] = (uint16_t)id;
                 P.wt[lane] = wt;
                 P.owner[id] = (uint32_t)lane; // after the clear: one wave's LDS writes stay in order
@@ -91,18 +83,10 @@ __device__ __forceinline__ uint32_t build_plan(const DecodeArgs &a, DecodePlan &
     for (int e = tid; e < DEC_EMAX; e += blockDim.x) P.owner[e] = 0xFFFFFFFFu;
     if (a.logits) {
         for (int t = wv; t < a.M; t += nw) {
-            int sel[TOPK];
-            float ws[TOPK];
-            route_wave<4>(a.logits + (size_t)t * a.E, a.E, a.renorm, lane, sel, ws);
+            int id;
+            float wt;
+            route_wave<4>(a.logits + (size_t)t * a.E, a.E, a.renorm, lane, id, wt);
             if (lane < SLOTS) {
-                int id = a.E;
-                float wt = 1.0f;
-#pragma unroll
-                for (int r = 0; r < TOPK; ++r)
-                    if (lane == r) {
-                        id = sel[r];
-                        wt = ws[r];
-                    }
                 P.id[t * SLOTS + lane] = (uint16_t)id;
                 P.wt[t * SLOTS + lane] = wt;
                 if (publish) {

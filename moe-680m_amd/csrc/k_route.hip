@@ -8,45 +8,32 @@ namespace moe {
 // One 64-lane wave per token.  Replaces shaders/router_topk.comp, whose 256-lane workgroup
 // ran two 8-step LDS tree reductions and a serial insertion sort on lane 0
 // (router_topk.comp:37-85).  Here each lane keeps E/64 logits in registers; each of the 8
-// rounds is a wave max of the order-preserving key (DPP inside rows of 16, then four
-// v_readlane) followed by a wave min of the index among lanes holding that key, so the
-// lower index wins ties exactly like the shader's strict '>' insertion
-// (router_topk.comp:76).  The softmax sum is one DPP + readlane reduction.
-template <int NV>
-__global__ __launch_bounds__(64) void k_router_topk(const float *__restrict__ logits, int M, int E,
-                                                    int renorm, uint16_t *__restrict__ ids,
-                                                    float *__restrict__ w) {
+// rounds is one wave max of the order-preserving key (six DPP steps into lane 63) and a
+// ballot of the lanes holding it; the lowest index holding it wins, like the shader's strict
+// '>' insertion (router_topk.comp:76).  Lane r then stores rank r and its weight, lane 8 the
+// shared slot.  E <= 256 (moe_create's limit), so four logits per lane.
+__global__ __launch_bounds__(64) void k_router_topk(const float *__restrict__ logits, int M, int E, int renorm,
+                                                    uint16_t *__restrict__ ids, float *__restrict__ w) {
     // one wave per workgroup: the dispatcher spreads the tokens over every CU and SIMD
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x;
     if (t >= M) return; // whole wave leaves together
-    int sel[TOPK];
-    float ws[TOPK];
-    route_wave<NV>(logits + (size_t)t * E, E, renorm, lane, sel, ws);
-    if (lane < TOPK) {
-        float wv = ws[0];
-        int id = sel[0];
-#pragma unroll
-        for (int r = 1; r < TOPK; ++r)
-            if (lane == r) { wv = ws[r]; id = sel[r]; }
+    int id;
+    float wt;
+    route_wave<4>(logits + (size_t)t * E, E, renorm, lane, id, wt);
+    if (lane < SLOTS) {
         ids[(size_t)t * SLOTS + lane] = (uint16_t)id;
-        w[(size_t)t * SLOTS + lane] = wv;
-    } else if (lane == TOPK) {
-        ids[(size_t)t * SLOTS + TOPK] = (uint16_t)E;
-        w[(size_t)t * SLOTS + TOPK] = 1.0f;
+        w[(size_t)t * SLOTS + lane] = wt;
     }
 }
 
 hipError_t launch_router_topk(const float *logits, int M, int E, int renorm, uint16_t *ids, float *w,
                               hipStream_t st, KernelTimer *T) {
     if (M <= 0) return hipSuccess;
-    dim3 grid((unsigned)M);
+    if (E < TOPK || E > 256) return hipErrorInvalidValue;
     {
         TimedLaunch tl(T, MOE_K_ROUTER_TOPK, st);
-        if (E <= 256)
-            hipLaunchKernelGGL(k_router_topk<4>, grid, dim3(64), 0, st, logits, M, E, renorm, ids, w);
-        else
-            hipLaunchKernelGGL(k_router_topk<16>, grid, dim3(64), 0, st, logits, M, E, renorm, ids, w);
+        hipLaunchKernelGGL(k_router_topk, dim3((unsigned)M), dim3(64), 0, st, logits, M, E, renorm, ids, w);
     }
     return hipGetLastError();
 }

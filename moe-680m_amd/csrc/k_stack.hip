@@ -794,15 +794,10 @@ __global__ void k_stack_prep(StackArgs a, uint64_t words) {
         p4[i] = u32x4{0u, 0u, 0u, 0u};
     if ((int)blockIdx.x < a.n_layers && threadIdx.x < 64) {
         const int li = blockIdx.x, lane = threadIdx.x;
-        int sel[TOPK];
-        float ws[TOPK];
-        route_wave<4>(a.logits + (size_t)li * a.E, a.E, a.renorm, lane, sel, ws);
+        int id;
+        float wt;
+        route_wave<4>(a.logits + (size_t)li * a.E, a.E, a.renorm, lane, id, wt);
         if (lane < SLOTS) {
-            int id = a.E;
-            float wt = 1.0f;
-#pragma unroll
-            for (int r = 0; r < TOPK; ++r)
-                if (lane == r) { id = sel[r]; wt = ws[r]; }
             a.rid[(size_t)li * SLOTS + lane] = (uint16_t)id;
             a.rwt[(size_t)li * SLOTS + lane] = wt;
             if (a.ids_out) {

@@ -257,6 +257,25 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
     return min(min(a, b), min(c, d));
 }
 
+// Max over the wave, complete in lane 63 only: row maxima by DPP, then row_bcast:15 (rows
+// 1, 3 take the last lane of the row below) and row_bcast:31 (rows 2, 3 take lane 31), read
+// from lane 63 -- one readlane instead of four on the dependency chain.  The DPP source
+// defaults to 0, the identity of an unsigned max (rows outside a row mask), which lets
+// each step compile to one v_max_u32 with a DPP operand.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_max_step(uint32_t v) {
+    return max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xF, false));
+}
+__device__ __forceinline__ uint32_t wave_max_last_u32(uint32_t v) {
+    v = dpp_max_step<0xB1, 0xF>(v);  // quad_perm [1,0,3,2]
+    v = dpp_max_step<0x4E, 0xF>(v);  // quad_perm [2,3,0,1]
+    v = dpp_max_step<0x141, 0xF>(v); // row_half_mirror
+    v = dpp_max_step<0x140, 0xF>(v); // row_mirror
+    v = dpp_max_step<0x142, 0xA>(v); // row_bcast:15
+    v = dpp_max_step<0x143, 0xC>(v); // row_bcast:31
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 // Sum over groups of G lanes (G in 8,16,32,64), result in every lane of the group.
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
@@ -341,14 +360,19 @@ __device__ __forceinline__ void load_logits(const float *__restrict__ l, int E, 
     for (int j = 0; j < NV; ++j) v[j] = ldg<float>(l + min(lane + 64 * j, E - 1));
 }
 
-// Softmax + top-8 of one token's E logits (E <= 64*NV, E >= 8) by the calling wave, from
-// the values load_logits returned.
-// sel/wsel come out wave-uniform: the 8 ids by (logit desc, index asc) and their weights
-// (softmax probability, or renormalised over the 8 when renorm).
+// Softmax + top-8 of one token's E logits (8 <= E <= 64*NV) by the calling wave, from the
+// values load_logits returned.  Lane r < 8 comes out with rank r -- ids by (logit desc,
+// index asc) -- and its weight (softmax probability, or renormalised over the 8 when
+// renorm); lane 8 and above with the shared expert (id E, weight 1).
+// A round: each lane's best remaining key, its wave max in lane 63, a ballot of the lanes
+// holding it.  One lane: it wins with its lowest such index.  An exact tie across lanes:
+// the smallest index among the holders, by a min reduction.  The sums keep one order
+// (Z: lane terms j = 0..NV-1, then wave_sum; the top-8 sum: rank 0..7), so weights do not
+// depend on which lane computed them.
 template <int NV>
-__device__ __forceinline__ void route_values(const float (&raw)[NV], int E, int renorm, int lane, int sel[TOPK],
-                                             float wsel[TOPK]) {
-    float kf[NV];
+__device__ __forceinline__ void route_values(const float (&raw)[NV], int E, int renorm, int lane, int &id,
+                                             float &wt) {
+    float kf[NV], ex[NV];
     uint32_t ord[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
@@ -356,47 +380,57 @@ __device__ __forceinline__ void route_values(const float (&raw)[NV], int E, int 
         kf[j] = (i < E) ? router_key(raw[j]) : -INFINITY;
         ord[j] = (i < E) ? ord32(kf[j]) : 0u; // 0 sorts below every real key (-inf is 0x007FFFFF)
     }
-    uint32_t taken = 0, selord[TOPK];
+    float s8 = 0.f, my_e = 1.0f;
+    int my_id = E;
 #pragma unroll
     for (int r = 0; r < TOPK; ++r) {
-        uint32_t kb = 0;
+        uint32_t kb = ord[0];
 #pragma unroll
-        for (int j = 0; j < NV; ++j)
-            if (!((taken >> j) & 1u)) kb = max(kb, ord[j]);
-        const uint32_t K = wave_max_u32(kb);
-        uint32_t cand = 0xFFFFFFFFu;
+        for (int j = 1; j < NV; ++j) kb = max(kb, ord[j]);
+        const uint32_t K = wave_max_last_u32(kb);
+        if (r == 0) {
+            const float m = unord32(K);
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+                ex[j] = (lane + 64 * j < E) ? ((kf[j] == m) ? 1.0f : expf(kf[j] - m)) : 0.0f;
+        }
+        int jl = 0; // the lane's lowest j holding K (when it holds K)
+        float el = ex[0];
 #pragma unroll
         for (int j = NV - 1; j >= 0; --j)
-            if (!((taken >> j) & 1u) && ord[j] == K) cand = (uint32_t)(lane + 64 * j);
-        const uint32_t idx = wave_min_u32(cand);
-        if ((int)(idx & 63u) == lane) taken |= 1u << (idx >> 6);
-        sel[r] = (int)idx;
-        selord[r] = K;
+            if (ord[j] == K) {
+                jl = j;
+                el = ex[j];
+            }
+        const uint64_t hit = __ballot(kb == K);
+        int w = (int)__builtin_ctzll(hit);
+        if (__builtin_popcountll(hit) > 1)
+            w = (int)(wave_min_u32(kb == K ? (uint32_t)(lane + 64 * jl) : 0xFFFFFFFFu) & 63u);
+        const int jw = __builtin_amdgcn_readlane(jl, w);
+        const float e = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, el), w));
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            if (lane == w && j == jw) ord[j] = 0u;
+        s8 += e;
+        if (lane == r) {
+            my_id = w + 64 * jw;
+            my_e = e;
+        }
     }
-    const float m = unord32(selord[0]);
     float zs = 0.f;
 #pragma unroll
-    for (int j = 0; j < NV; ++j)
-        if (lane + 64 * j < E) zs += (kf[j] == m) ? 1.0f : expf(kf[j] - m);
+    for (int j = 0; j < NV; ++j) zs += ex[j];
     const float Z = wave_sum(zs);
-    float e8[TOPK], s8 = 0.f;
-#pragma unroll
-    for (int r = 0; r < TOPK; ++r) {
-        const float k = unord32(selord[r]);
-        e8[r] = (k == m) ? 1.0f : expf(k - m);
-        s8 += e8[r];
-    }
-    const float den = renorm ? s8 : Z;
-#pragma unroll
-    for (int r = 0; r < TOPK; ++r) wsel[r] = e8[r] / den;
+    id = my_id;
+    wt = (lane < TOPK) ? my_e / (renorm ? s8 : Z) : 1.0f;
 }
 
 template <int NV>
-__device__ __forceinline__ void route_wave(const float *__restrict__ l, int E, int renorm, int lane, int sel[TOPK],
-                                           float wsel[TOPK]) {
+__device__ __forceinline__ void route_wave(const float *__restrict__ l, int E, int renorm, int lane, int &id,
+                                           float &wt) {
     float raw[NV];
     load_logits<NV>(l, E, lane, raw);
-    route_values<NV>(raw, E, renorm, lane, sel, wsel);
+    route_values<NV>(raw, E, renorm, lane, id, wt);
 }
 
 // ---------------------------------------------------------------- expert table
