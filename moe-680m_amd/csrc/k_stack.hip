@@ -60,6 +60,7 @@
 namespace moe {
 
 constexpr int STK_NX = 8;   // XCDs
+constexpr uint32_t STK_DONE_ABORT = 1u << 16; // a done-count contribution that vetoes the y store
 
 // XCD-local publish: a plain store, which stays in this XCD's L2.
 __device__ __forceinline__ void tag_store_local(uint32_t *p, float v) {
@@ -112,48 +113,19 @@ __device__ __forceinline__ void stack_abort(uint32_t *flags, lds_flag *s_abort) 
 // Bounded wait until every quad in v[] is tagged, reloading only the untagged ones.  All
 // loads of a round are in flight together; a round ends with one wave-wide test.  After
 // spin_max failed rounds (checked every 32 rounds, or every round once past the limit) the
-// wait expires; it also gives up when this workgroup or any other has aborted.  Either way
-// it returns with the abort flag set and the caller's data invalid -- and once it is set,
-// nothing more is published, so no other workgroup can receive data computed from it.
+// wait expires; it also gives up when this workgroup or any other has aborted (checked at
+// the same points, so a wait whose data is there costs no LDS or flag read).  Returns false
+// -- with the abort flag set and the caller's data invalid -- when it gave up.
 template <int MAXQ, typename LD, typename TAG = LsbTag>
-__device__ __forceinline__ void poll_until_tagged(u32x4 (&v)[MAXQ], const int (&q)[MAXQ], const LD &ld,
+__device__ __forceinline__ bool poll_until_tagged(u32x4 (&v)[MAXQ], const int (&q)[MAXQ], const LD &ld,
                                                   uint32_t *flags, uint32_t spin_max, lds_flag *s_abort,
                                                   TAG tag = TAG{}) {
-    if (*s_abort) return;
     uint32_t spins = 0;
     while (true) {
         uint32_t t = 1u;
 #pragma unroll
         for (int j = 0; j < MAXQ; ++j) t &= tag(v[j]);
-        if (__all(t)) break;
-        ++spins;
-        if ((spins & 31u) == 0 || spins > spin_max) {
-            if (*s_abort) break;
-            if (__hip_atomic_load((const MOE_GLOBAL uint32_t *)(flags + 1), __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT)) {
-                *s_abort = 1;
-                break;
-            }
-            if (spins > spin_max) {
-                stack_abort(flags, s_abort);
-                break;
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < MAXQ; ++j)
-            if (!tag(v[j])) v[j] = ld(q[j]);
-    }
-}
-
-// Bounded wait (same limits as poll_until_tagged) until the XCD-local counter reaches
-// target; false when the wait expired or the launch aborted.
-__device__ __forceinline__ bool wait_count(const uint32_t *ctr, uint32_t target, uint32_t *flags, uint32_t spin_max,
-                                           lds_flag *s_abort) {
-    uint32_t spins = 0;
-    while (true) {
-        const uint32_t c = (uint32_t)__builtin_amdgcn_readfirstlane((int)__hip_atomic_load(
-            (const MOE_GLOBAL uint32_t *)ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        if (c >= target) return !*s_abort;
+        if (__all(t)) return true;
         ++spins;
         if ((spins & 31u) == 0 || spins > spin_max) {
             if (*s_abort) return false;
@@ -165,6 +137,34 @@ __device__ __forceinline__ bool wait_count(const uint32_t *ctr, uint32_t target,
             if (spins > spin_max) {
                 stack_abort(flags, s_abort);
                 return false;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < MAXQ; ++j)
+            if (!tag(v[j])) v[j] = ld(q[j]);
+    }
+}
+
+// Bounded wait (same limits as poll_until_tagged) until the XCD-local counter reaches
+// target; returns the count seen, or 0 when the wait expired or the launch aborted.
+__device__ __forceinline__ uint32_t wait_count(const uint32_t *ctr, uint32_t target, uint32_t *flags,
+                                               uint32_t spin_max, lds_flag *s_abort) {
+    uint32_t spins = 0;
+    while (true) {
+        const uint32_t c = (uint32_t)__builtin_amdgcn_readfirstlane((int)__hip_atomic_load(
+            (const MOE_GLOBAL uint32_t *)ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        if (c >= target) return c;
+        ++spins;
+        if ((spins & 31u) == 0 || spins > spin_max) {
+            if (*s_abort) return 0u;
+            if (__hip_atomic_load((const MOE_GLOBAL uint32_t *)(flags + 1), __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT)) {
+                *s_abort = 1;
+                return 0u;
+            }
+            if (spins > spin_max) {
+                stack_abort(flags, s_abort);
+                return 0u;
             }
         }
     }
@@ -338,6 +338,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         // ---------------- poller waves: x and h into LDS; the first also reduces
         const int ptid = tid - 64 * (NCW + 1);
         const bool first = wv == NCW + 1;
+        bool got = true; // every wait of this wave so far ended with its data
         // x_0 from the input: quad q (8 elements) per thread, a chunk on four adjacent lanes
         {
             float ss = 0.f;
@@ -383,7 +384,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                     q[m] = first ? I / 4 + 4 * lane + m : lane + 64 * m;
                     v[m] = ok ? ld(q[m]) : u32x4{1u, 1u, 1u, 1u};
                 }
-                poll_until_tagged<4>(v, q, ld, a.flags, a.spin_max, abort_lds);
+                got = poll_until_tagged<4>(v, q, ld, a.flags, a.spin_max, abort_lds) && got;
                 if (first) {
                     if (lane < I / NX) {
                         float g = 0.f, u = 0.f;
@@ -420,13 +421,17 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             if (first) {
                 // publish this XCD's partial of rows [64j, 64j+64) ...
                 uint32_t *pb = pbuf(li);
-                if (!*abort_lds) tag_store(pb + (size_t)k * H + ROWS * j + lane, part[0][lane] + part[1][lane]);
+                // (the workgroup's abort word read with the contributions: a wait that gave up in
+                // another wave of this workgroup left them invalid)
+                const float pv = part[0][lane] + part[1][lane];
+                const int ab = *abort_lds;
+                if (got && !ab) tag_store(pb + (size_t)k * H + ROWS * j + lane, pv);
                 // ... gather all eight (lane: quad lane&15 of XCDs lane>>4 and (lane>>4)+4) ...
                 const RemoteQuads ld{reinterpret_cast<const u32x4 *>(pb + ROWS * j)};
                 const int m = lane >> 4, qq = lane & 15;
                 int q[2] = {m * (H / 4) + qq, (m + 4) * (H / 4) + qq};
                 u32x4 v[2] = {ld(q[0]), ld(q[1])};
-                poll_until_tagged<2>(v, q, ld, a.flags, a.spin_max, abort_lds);
+                got = poll_until_tagged<2>(v, q, ld, a.flags, a.spin_max, abort_lds) && got;
                 *reinterpret_cast<f32x4 *>(&ps[m][4 * qq]) = __builtin_bit_cast(f32x4, v[0]);
                 *reinterpret_cast<f32x4 *>(&ps[m + 4][4 * qq]) = __builtin_bit_cast(f32x4, v[1]);
                 // lanes read what other lanes of this wave wrote: LDS keeps a wave's
@@ -454,20 +459,28 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                     }
                     const float xo = dpp_mov<0xB1>(x1); // the odd partner of an even lane
                     const float ss = wave_sum(x1 * x1);
-                    if (!*abort_lds) {
+                    if (got) {
                         if ((lane & 1) == 0)
                             *(MOE_GLOBAL uint32_t *)(xb + (row >> 1)) = pack_pair(x1, xo, quant_ratio(am));
                         if ((lane & 31) == 0) tag_store_local(xb + H / 2 + (row >> 5), am * (1.0f / 127.0f));
                         if (lane == 0) tag_store_local(xb + H / 2 + H / 32 + j, ss);
                     }
-                } else if (k == 0 && !*abort_lds) {
-                    // y is written only once every reducer of XCD 0 holds its final rows (a
-                    // count in that XCD's L2): an expired wait anywhere in the launch leaves y
-                    // -- and an x it aliases -- as it was
+                } else if (k == 0) {
+                    // y is written by all of XCD 0's reducers or by none.  Nothing computed
+                    // from a wait that gave up is ever published (a wave publishes only after
+                    // its own waits succeeded and, for data other waves left in LDS, with the
+                    // workgroup's abort word clear), so a reducer whose waits all succeeded
+                    // holds valid rows.  Each adds to a count in that XCD's L2: 1 when sound,
+                    // else STK_DONE_ABORT; all NJ write y only on a count of exactly NJ.  An
+                    // expired wait anywhere in the launch -- every later wait on what it would
+                    // have published expires too -- thus leaves y, and an x it aliases, as it
+                    // was.
                     uint32_t *done = a.ctl + STK_CTL_DONE;
+                    const bool sound = got && !*abort_lds;
                     if (lane == 0)
-                        __hip_atomic_fetch_add((MOE_GLOBAL uint32_t *)done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    if (wait_count(done, (uint32_t)NJ, a.flags, a.spin_max, abort_lds))
+                        __hip_atomic_fetch_add((MOE_GLOBAL uint32_t *)done, sound ? 1u : STK_DONE_ABORT,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (wait_count(done, (uint32_t)NJ, a.flags, a.spin_max, abort_lds) == (uint32_t)NJ)
                         *(MOE_GLOBAL float *)(a.y + row) = x1;
                 }
             }
@@ -483,7 +496,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 }
                 // pair words are tagged by being nonzero; the scales and sums of squares
                 // are LSB-tagged f32 words, which are nonzero too
-                poll_until_tagged<XP>(v, q, ld, a.flags, a.spin_max, abort_lds, NonzeroTag{});
+                got = poll_until_tagged<XP>(v, q, ld, a.flags, a.spin_max, abort_lds, NonzeroTag{}) && got;
 #pragma unroll
                 for (int m = 0; m < XP; ++m) {
                     if (q[m] < XD) {
@@ -705,6 +718,8 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 }
             }
             const float sx = xsc[g1];
+            // a poller whose wait gave up left x invalid (read with the planes: no extra wait)
+            const int ab = *abort_lds;
             // shared half sub-block: qs dwords 2hh, 2hh+1 of sub-block sbg
             const uint32_t *cs = xq + XQS * sbg + 2 * hh;
             const u32x2 sxh0 = *reinterpret_cast<const u32x2 *>(cs), sxh1 = *reinterpret_cast<const u32x2 *>(cs + 4);
@@ -725,14 +740,14 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 float u = (as3[st] * sx) * subblock_idot(ak3[st], xh, xl);
                 g = inv * row_total<LPR1>(g);
                 u = inv * row_total<LPR1>(u);
-                if (g1 == LPR1_LAST && !*abort_lds) tag_store_local(hb + rowA + st * RPS1 + rr1, silu_rcp(g) * u);
+                if (g1 == LPR1_LAST && !ab) tag_store_local(hb + rowA + st * RPS1 + rr1, silu_rcp(g) * u);
             }
             int sah_i = 0, sal_i = 0;
             dword_idot(sak[0], sak[1], sxh0[0], sxh1[0], sxl0[0], sxl1[0], sah_i, sal_i);
             dword_idot(sak[2], sak[3], sxh0[1], sxh1[1], sxl0[1], sxl1[1], sah_i, sal_i);
             float sp = (sas * ssx) * __builtin_fmaf((float)sal_i, 1.0f / 256.0f, (float)sah_i);
             sp = inv * adjacent_sum<LPRS>(sp);
-            if (lane % LPRS == 0 && lane < NSA && !*abort_lds)
+            if (lane % LPRS == 0 && lane < NSA && !ab)
                 tag_store_local(hb + I + ((j * SRP + pA) * NCW + w) * 2 + mA, sp);
         }
         __builtin_amdgcn_s_setprio(0);
