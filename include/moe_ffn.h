@@ -140,7 +140,7 @@ moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids,
 
 /* Router and expert FFN of one layer in one call: (ids, w) = top8(softmax(logits)) exactly
  * as moe_router_topk computes them (written to ids/w, [M][9]), then moe_ffn with them.  For
- * M <= 2 the routing runs inside the decode launch (no separate router launch).
+ * M <= 8 the routing runs inside the decode launches (no separate router launch).
  * Replaces the RouterTopk dispatch (src/inference.rs:608-616), do_route's readback
  * (src/inference.rs:622-659) and record_and_submit_moe (src/inference.rs:663-766) of one
  * layer. */
@@ -148,7 +148,7 @@ moe_status moe_ffn_route(moe_ctx *ctx, int layer, const float *x, const float *l
                          float *y, uint16_t *ids, float *w, int flags, void *stream);
 
 /* moe_ffn for M <= MOE_DECODE_MAX_M whose h scratch is a static device array of the library
- * (147,456 bytes per GPU, held until the process ends) instead of the context's workspace:
+ * (191,744 bytes per GPU, held until the process ends) instead of the context's workspace:
  * nothing in this call allocates, frees or calls an allocating library routine.  No
  * counterpart in the reference; it is for callers that cannot allocate device memory
  * (work under graph capture, tight serving loops, harnesses that forbid allocation).
@@ -208,7 +208,7 @@ const char *moe_last_error(void);
  * timed launches and their summed milliseconds, and starts a new window.  Events are
  * created here, never inside a hot call; capacity 0 disables and frees them. */
 enum {
-    MOE_K_ROUTER_TOPK = 0,     /* moe_router_topk, and moe_ffn_route's router launch for M > 2 */
+    MOE_K_ROUTER_TOPK = 0,     /* moe_router_topk, and moe_ffn_route's router launch for M > 8 */
     MOE_K_BUCKET_FILL = 1,     /* moe_bucket_fill; moe_ffn's first prefill launch (bucket fill + prep) */
     MOE_K_DECODE_GATE_UP = 2,  /* moe_ffn / moe_ffn_route, M <= 8 */
     MOE_K_DECODE_DOWN = 3,
@@ -218,7 +218,8 @@ enum {
     MOE_K_DECODE_STACK = 7,    /* moe_decode_stack: the persistent launch */
     MOE_K_STACK_PREP = 8,      /* moe_decode_stack: the routing + clearing launch before it */
     MOE_K_ROUTER_GEMV = 9,     /* moe_router_gemv_topk: the GEMV launch (its top-8 is ROUTER_TOPK) */
-    MOE_K_COUNT = 10
+    MOE_K_DECODE_PREP = 10,    /* moe_ffn / moe_ffn_route, 2 <= M <= 8: routing, plan, int8 activations */
+    MOE_K_COUNT = 11
 };
 moe_status moe_timing_enable(moe_ctx *ctx, int capacity);
 moe_status moe_timing_read(moe_ctx *ctx, int counts[MOE_K_COUNT], double total_ms[MOE_K_COUNT]);

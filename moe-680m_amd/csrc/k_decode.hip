@@ -4,38 +4,46 @@
 // w1_w3_fused_m1 GEMV and a w2_scatter_m1 GEMV (shaders/w1_w3_fused_m1.comp,
 // shaders/w2_scatter_m1.comp), 18 dispatches and 18 barriers per layer, with SiLU fused
 // into the down projection and the combine done as an f16 read-modify-write of the hidden
-// state.  Here one layer is two launches, with no waits between workgroups:
-//   gate/up item = (pair p, a block of 16 W1/W3 row pairs), where a pair is one (token, slot)
-//            of the routing.  The item runs only when p is the first valid pair naming its
-//            expert, and then serves every token that named that expert: each selected
-//            expert's rows are fetched and decoded once per call, whatever the number of
-//            tokens sharing it.  The served tokens' activations are staged in LDS as int8
-//            planes (quant4; RMSNorm is one factor per token, applied to the row sums);
-//            h = silu(g) * u goes to a [9M][I] f32 scratch.
-//   down item = 8 output rows for every token: the waves take the selected experts in turn
-//            (each W2 row fetched once per call); every pair's contribution c * w * (W2 h)
-//            goes to LDS and a token's 9 contributions are summed in slot order
-//            (deterministic, no atomics), the residual added in the same store.
+// state.  Here one layer is two launches at M = 1 and three at 2 <= M <= 8, with no waits
+// between workgroups:
+//   prep (M >= 2) = one workgroup, once per call: the routing when the call passed logits
+//            (wave t routes token t; ids and w are published), pair validity, the selected
+//            experts in slot order with the tokens each serves, every token's activations as
+//            int8 planes (quant4) and its RMSNorm factor -- a plan block in the scratch.
+//   gate/up = one workgroup per CU at M = 1, two beyond.  A step is one W1 row and the same
+//            W3 row (16 rows at hidden 512) of one selected expert; wave gw of NW takes
+//            steps gw, gw + NW, ..., so every SIMD does an equal share and the shared
+//            expert's rows spread over all of them.  Each selected expert's rows are fetched
+//            and decoded once per call, whatever the number of tokens sharing it.  At M = 1
+//            every wave routes the token itself (the top-8 code of moe_router_topk, so all
+//            agree bit for bit) and quantizes x into registers: no plan, no barrier, and the
+//            shared expert first in slot order.  Beyond, each workgroup copies the plan block
+//            into LDS and keeps two rounds of loads in flight.  h = silu(g) * u goes to a
+//            [9M][I] f32 scratch.
+//   down    = 8 output rows per workgroup for every token.  At M = 1 wave s takes slot s; beyond,
+//            the valid pairs are dealt to eight waves, each requesting all its W2 rows at once.
+//            Every pair's contribution c * w * (W2 h) goes to LDS and a token's 9 contributions
+//            are summed in slot order (deterministic, no atomics), the residual added in the
+//            same store.
 // A single launch with a device-side h exchange between the two roles was built and measured
 // (28 us per M = 1 layer against 23 for two launches): every down item needs every expert's
 // h, so ~256 workgroups poll and read the same few cache lines past their L2, and memory
 // serialises same-address accesses (~11 ns each); a device-scope release fence, the other
-// way to publish h, is an L2 writeback here.
-// Called with logits (moe_ffn_route, M <= 2), every gate/up workgroup first routes the tokens
-// itself -- the top-8 code of moe_router_topk, so all agree bit for bit -- and item 0 publishes
-// ids and w for the caller and the down launch (the reference's RouterTopk dispatch + readback
-// in do_route, src/inference.rs:608-639, folded into the first launch).
+// way to publish h, is an L2 writeback here.  The routing inside the decode launches stands
+// in for the reference's RouterTopk dispatch + readback in do_route
+// (src/inference.rs:608-639).
 // Pair validity: an id above n_experts, or an id the token already named in an earlier slot,
 // drops that slot (MOE_DEVFLAG_BAD_ID / MOE_DEVFLAG_DUP_ID) -- the same slots the prefill
 // bucket fill drops, so M = 8 and M = 9 treat such routing alike.
 // Lane mapping: a lane owns one 32-weight sub-block of a row: a 16-byte aligned qs load and
 // the row's 8-byte header (a row's headers are contiguous in the split layout, so one load
 // instruction of a wave touches one cache line of them).
+#include <cstddef>
+
 #include "moe_internal.hpp"
 
 namespace moe {
 
-constexpr int DEC_MAXP = MOE_DECODE_MAX_M * SLOTS; // (token, slot) pairs of one call
 constexpr int DEC_EMAX = 257;                      // owner table: n_experts <= 256, + shared
 
 struct DecodePlan {
@@ -54,32 +62,6 @@ __device__ __forceinline__ bool pair_valid(const DecodePlan &P, int q) { return 
 __device__ __forceinline__ uint32_t build_plan(const DecodeArgs &a, DecodePlan &P, bool publish) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
     const int np = a.M * SLOTS;
-    if (a.logits && a.M == 1) {
-        // One token routed here: its 8 ids are distinct and below E and the shared id is E,
-        // so every slot is valid and the only pair naming its expert -- no validity pass,
-        // and one LDS-only barrier (the published ids/w are for the next launch).
-        if (wv == 0) {
-            for (int e = lane; e < DEC_EMAX; e += 64) P.owner[e] = 0xFFFFFFFFu;
-            int id;
-            float wt;
-            route_wave<4>(a.logits, a.E, a.renorm, lane, id, wt);
-            if (lane < SLOTS) {
-                P.id[lane] = (uint16_t)id;
-                P.wt[lane] = wt;
-                P.owner[id] = (uint32_t)lane; // after the clear: one wave's LDS writes stay in order
-                if (publish) {
-                    a.ids[lane] = (uint16_t)id;
-                    a.w[lane] = wt;
-                }
-            }
-            if (lane == 0) {
-                P.valid[0] = (1ull << SLOTS) - 1;
-                P.valid[1] = 0;
-            }
-        }
-        lds_barrier();
-        return 0u;
-    }
     for (int e = tid; e < DEC_EMAX; e += blockDim.x) P.owner[e] = 0xFFFFFFFFu;
     if (a.logits) {
         for (int t = wv; t < a.M; t += nw) {
@@ -163,210 +145,514 @@ struct DecShape {
     static_assert(NCH <= 64, "chunk sums of squares: one per lane");
 };
 
-template <int H, int MT>
-struct GateUpLds {
-    uint32_t xq[MT][(H / 32) * XQS]; // int8 planes per served token
-    float xsc[MT][H / 32];           // chunk scales
-    float xss[MT][H / 32];           // chunk sums of squares
-    int pair[MT];
-    int n;
-};
-struct DownLds {
-    float part[DEC_MAXP][DEC_ROWS];
-    int first[DEC_MAXP];
-    int nf;
+// ---------------------------------------------------------------- gate/up
+// A step is RPS consecutive row pairs (W1 rows and the same W3 rows) of one selected expert:
+// one 16-byte qs piece of each matrix per lane.  The U selected experts are numbered u in
+// slot order; expert u owns steps u*SPE .. u*SPE + SPE-1.  Wave gw of the NW = 4 * gridDim.x
+// waves takes steps gw, gw + NW, gw + 2 NW, ...: with one workgroup per CU every SIMD gets
+// floor or ceil of U*SPE / NW steps, and an expert's rows -- the shared expert's, which serve
+// every token, included -- are spread over all waves instead of one workgroup's.
+template <int H, int I>
+struct GuShape {
+    static constexpr int SBR = H / QK, LPR = SBR * 8, RPS = 64 / LPR, SPE = I / RPS, NCH = H / 32;
+    static_assert(LPR <= 64 && 64 % LPR == 0 && I % RPS == 0, "a row must tile a wave");
+    static_assert(NCH <= 64, "chunk sums of squares: one per lane");
 };
 
-// ---------------------------------------------------------------- gate/up item
-template <int H, int I, int MT, int RP>
-__device__ __forceinline__ void gate_up_item(const DecodeArgs &a, const DecodePlan &P, GateUpLds<H, MT> &L, int item) {
-    using S = DecShape<H, I, RP>;
-    constexpr int SBR = S::SBR1, LPR = S::LPR1, RPS = S::RPS1, RPW = S::RPW1, NCH = S::NCH;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int p = item / S::NCHK, chunk = item - p * S::NCHK;
-    const int e = P.id[p];
-    if (!pair_valid(P, p) || P.owner[e] != (uint32_t)p) return; // the whole workgroup
-    // the pairs this item serves: every valid pair naming e (at most one per token)
-    const int np = a.M * SLOTS;
-    if (wv == 0) {
-        const int n = collect_pairs(np, lane, L.pair, [&](int q) { return pair_valid(P, q) && P.id[q] == e; });
-        if (lane == 0) L.n = n;
+// One step's loads for this lane: its qs piece and its super-block header of both matrices.
+struct GuLoad {
+    u32x4 q1, q3;
+    u32x2 h1, h3;
+};
+
+template <int H, int I>
+__device__ __forceinline__ GuLoad gu_load(const uint8_t *W1, const uint8_t *W3, int row, int sb, int ib) {
+    constexpr int SBR = GuShape<H, I>::SBR;
+    GuLoad l;
+    l.q1 = ldg<u32x4>(W1 + split_qs<SBR>(row, sb) + 16 * ib);
+    l.q3 = ldg<u32x4>(W3 + split_qs<SBR>(row, sb) + 16 * ib);
+    l.h1 = ldg<u32x2>(W1 + split_hdr<I, SBR>(row, sb));
+    l.h3 = ldg<u32x2>(W3 + split_hdr<I, SBR>(row, sb));
+    return l;
+}
+
+// Signed codebook bytes and sub-block scales of one step's two pieces.
+struct GuDec {
+    uint32_t k1[8], k3[8];
+    float d1, d3;
+};
+
+__device__ __forceinline__ void gu_decode(const GuLoad &l, int ib, GuDec &d) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        kv_signed8(l.q1[i], d.k1[2 * i], d.k1[2 * i + 1]);
+        kv_signed8(l.q3[i], d.k3[2 * i], d.k3[2 * i + 1]);
     }
-    lds_barrier();
-    const int n = L.n;
-    // Loads: this thread's activation chunks (staged below), then the wave's weight rows;
-    // the staging waits for the former only.  The barriers up to the compute loop are
-    // LDS-only: __syncthreads would also wait for every weight load in flight.
-    constexpr int SPT = (MT * NCH + 255) / 256; // chunks per thread
-    f32x4 v[SPT][8];
-    int kc[SPT];
+    d.d1 = sub_scale(l.h1, ib);
+    d.d3 = sub_scale(l.h3, ib);
+}
+
+// Row totals of g and u over the LPR lanes of a row in one chain: after the first exchange
+// the even lanes carry g and the odd lanes u, and every later level adds lanes of equal parity
+// (the other pair of the quad, the row rotated by 4 and by 8, then the gfx950 row swaps), so
+// each lane ends with its parity's total.
+template <int LPR>
+__device__ __forceinline__ float gu_totals(float g, float u, int lane) {
+    static_assert(LPR == 16 || LPR == 32 || LPR == 64, "rows of 16, 32 or 64 lanes");
+    const bool odd = lane & 1;
+    float a = odd ? u : g;
+    a += dpp_mov<0xB1>(odd ? g : u); // quad_perm [1,0,3,2]
+    a += dpp_mov<0x4E>(a);           // quad_perm [2,3,0,1]
+    a += dpp_mov<0x124>(a);          // row_ror:4
+    a += dpp_mov<0x128>(a);          // row_ror:8
+    if constexpr (LPR >= 32) {
+        const auto sw = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, a),
+                                                         false, false);
+        const uint32_t s0 = sw[0], s1 = sw[1];
+        a = __builtin_bit_cast(float, s0) + __builtin_bit_cast(float, s1);
+    }
+    if constexpr (LPR >= 64) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, a),
+                                                         false, false);
+        const uint32_t s0 = sw[0], s1 = sw[1];
+        a = __builtin_bit_cast(float, s0) + __builtin_bit_cast(float, s1);
+    }
+    return a;
+}
+
+// One (row pair, token): the g and u dots of this lane's sub-block against the token's int8
+// planes (scale sx), their row totals, and h = silu(g) * u stored by the row's first lane.
+template <int LPR>
+__device__ __forceinline__ void gu_row(const GuDec &d, const uint32_t (&xh)[8], const uint32_t (&xl)[8], float sx,
+                                       float inv, float *hp, int gsb, int lane) {
+    const float g = (d.d1 * sx) * subblock_idot(d.k1, xh, xl);
+    const float u = (d.d3 * sx) * subblock_idot(d.k3, xh, xl);
+    const float t = inv * gu_totals<LPR>(g, u, lane);
+    const float tu = dpp_mov<0xB1>(t); // at an even lane: its odd partner's total, u
+    if (gsb == 0) *hp = silu_rcp(t) * tu;
+}
+
+// 32 activations (eight quads) -> this chunk's int8 planes, scale (NaN when an activation is
+// not finite, so every row it meets is NaN) and sum of squares.
+__device__ __forceinline__ void quant_chunk(const f32x4 (&v)[8], uint32_t (&xh)[8], uint32_t (&xl)[8], float &sx,
+                                            float &ss) {
+    float am = 0.f;
+    bool finite = true;
+    ss = 0.f;
 #pragma unroll
-    for (int j = 0; j < SPT; ++j) {
-        const int i = tid + 256 * j;
-        kc[j] = i < n * NCH ? i : -1;
-        if (kc[j] >= 0) {
-            const int k = i / NCH, c = i - k * NCH;
-            const f32x4 *src = reinterpret_cast<const f32x4 *>(a.x + (size_t)(L.pair[k] / SLOTS) * H + 32 * c);
+    for (int u = 0; u < 8; ++u)
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[j][u] = ldg<f32x4>(src + u);
+        for (int e4 = 0; e4 < 4; ++e4) {
+            const float f = fabsf(v[u][e4]);
+            finite = finite && f <= 3.4028234e38f;
+            am = fmaxf(am, f);
+            ss = __builtin_fmaf(v[u][e4], v[u][e4], ss);
         }
-    }
+    const float rq = quant_ratio(am);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) quant4(v[u], rq, xh[u], xl[u]);
+    sx = finite ? am * (1.0f / 127.0f) : __builtin_nanf("");
+}
+
+__device__ __forceinline__ float rms_factor(int rmsnorm, float ss_wave, int H) {
+    return rmsnorm ? 1.0f / sqrtf(ss_wave * (1.0f / (float)H) + 1e-6f) : 1.0f;
+}
+
+// ---------------------------------------------------------------- gate/up, M = 1
+// No plan and no barrier: every wave routes the token itself (the top-8 code of
+// moe_router_topk, so all agree bit for bit) or reads its 9 ids, checks them by the rule of
+// build_plan, quantizes the lane's chunk of x into registers, and runs its steps.  Slot order
+// puts the shared expert first: u = 0 is slot 8, u = 1.. the valid routed slots ascending.
+// Workgroup 0 publishes the routing (ids and w, for the caller and the down launch) or raises
+// the flags of invalid ids.
+template <int H, int I>
+__global__ __launch_bounds__(256) void k_dec_gate_up_m1(DecodeArgs a) {
+    using S = GuShape<H, I>;
+    constexpr int LPR = S::LPR, RPS = S::RPS, SPE = S::SPE, NCH = S::NCH;
+    constexpr int G = 5; // steps per round of loads (one round with 256 CUs)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int gw = (int)blockIdx.x * 4 + wv, NW = (int)gridDim.x * 4;
     const int gsb = lane % LPR, rr = lane / LPR, sb = gsb >> 3, ib = gsb & 7;
-    const int rbase = (chunk * 4 + wv) * RPW;
-    const uint8_t *W1 = expert_w(a.L.w1, a.L.s1, a.L.sw1, e, a.E);
-    const uint8_t *W3 = expert_w(a.L.w3, a.L.s3, a.L.sw3, e, a.E);
-    u32x4 q1[RP], q3[RP];
-    u32x2 h1[RP], h3[RP];
+    // this lane's chunk of x, requested first
+    f32x4 xv[8];
 #pragma unroll
-    for (int r = 0; r < RP; ++r) {
-        const int row = rbase + r * RPS + rr;
-        q1[r] = ldg<u32x4>(W1 + split_qs<SBR>(row, sb) + 16 * ib);
-        q3[r] = ldg<u32x4>(W3 + split_qs<SBR>(row, sb) + 16 * ib);
-        h1[r] = ldg<u32x2>(W1 + split_hdr<I, SBR>(row, sb));
-        h3[r] = ldg<u32x2>(W3 + split_hdr<I, SBR>(row, sb));
+    for (int u = 0; u < 8; ++u) xv[u] = ldg<f32x4>(a.x + 32 * gsb + 4 * u);
+    // routing of the token: lane p < 9 holds slot p
+    int id;
+    float wt = 1.0f;
+    if (a.logits) {
+        route_wave<4>(a.logits, a.E, a.renorm, lane, id, wt);
+    } else {
+        id = lane < SLOTS ? (int)a.ids[lane] : 0;
     }
-    // the activations as int8 planes: one 32-element chunk per thread and step
+    bool ok = lane < SLOTS && id <= a.E;
+    bool dup = false;
 #pragma unroll
-    for (int j = 0; j < SPT; ++j) {
-        if (kc[j] < 0) continue;
-        const int k = kc[j] / NCH, c = kc[j] - k * NCH;
-        float am = 0.f, ss = 0.f;
-        bool finite = true;
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-#pragma unroll
-            for (int e4 = 0; e4 < 4; ++e4) {
-                const float f = fabsf(v[j][u][e4]);
-                finite = finite && f <= 3.4028234e38f;
-                am = fmaxf(am, f);
-                ss = __builtin_fmaf(v[j][u][e4], v[j][u][e4], ss);
+    for (int s2 = 0; s2 < SLOTS - 1; ++s2)
+        dup = dup || (s2 < lane && __builtin_amdgcn_readlane(id, s2) == id);
+    ok = ok && !dup;
+    const uint32_t vm = (uint32_t)__ballot(ok) & 0x1FFu;
+    if (blockIdx.x == 0 && wv == 0) {
+        if (a.logits) {
+            if (lane < SLOTS) {
+                a.ids[lane] = (uint16_t)id;
+                a.w[lane] = wt;
             }
-        const float rq = quant_ratio(am);
-        uint32_t hw[8], lw[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) quant4(v[j][u], rq, hw[u], lw[u]);
-        u32x4 *dst = reinterpret_cast<u32x4 *>(&L.xq[k][c * XQS]);
-        dst[0] = u32x4{hw[0], hw[1], hw[2], hw[3]};
-        dst[1] = u32x4{hw[4], hw[5], hw[6], hw[7]};
-        dst[2] = u32x4{lw[0], lw[1], lw[2], lw[3]};
-        dst[3] = u32x4{lw[4], lw[5], lw[6], lw[7]};
-        // a non-finite activation makes its chunk's scale NaN, so the rows it meets are NaN
-        L.xsc[k][c] = finite ? am * (1.0f / 127.0f) : __builtin_nanf("");
-        L.xss[k][c] = ss;
-    }
-    // codebook bytes and sub-block scales, once for all served tokens
-    uint32_t k1[RP][8], k3[RP][8];
-    float d1[RP], d3[RP];
-#pragma unroll
-    for (int r = 0; r < RP; ++r) {
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            kv_signed8(q1[r][d], k1[r][2 * d], k1[r][2 * d + 1]);
-            kv_signed8(q3[r][d], k3[r][2 * d], k3[r][2 * d + 1]);
+        } else {
+            const uint32_t fl = (__ballot(lane < SLOTS && id > a.E) ? MOE_DEVFLAG_BAD_ID : 0u) |
+                                (__ballot(lane < SLOTS && id <= a.E && dup) ? MOE_DEVFLAG_DUP_ID : 0u);
+            if (lane == 0 && fl) set_flag(a.flags, fl);
         }
-        d1[r] = sub_scale(h1[r], ib);
-        d3[r] = sub_scale(h3[r], ib);
     }
-    lds_barrier();
-    for (int k = 0; k < n; ++k) {
-        float inv = 1.0f;
-        if (a.rmsnorm) {
-            const float ss = wave_sum(lane < NCH ? L.xss[k][lane] : 0.f);
-            inv = 1.0f / sqrtf(ss * (1.0f / (float)H) + 1e-6f);
-        }
-        const u32x4 *cq = reinterpret_cast<const u32x4 *>(&L.xq[k][gsb * XQS]);
-        const u32x4 c0 = cq[0], c1 = cq[1], c2 = cq[2], c3 = cq[3];
-        const uint32_t xh[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
-        const uint32_t xl[8] = {c2[0], c2[1], c2[2], c2[3], c3[0], c3[1], c3[2], c3[3]};
-        const float sx = L.xsc[k][gsb];
-        float *hp = a.hbuf + (size_t)L.pair[k] * I + rbase + rr;
+    // slot order, shared first: bit r of vr = rank position r, slot (r + 8) % 9
+    const uint32_t vr = ((vm >> 8) & 1u) | ((vm & 0xFFu) << 1);
+    const int U = __builtin_popcount(vm), NS = U * SPE;
+    const int nk = gw < NS ? (NS - gw + NW - 1) / NW : 0;
+    auto slot_of = [&](int u) __attribute__((always_inline)) {
+        uint32_t m = vr;
+        if (m != 0x1FFu)
+            for (int i = 0; i < u; ++i) m &= m - 1u;
+        const int r = m == 0x1FFu ? u : __builtin_ctz(m);
+        return r == 0 ? SLOTS - 1 : r - 1;
+    };
+    uint32_t xh[8], xl[8];
+    float sx = 0.f, inv = 1.0f;
+    bool staged = false;
+    for (int k0 = 0; k0 < nk; k0 += G) {
+        GuLoad ld[G];
 #pragma unroll
-        for (int r = 0; r < RP; ++r) {
-            float g = (d1[r] * sx) * subblock_idot(k1[r], xh, xl);
-            float u = (d3[r] * sx) * subblock_idot(k3[r], xh, xl);
-            g = inv * row_total<LPR>(g);
-            u = inv * row_total<LPR>(u);
-            if (gsb == row_total_lane<LPR>()) hp[r * RPS] = silu(g) * u;
+        for (int g = 0; g < G; ++g) {
+            const int st = min(gw + (k0 + g) * NW, NS - 1); // past the last step: a valid re-read
+            const int u = st / SPE, rs = st - u * SPE;
+            const int e = __builtin_amdgcn_readlane(id, slot_of(u));
+            ld[g] = gu_load<H, I>(expert_w(a.L.w1, a.L.s1, a.L.sw1, e, a.E),
+                                  expert_w(a.L.w3, a.L.s3, a.L.sw3, e, a.E), rs * RPS + rr, sb, ib);
+        }
+        if (!staged) {
+            // the activations as int8 planes while the weights are in flight
+            float ss;
+            quant_chunk(xv, xh, xl, sx, ss);
+            inv = rms_factor(a.rmsnorm, wave_sum(lane < NCH ? ss : 0.f), H);
+            staged = true;
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int st = gw + (k0 + g) * NW;
+            if (st >= NS) break;
+            const int u = st / SPE, rs = st - u * SPE;
+            GuDec d;
+            gu_decode(ld[g], ib, d);
+            gu_row<LPR>(d, xh, xl, sx, inv, a.hbuf + (size_t)slot_of(u) * I + rs * RPS + rr, gsb, lane);
         }
     }
 }
 
-// ---------------------------------------------------------------- down item
-// NW waves per workgroup: 9 at M = 1 (one per selected expert, all loads in flight at once),
-// 16 beyond (each wave takes every NW-th expert)
-template <int H, int I, int NW>
-__device__ __forceinline__ void down_item(const DecodeArgs &a, const DecodePlan &P, DownLds &L, int item) {
+// ---------------------------------------------------------------- prep, 2 <= M <= 8
+// One workgroup of eight waves, once per call: the routing (wave t routes token t when the call
+// passed logits, and the ids and weights are published), pair validity and the device flags of
+// invalid ids (build_plan), the selected experts in slot order with the tokens each serves,
+// every token's activations as int8 planes and its RMSNorm factor -- the plan block every
+// gate/up workgroup then copies instead of building it.
+template <int H>
+struct PrepLds {
+    DecodePlan P;
+    float xss[MOE_DECODE_MAX_M][H / 32];
+    uint8_t uof[DEC_MAXP];
+    DecPlan<H, MOE_DECODE_MAX_M> G;
+};
+
+template <int H>
+__global__ __launch_bounds__(512) void k_dec_prep(DecodeArgs a) {
+    constexpr int NCH = H / 32;
+    static_assert(MOE_DECODE_MAX_M * NCH <= 512 * 2, "two chunks per thread at most");
+    __shared__ PrepLds<H> L;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int np = a.M * SLOTS;
+    constexpr int SPT = (MOE_DECODE_MAX_M * NCH + 511) / 512;
+    // activation chunks, requested first
+    f32x4 v[SPT][8];
+#pragma unroll
+    for (int j = 0; j < SPT; ++j) {
+        const int i = min(tid + 512 * j, a.M * NCH - 1);
+        const int t = i / NCH, c = i - t * NCH;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[j][u] = ldg<f32x4>(a.x + (size_t)t * H + 32 * c + 4 * u);
+    }
+    const uint32_t fl = build_plan(a, L.P, true); // ends with a barrier
+    if (tid == 0 && fl) set_flag(a.flags, fl);
+#pragma unroll
+    for (int j = 0; j < SPT; ++j) {
+        const int i = tid + 512 * j;
+        if (i >= a.M * NCH) continue;
+        const int t = i / NCH, c = i - t * NCH;
+        uint32_t xh[8], xl[8];
+        float sx, ss;
+        quant_chunk(v[j], xh, xl, sx, ss);
+        u32x4 *dst = reinterpret_cast<u32x4 *>(&L.G.xq[t][c * XQS]);
+        dst[0] = u32x4{xh[0], xh[1], xh[2], xh[3]};
+        dst[1] = u32x4{xh[4], xh[5], xh[6], xh[7]};
+        dst[2] = u32x4{xl[0], xl[1], xl[2], xl[3]};
+        dst[3] = u32x4{xl[4], xl[5], xl[6], xl[7]};
+        L.G.xsc[t][c] = sx;
+        L.xss[t][c] = ss;
+    }
+    lds_barrier(); // the staged chunks, for the RMSNorm factors below
+    if (wv == 0) {
+        // the selected experts in slot order (each one's first valid pair, ascending) ...
+        int list[2];
+        const int U = collect_pairs(np, lane, reinterpret_cast<int *>(L.G.tmask), [&](int q) {
+            return pair_valid(L.P, q) && L.P.owner[L.P.id[q]] == (uint32_t)q;
+        });
+#pragma unroll
+        for (int r = 0; r < 2; ++r) list[r] = lane + 64 * r < U ? (int)L.G.tmask[lane + 64 * r] : 0;
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+            if (lane + 64 * r < U) {
+                L.uof[list[r]] = (uint8_t)(lane + 64 * r);
+                L.G.uexp[lane + 64 * r] = L.P.id[list[r]];
+                L.G.tmask[lane + 64 * r] = 0u;
+            }
+        // ... the tokens each serves, with their pairs ...
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int q = lane + 64 * r;
+            if (q < np && pair_valid(L.P, q)) {
+                const int t = q / SLOTS, u = L.uof[L.P.owner[L.P.id[q]]];
+                atomicOr(&L.G.tmask[u], 1u << t);
+                L.G.tpair[u][t] = (uint8_t)q;
+            }
+        }
+        // ... and every token's RMSNorm factor
+        for (int t = 0; t < a.M; ++t)
+            L.G.inv[t] = rms_factor(a.rmsnorm, wave_sum(lane < NCH ? L.xss[t][lane] : 0.f), H);
+        if (lane == 0) L.G.U = U;
+    }
+    __syncthreads();
+    // the block out: the head, then the M token rows of the planes and of the scales
+    const uint8_t *src = reinterpret_cast<const uint8_t *>(&L.G);
+    uint8_t *dst = reinterpret_cast<uint8_t *>(a.plan);
+    constexpr int XQR = NCH * XQS * 4, XSR = NCH * 4;
+    constexpr size_t XSO = DEC_PLAN_HEAD + (size_t)MOE_DECODE_MAX_M * XQR;
+    for (int i = 16 * tid; i < (int)DEC_PLAN_HEAD; i += 16 * 512)
+        *reinterpret_cast<u32x4 *>(dst + i) = *reinterpret_cast<const u32x4 *>(src + i);
+    for (int i = 16 * tid; i < a.M * XQR; i += 16 * 512)
+        *reinterpret_cast<u32x4 *>(dst + DEC_PLAN_HEAD + i) = *reinterpret_cast<const u32x4 *>(src + DEC_PLAN_HEAD + i);
+    for (int i = 16 * tid; i < a.M * XSR; i += 16 * 512)
+        *reinterpret_cast<u32x4 *>(dst + XSO + i) = *reinterpret_cast<const u32x4 *>(src + XSO + i);
+}
+
+// ---------------------------------------------------------------- gate/up, 2 <= M <= 8
+// Each workgroup copies the plan block into LDS (one round of loads), then each wave runs its
+// steps with two rounds of G steps' loads in flight.
+template <int H, int I, int MT>
+__global__ __launch_bounds__(256) void k_dec_gate_up_mt(DecodeArgs a) {
+    using S = GuShape<H, I>;
+    constexpr int LPR = S::LPR, RPS = S::RPS, SPE = S::SPE, NCH = S::NCH;
+    constexpr int G = 4;
+    constexpr int XQR = NCH * XQS * 4, XSR = NCH * 4;
+    constexpr int PLB = (int)DEC_PLAN_HEAD + MT * (XQR + XSR); // plan bytes this launch copies
+    constexpr int CPT = (PLB / 16 + 255) / 256;                  // 16-byte pieces per thread
+    __shared__ DecPlan<H, MT> L;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int gw = (int)blockIdx.x * 4 + wv, NW = (int)gridDim.x * 4;
+    {
+        // the head, the M rows of planes and the M rows of scales (global rows are
+        // MOE_DECODE_MAX_M apart, local ones MT): all loads in flight, then the stores
+        const uint8_t *src = reinterpret_cast<const uint8_t *>(a.plan);
+        uint8_t *dst = reinterpret_cast<uint8_t *>(&L);
+        const int nq = (int)DEC_PLAN_HEAD / 16 + a.M * (XQR + XSR) / 16;
+        u32x4 cv[CPT];
+        int co[CPT];
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int k = min(tid + 256 * j, nq - 1);
+            int gi, li; // byte offsets
+            if (k < (int)DEC_PLAN_HEAD / 16) {
+                gi = li = 16 * k;
+            } else if (k < (int)DEC_PLAN_HEAD / 16 + a.M * XQR / 16) {
+                gi = li = 16 * k;
+            } else {
+                const int r = 16 * k - (int)DEC_PLAN_HEAD - a.M * XQR;
+                gi = (int)DEC_PLAN_HEAD + MOE_DECODE_MAX_M * XQR + r;
+                li = (int)DEC_PLAN_HEAD + MT * XQR + r;
+            }
+            co[j] = tid + 256 * j < nq ? li : -1;
+            cv[j] = ldg<u32x4>(src + gi);
+        }
+#pragma unroll
+        for (int j = 0; j < CPT; ++j)
+            if (co[j] >= 0) *reinterpret_cast<u32x4 *>(dst + co[j]) = cv[j];
+    }
+    __syncthreads();
+    const int gsb = lane % LPR, rr = lane / LPR, sb = gsb >> 3, ib = gsb & 7;
+    const int NS = L.U * SPE;
+    const int nk = gw < NS ? (NS - gw + NW - 1) / NW : 0;
+    const int nit = (nk + G - 1) / G;
+    if (nit == 0) return;
+    auto issue = [&](GuLoad (&ld)[G], int it) __attribute__((always_inline)) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int st = min(gw + (it * G + g) * NW, NS - 1); // past the last step: a valid re-read
+            const int u = st / SPE, rs = st - u * SPE;
+            const int e = L.uexp[u];
+            ld[g] = gu_load<H, I>(expert_w(a.L.w1, a.L.s1, a.L.sw1, e, a.E),
+                                  expert_w(a.L.w3, a.L.s3, a.L.sw3, e, a.E), rs * RPS + rr, sb, ib);
+        }
+    };
+    auto compute = [&](const GuLoad (&ld)[G], int it) __attribute__((always_inline)) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int st = gw + (it * G + g) * NW;
+            if (st >= NS) break;
+            const int u = st / SPE, rs = st - u * SPE;
+            GuDec d;
+            gu_decode(ld[g], ib, d);
+            uint32_t tm = L.tmask[u];
+            while (tm) {
+                const int t = __builtin_ctz(tm);
+                tm &= tm - 1u;
+                const u32x4 *cq = reinterpret_cast<const u32x4 *>(&L.xq[t][gsb * XQS]);
+                const u32x4 c0 = cq[0], c1 = cq[1], c2 = cq[2], c3 = cq[3];
+                const uint32_t xh[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+                const uint32_t xl[8] = {c2[0], c2[1], c2[2], c2[3], c3[0], c3[1], c3[2], c3[3]};
+                gu_row<LPR>(d, xh, xl, L.xsc[t][gsb], L.inv[t], a.hbuf + (size_t)L.tpair[u][t] * I + rs * RPS + rr,
+                            gsb, lane);
+            }
+        }
+    };
+    GuLoad A[G], B[G];
+    issue(A, 0);
+    issue(B, 1);
+    int it = 0;
+    for (; it + 2 < nit; it += 2) {
+        compute(A, it);
+        issue(A, it + 2);
+        compute(B, it + 1);
+        issue(B, it + 3);
+    }
+    compute(A, it);
+    compute(B, it + 1);
+}
+
+// ---------------------------------------------------------------- down, 2 <= M <= 8
+// Eight waves per workgroup of 8 output rows.  Every valid (token, slot) pair is one element:
+// the element's expert's W2 rows against the pair's h, times c * w, into LDS; the valid pairs
+// are dealt to the waves in ascending order, so the shared expert's M pairs -- and any two
+// tokens' shared routed expert -- go to different waves (repeated W2 rows are L2 hits).  A
+// wave requests the W2 rows of all its elements at once, then the h of its elements two
+// ahead.  Each wave checks pair validity itself, by the rule of build_plan, from the ids in
+// its own LDS region: no barrier until the slot-order sums.
+template <int H, int I, int MT>
+__global__ __launch_bounds__(512) void k_dec_down_mt(DecodeArgs a) {
     using S = DecShape<H, I>;
     constexpr int SBR = S::SBR2, LPR = S::LPR2, RPS = S::RPS2, STEPS = S::STEPS;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    constexpr int NWV = 8, NPM = MT * SLOTS, MAXE = (NPM + NWV - 1) / NWV, HD = 2;
+    static_assert(NPM <= 128 && MT * DEC_ROWS <= 64 * NWV, "pairs in two registers, one output per thread");
+    __shared__ float part[NPM][DEC_ROWS];
+    __shared__ uint16_t sid[NWV][NPM];
+    __shared__ float swt[NWV][NPM];
+    __shared__ uint8_t slist[NWV][MAXE];
+    __shared__ uint64_t svalid[2];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int np = a.M * SLOTS;
-    const int n0 = item * DEC_ROWS;
-    // the residual this thread adds at the end, requested now (one value per thread)
+    const int n0 = blockIdx.x * DEC_ROWS;
     float yres = 0.f;
-    if (a.accumulate && tid < a.M * DEC_ROWS)
-        yres = a.y[(size_t)(tid / DEC_ROWS) * H + n0 + tid % DEC_ROWS];
-    // the selected experts: each one's first valid pair, ascending
-    if (wv == 0) {
-        const int nf = collect_pairs(np, lane, L.first,
-                                     [&](int q) { return pair_valid(P, q) && P.owner[P.id[q]] == (uint32_t)q; });
-        if (lane == 0) L.nf = nf;
+    if (a.accumulate && tid < a.M * DEC_ROWS) yres = a.y[(size_t)(tid / DEC_ROWS) * H + n0 + tid % DEC_ROWS];
+    // the routing into this wave's LDS region, then pair validity
+    int idr[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int q = lane + 64 * r;
+        idr[r] = q < np ? (int)a.ids[q] : 0;
+        if (q < np) {
+            sid[wv][q] = (uint16_t)idr[r];
+            swt[wv][q] = a.w[q];
+        }
     }
-    lds_barrier();
-    const int nf = L.nf;
+    uint64_t vb[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int q = lane + 64 * r;
+        bool ok = q < np && idr[r] <= a.E;
+        if (ok) {
+            const int t = q / SLOTS, s = q - t * SLOTS;
+            for (int s2 = 0; s2 < s; ++s2) ok = ok && (int)sid[wv][t * SLOTS + s2] != idr[r];
+        }
+        vb[r] = __ballot(ok);
+    }
+    // this wave's elements: the valid pairs of rank wv, wv + 8, ...
+    const int nv0 = __popcll(vb[0]), nv = nv0 + __popcll(vb[1]);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        if ((vb[r] >> lane) & 1ull) {
+            const int rk = (r ? nv0 : 0) + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(vb[r] >> 32),
+                                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)vb[r], 0u));
+            if (rk % NWV == wv) slist[wv][rk / NWV] = (uint8_t)(lane + 64 * r);
+        }
+    }
+    if (wv == 0 && lane == 0) {
+        svalid[0] = vb[0];
+        svalid[1] = vb[1];
+    }
+    const int ne = nv > wv ? (nv - wv + NWV - 1) / NWV : 0;
     const int gsb = lane % LPR, rr = lane / LPR, sb = gsb >> 3, ib = gsb & 7;
-    for (int u = wv; u < nf; u += NW) {
-        const int q0 = L.first[u];
-        const int e = P.id[q0];
-        // every valid pair naming e, as two 64-bit lane masks
-        const uint64_t m0 = __ballot(lane < np && pair_valid(P, lane) && P.id[lane] == e);
-        const uint64_t m1 = __ballot(lane + 64 < np && pair_valid(P, lane + 64) && P.id[lane + 64] == e);
-        const uint8_t *W2 = expert_w(a.L.w2, a.L.s2, a.L.sw2, e, a.E);
-        u32x4 qs[STEPS];
-        u32x2 hd[STEPS];
+    if (ne > 0) {
+        // h of the first HD elements, then W2 rows of every element (past the last one: a valid
+        // re-read): loads complete in order, so element k waits only for its own W2 rows and
+        // what came before them, and its products overlap the later elements' W2 stream
+        int qe[MAXE];
 #pragma unroll
-        for (int st = 0; st < STEPS; ++st) {
-            const int row = n0 + st * RPS + rr;
-            qs[st] = ldg<u32x4>(W2 + split_qs<SBR>(row, sb) + 16 * ib);
-            hd[st] = ldg<u32x2>(W2 + split_hdr<H, SBR>(row, sb));
-        }
-        // the first pair's h travels with the weights
-        float hv[32];
-        load32(a.hbuf + (size_t)q0 * I + 32 * gsb, hv);
-        uint32_t kv[STEPS][8];
-        float dl[STEPS];
+        for (int k = 0; k < MAXE; ++k) qe[k] = slist[wv][min(k, ne - 1)];
+        float hv[HD][32];
 #pragma unroll
-        for (int st = 0; st < STEPS; ++st) {
+        for (int j = 0; j < HD; ++j) load32(a.hbuf + (size_t)qe[min(j, MAXE - 1)] * I + 32 * gsb, hv[j]);
+        u32x4 qs[MAXE][STEPS];
+        u32x2 hd[MAXE][STEPS];
 #pragma unroll
-            for (int d = 0; d < 4; ++d) kv_biased8(qs[st][d], kv[st][2 * d], kv[st][2 * d + 1]);
-            dl[st] = sub_scale(hd[st], ib);
-        }
-        uint64_t rest[2] = {m0, m1};
-        int q = q0;
-        while (true) {
-            rest[q >> 6] &= ~(1ull << (q & 63));
-            float hs = 0.f;
-#pragma unroll
-            for (int i = 0; i < 32; ++i) hs += hv[i];
-            const float wq = a.c * P.wt[q];
+        for (int k = 0; k < MAXE; ++k) {
+            const int e = sid[wv][qe[k]];
+            const uint8_t *W2 = expert_w(a.L.w2, a.L.s2, a.L.sw2, e, a.E);
 #pragma unroll
             for (int st = 0; st < STEPS; ++st) {
-                float d = dl[st] * subblock_dot(kv[st], hv, hs);
-                d = group_sum<LPR>(d);
-                if (gsb == 0) L.part[q][st * RPS + rr] = wq * d;
+                const int row = n0 + st * RPS + rr;
+                qs[k][st] = ldg<u32x4>(W2 + split_qs<SBR>(row, sb) + 16 * ib);
+                hd[k][st] = ldg<u32x2>(W2 + split_hdr<H, SBR>(row, sb));
             }
-            if (!(rest[0] | rest[1])) break;
-            q = rest[0] ? __builtin_ctzll(rest[0]) : 64 + __builtin_ctzll(rest[1]);
-            load32(a.hbuf + (size_t)q * I + 32 * gsb, hv);
+        }
+#pragma unroll
+        for (int k = 0; k < MAXE; ++k) {
+            if (k < ne) {
+                const int q = qe[k];
+                float hs = 0.f;
+#pragma unroll
+                for (int i = 0; i < 32; ++i) hs += hv[k % HD][i];
+                const float wq = a.c * swt[wv][q];
+#pragma unroll
+                for (int st = 0; st < STEPS; ++st) {
+                    uint32_t kv[8];
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) kv_biased8(qs[k][st][d], kv[2 * d], kv[2 * d + 1]);
+                    float d = sub_scale(hd[k][st], ib) * subblock_dot(kv, hv[k % HD], hs);
+                    d = group_sum<LPR>(d);
+                    if (gsb == 0) part[q][st * RPS + rr] = wq * d;
+                }
+            }
+            if (k + HD < MAXE) load32(a.hbuf + (size_t)qe[k + HD] * I + 32 * gsb, hv[k % HD]);
         }
     }
     __syncthreads();
-    static_assert(MOE_DECODE_MAX_M * DEC_ROWS <= 64 * NW, "one output per thread");
     if (tid < a.M * DEC_ROWS) {
         const int t = tid / DEC_ROWS, r = tid - t * DEC_ROWS;
         float sum = 0.f;
 #pragma unroll
-        for (int s = 0; s < SLOTS; ++s)
-            if (pair_valid(P, t * SLOTS + s)) sum += L.part[t * SLOTS + s][r];
+        for (int s = 0; s < SLOTS; ++s) {
+            const int q = t * SLOTS + s;
+            if ((svalid[q >> 6] >> (q & 63)) & 1ull) sum += part[q][r];
+        }
         a.y[(size_t)t * H + n0 + r] = yres + sum;
     }
 }
@@ -429,53 +715,46 @@ __global__ __launch_bounds__(64 * SLOTS) void k_dec_down_m1(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------- the launches
-// MT: the most tokens one expert can serve in this call (M rounded up to 1, 2, 4, 8).
-template <int H, int I, int MT, int RP>
-__global__ __launch_bounds__(256) void k_dec_gate_up(DecodeArgs a) {
-    __shared__ DecodePlan P;
-    __shared__ GateUpLds<H, MT> L;
-    const uint32_t fl = build_plan(a, P, blockIdx.x == 0); // ends with a barrier
-    if (blockIdx.x == 0 && threadIdx.x == 0 && fl) set_flag(a.flags, fl);
-    gate_up_item<H, I, MT, RP>(a, P, L, blockIdx.x);
-}
-
-template <int H, int I, int NW>
-__global__ __launch_bounds__(64 * NW) void k_dec_down(DecodeArgs a) {
-    __shared__ DecodePlan P;
-    __shared__ DownLds L;
-    (void)build_plan(a, P, false);
-    down_item<H, I, NW>(a, P, L, blockIdx.x);
-}
-
-template <int H, int I, int MT, int RP>
-static void launch_gate_up(const DecodeArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL((k_dec_gate_up<H, I, MT, RP>), dim3(a.M * SLOTS * DecShape<H, I, RP>::NCHK), dim3(256), 0, st,
-                       a);
-}
+using DecPlanBig = DecPlan<2048, 8>;
+using DecPlanSmall = DecPlan<512, 2>;
+static_assert(offsetof(DecPlanBig, xq) == DEC_PLAN_HEAD && offsetof(DecPlanSmall, xq) == DEC_PLAN_HEAD,
+              "plan head layout");
+static_assert(sizeof(DecPlan<DEC_MAX_H, MOE_DECODE_MAX_M>) <= decode_plan_floats(DEC_MAX_H) * 4, "plan block size");
 
 template <int H, int I>
 static hipError_t launch_decode_t(const DecodeArgs &a, hipStream_t st, KernelTimer *T) {
+    // M >= 2: the prep launch routes (when given logits) and publishes ids/w, so the later
+    // launches read the routing from ids/w and the plan block
+    DecodeArgs b = a;
+    if (a.M >= 2) {
+        TimedLaunch tl(T, MOE_K_DECODE_PREP, st);
+        hipLaunchKernelGGL((k_dec_prep<H>), dim3(1), dim3(512), 0, st, a);
+        b.logits = nullptr;
+    }
     {
         TimedLaunch tl(T, MOE_K_DECODE_GATE_UP, st);
-        if (a.M == 1) launch_gate_up<H, I, 1, 4>(a, st);
-        else if (a.M == 2) launch_gate_up<H, I, 2, 4>(a, st);
-        else if (a.M <= 4) launch_gate_up<H, I, 4, 8>(a, st);
-        else launch_gate_up<H, I, 8, 8>(a, st);
+        const dim3 grid((unsigned)a.nwg), blk(256);
+        if (a.M == 1) hipLaunchKernelGGL((k_dec_gate_up_m1<H, I>), grid, blk, 0, st, a);
+        else if (a.M == 2) hipLaunchKernelGGL((k_dec_gate_up_mt<H, I, 2>), grid, blk, 0, st, b);
+        else if (a.M <= 4) hipLaunchKernelGGL((k_dec_gate_up_mt<H, I, 4>), grid, blk, 0, st, b);
+        else hipLaunchKernelGGL((k_dec_gate_up_mt<H, I, 8>), grid, blk, 0, st, b);
     }
-    // the down launch reads the routing from ids/w (published by the gate/up launch when it
+    // the down launch reads the routing from ids/w (published by the first launch when it
     // routed the tokens itself)
-    DecodeArgs b = a;
     b.logits = nullptr;
     {
         TimedLaunch tl(T, MOE_K_DECODE_DOWN, st);
         if (a.M == 1) hipLaunchKernelGGL((k_dec_down_m1<H, I>), dim3(H / DEC_ROWS), dim3(64 * SLOTS), 0, st, b);
-        else hipLaunchKernelGGL((k_dec_down<H, I, 16>), dim3(H / DEC_ROWS), dim3(1024), 0, st, b);
+        else if (a.M == 2) hipLaunchKernelGGL((k_dec_down_mt<H, I, 2>), dim3(H / DEC_ROWS), dim3(512), 0, st, b);
+        else if (a.M <= 4) hipLaunchKernelGGL((k_dec_down_mt<H, I, 4>), dim3(H / DEC_ROWS), dim3(512), 0, st, b);
+        else hipLaunchKernelGGL((k_dec_down_mt<H, I, 8>), dim3(H / DEC_ROWS), dim3(512), 0, st, b);
     }
     return hipGetLastError();
 }
 
 hipError_t launch_decode(int H, int I, const DecodeArgs &a, hipStream_t st, KernelTimer *T) {
-    if (a.M < 1 || a.M > MOE_DECODE_MAX_M || a.E > DEC_EMAX - 1 || !a.hbuf) return hipErrorInvalidValue;
+    if (a.M < 1 || a.M > MOE_DECODE_MAX_M || a.E > DEC_EMAX - 1 || !a.hbuf || a.nwg < 1 || (a.M >= 2 && !a.plan))
+        return hipErrorInvalidValue;
     if (H == 2048 && I == 512) return launch_decode_t<2048, 512>(a, st, T);
     if (H == 512 && I == 256) return launch_decode_t<512, 256>(a, st, T);
     return hipErrorInvalidValue;

@@ -45,6 +45,7 @@ struct moe_ctx {
     uint16_t *srid = nullptr;    // decode stack: routing of every layer
     float *srw = nullptr;
     int stack_ok = 0;            // all stack workgroups fit on the device at once
+    int ncu = 0;                 // compute units of the device
     uint32_t spin_max = STK_SPIN_DEFAULT; // decode stack: poll rounds before a wait expires
     KernelTimer timer;
 };
@@ -137,7 +138,7 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
         size_t bytes;
     } parts[] = {
         {(void **)&c->flags, 256},
-        {(void **)&c->hbuf, decode_scratch_floats(I) * sizeof(float)},
+        {(void **)&c->hbuf, decode_scratch_floats(H, I) * sizeof(float)},
         {(void **)&c->xh, mm * H * 2},
         {(void **)&c->xinv, mm * 4},
         {(void **)&c->hh, SLOTS * mm * I * 2},
@@ -193,8 +194,10 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
     }
     // The decode stack needs every one of its workgroups resident at once.
     int per_cu = 0, ncu = 0;
-    if (stack_occupancy(H, I, &per_cu) == hipSuccess &&
-        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess)
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || ncu < 1)
+        ncu = 1;
+    c->ncu = ncu;
+    if (stack_occupancy(H, I, &per_cu) == hipSuccess)
         c->stack_ok = (per_cu >= 1 && (long)per_cu * ncu >= stack_blocks(H) && E <= 256) ? 1 : 0;
     *out = c;
     return ok();
@@ -328,7 +331,7 @@ moe_status moe_bucket_fill(moe_ctx *ctx, const uint16_t *ids, const float *w, in
 
 // The checks and launches shared by moe_ffn and moe_ffn_route.  logits == NULL: ids/w are
 // inputs; otherwise the tokens are routed first and ids/w receive the routing.  scr is the
-// decode path's h scratch (decode_scratch_floats(inter)).
+// decode path's scratch (decode_scratch_floats(hidden, inter): h, then the plan block).
 static moe_status ffn_call(const char *fn, moe_ctx *ctx, int layer, const float *x, const float *logits,
                            uint16_t *ids, float *w, int M, float *y, int flags, void *stream, float *hbuf) {
     if (!ctx) return fail(MOE_EINVAL, "%s: null context", fn);
@@ -349,13 +352,8 @@ static moe_status ffn_call(const char *fn, moe_ctx *ctx, int layer, const float 
     KernelTimer *T = timer_for(ctx, st);
     hipError_t he;
     if (M <= MOE_DECODE_MAX_M) {
-        // Routing inside the decode launch repeats the top-8 in every workgroup: it pays for a
-        // separate router launch only while M is small.
-        if (logits && M > DEC_ROUTE_IN_KERNEL_MAX_M) {
-            he = launch_router_topk(logits, M, E, renorm, ids, w, st, T);
-            if (he != hipSuccess) return fail(MOE_EHIP, "%s: router launch: %s", fn, hipGetErrorString(he));
-            logits = nullptr;
-        }
+        // the decode launches route the tokens themselves (M = 1: every gate/up wave; M >= 2:
+        // the prep launch) and publish ids/w
         DecodeArgs a{};
         a.L = ctx->slayers[layer];
         a.x = x;
@@ -364,6 +362,7 @@ static moe_status ffn_call(const char *fn, moe_ctx *ctx, int layer, const float 
         a.w = w;
         a.y = y;
         a.hbuf = hbuf;
+        a.plan = hbuf + decode_hbuf_floats((size_t)I);
         a.flags = ctx->flags;
         a.M = M;
         a.E = E;
@@ -371,6 +370,8 @@ static moe_status ffn_call(const char *fn, moe_ctx *ctx, int layer, const float 
         a.rmsnorm = (flags & MOE_FFN_RMSNORM) ? 1 : 0;
         a.renorm = renorm;
         a.c = c;
+        // gate/up: one workgroup per CU for M = 1 (every SIMD one wave), two beyond
+        a.nwg = ctx->ncu * (M == 1 ? 1 : 2);
         he = launch_decode(H, I, a, st, T);
         if (he != hipSuccess) return fail(MOE_EHIP, "%s: decode launch: %s", fn, hipGetErrorString(he));
         return ok();

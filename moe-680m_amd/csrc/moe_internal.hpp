@@ -33,10 +33,38 @@ struct DecodeArgs {
     uint32_t *flags;      // sticky device flags
     int M, E, accumulate, rmsnorm, renorm;
     float c;
+    int nwg;              // gate/up workgroups (a multiple of the CU count)
+    void *plan;           // 2 <= M <= 8: the plan block (DecPlan<H, MOE_DECODE_MAX_M>) after hbuf
 };
-constexpr int DEC_ROUTE_IN_KERNEL_MAX_M = 2; // moe_ffn_route: larger M launches the router first
-// Floats of the decode path's h scratch for inter size I.
-inline size_t decode_scratch_floats(int I) { return (size_t)MOE_DECODE_MAX_M * SLOTS * I; }
+
+constexpr int DEC_MAXP = MOE_DECODE_MAX_M * SLOTS; // (token, slot) pairs of one decode call
+
+// Plan block of the 2 <= M <= 8 decode launches: written once per call by k_dec_prep, copied
+// into LDS by every gate/up workgroup.  The selected experts in slot order (each one's first
+// valid pair ascending), the tokens each serves with their pairs, every token's RMSNorm factor,
+// and the activations as int8 planes with their chunk scales (MT token rows of each).
+template <int H, int MT>
+struct DecPlan {
+    int U;
+    int pad_[3];
+    float inv[MOE_DECODE_MAX_M];
+    int uexp[DEC_MAXP];
+    uint32_t tmask[DEC_MAXP];
+    uint8_t tpair[DEC_MAXP][MOE_DECODE_MAX_M];
+    uint32_t xq[MT][(H / 32) * XQS]; // int8 planes per token (chunk c at XQS * c)
+    float xsc[MT][H / 32];           // chunk scales
+};
+constexpr size_t DEC_PLAN_HEAD = 16 + 4 * MOE_DECODE_MAX_M + 8 * DEC_MAXP + DEC_MAXP * MOE_DECODE_MAX_M;
+static_assert(DEC_PLAN_HEAD % 16 == 0, "plan rows start 16-byte aligned");
+constexpr size_t DEC_MAX_H = 2048; // the largest hidden size the decode kernels are built for
+// Floats of the decode path's scratch: h [9 * MOE_DECODE_MAX_M][I] f32, then the plan block.
+constexpr size_t decode_hbuf_floats(size_t I) { return (size_t)DEC_MAXP * I; }
+constexpr size_t decode_plan_floats(size_t H) {
+    return (DEC_PLAN_HEAD + MOE_DECODE_MAX_M * (H / 32) * (XQS + 1) * 4 + 255) / 256 * 64;
+}
+inline size_t decode_scratch_floats(int H, int I) {
+    return decode_hbuf_floats((size_t)I) + decode_plan_floats((size_t)H);
+}
 
 struct BucketArgs {
     const uint16_t *ids;
@@ -169,7 +197,7 @@ inline int stile_max_for(int E1) { return E1; }
 // Internal services of moe_api.hip for the entry points defined in other files.
 namespace moe {
 // moe_ffn with ids/w given, its decode path (M <= MOE_DECODE_MAX_M) using hbuf
-// (decode_scratch_floats(inter)) as its h scratch.
+// (decode_scratch_floats(hidden, inter)) as its scratch.
 moe_status ffn_with_scratch(const char *fn, moe_ctx *ctx, int layer, const float *x, const uint16_t *ids,
                             const float *w, int M, float *y, int flags, void *stream, float *hbuf);
 int ctx_device(const moe_ctx *ctx);

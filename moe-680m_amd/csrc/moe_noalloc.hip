@@ -4,13 +4,14 @@
 // call happens in it -- nor in moe_ffn's hot path, but that path's scratch is memory the
 // context allocated).  No counterpart in the reference.
 //
-// `scratch` holds the decode path's h values, [9 * MOE_DECODE_MAX_M][inter <= 512] f32,
-// 147,456 bytes; each GPU the library runs on keeps its own copy until the process ends.  On
+// `scratch` holds the decode path's h values, [9 * MOE_DECODE_MAX_M][inter <= 512] f32, and
+// the plan block of its 2 <= M <= 8 launches (hidden <= 2048): 191,744 bytes; each GPU the
+// library runs on keeps its own copy until the process ends.  On
 // the host the array's name is only a stand-in for the symbol: host code never passes it to a
 // kernel or a copy, but the device address hipGetSymbolAddress returns for it, looked up once
 // per device (with that device current) on the first call there and kept in scratch_dev[].
 // Every call on a GPU shares that GPU's array; nothing in it needs to start at zero (the
-// gate/up launch writes every h value the down launch reads), and calls that overlap on one
+// launches of a call write every h value and plan word they read), and calls that overlap on one
 // GPU -- on two streams at once -- race.
 #include <cstdio>
 #include <mutex>
@@ -22,9 +23,10 @@ using namespace moe;
 namespace {
 
 constexpr int NOALLOC_MAX_INTER = 512;
-constexpr size_t NOALLOC_FLOATS = (size_t)MOE_DECODE_MAX_M * SLOTS * NOALLOC_MAX_INTER;
+constexpr size_t NOALLOC_FLOATS = decode_hbuf_floats(NOALLOC_MAX_INTER) + decode_plan_floats(DEC_MAX_H);
 constexpr size_t NOALLOC_SCRATCH_BYTES = NOALLOC_FLOATS * sizeof(float);
 static __device__ __align__(256) float scratch[NOALLOC_FLOATS];
+static_assert(NOALLOC_FLOATS * sizeof(float) == 191744, "the size the header and the docs state");
 
 constexpr int SCRATCH_MAX_DEVICES = 64;
 std::mutex scratch_mu;
