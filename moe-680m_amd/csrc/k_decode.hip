@@ -46,103 +46,29 @@ namespace moe {
 
 constexpr int DEC_EMAX = 257;                      // owner table: n_experts <= 256, + shared
 
-struct DecodePlan {
-    uint32_t owner[DEC_EMAX]; // first valid pair naming each expert (all ones: none)
-    uint64_t valid[2];        // bit q & 63 of word q >> 6: pair q is valid
-    uint16_t id[DEC_MAXP];
-    float wt[DEC_MAXP];
-};
-
-__device__ __forceinline__ bool pair_valid(const DecodePlan &P, int q) { return (P.valid[q >> 6] >> (q & 63)) & 1u; }
-
-// All threads of the workgroup.  The M*9 ids and weights into LDS -- routed here from the
-// logits when the call passed them (`publish`: also written out to a.ids / a.w) -- then pair
-// validity and each expert's first valid pair.  Returns, in wave 0, the device flags the
-// routing raises (0 elsewhere).  Ends with a barrier.
-__device__ __forceinline__ uint32_t build_plan(const DecodeArgs &a, DecodePlan &P, bool publish) {
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
-    const int np = a.M * SLOTS;
-    for (int e = tid; e < DEC_EMAX; e += blockDim.x) P.owner[e] = 0xFFFFFFFFu;
-    if (a.logits) {
-        for (int t = wv; t < a.M; t += nw) {
-            int id;
-            float wt;
-            route_wave<4>(a.logits + (size_t)t * a.E, a.E, a.renorm, lane, id, wt);
-            if (lane < SLOTS) {
-                P.id[t * SLOTS + lane] = (uint16_t)id;
-                P.wt[t * SLOTS + lane] = wt;
-                if (publish) {
-                    a.ids[t * SLOTS + lane] = (uint16_t)id;
-                    a.w[t * SLOTS + lane] = wt;
-                }
-            }
-        }
-    } else {
-        for (int q = tid; q < np; q += blockDim.x) {
-            P.id[q] = a.ids[q];
-            P.wt[q] = a.w[q];
-        }
-    }
-    __syncthreads();
-    uint32_t fl = 0;
-    if (wv == 0) {
+// The pair rule, the prefill bucket fill's too: slot s of a token is dropped when its id
+// exceeds n_experts (MOE_DEVFLAG_BAD_ID) or an earlier slot of the token names the same id
+// (MOE_DEVFLAG_DUP_ID).  Lane s < 9 holds slot s's id; returns whether the lane's slot is kept,
+// and the wave's flags in fl.
+__device__ __forceinline__ bool slot_kept(int id, int lane, int E, uint32_t &fl) {
+    bool dup = false;
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int q = lane + 64 * r;
-            bool ok = false;
-            if (q < np) {
-                const int t = q / SLOTS, s = q - t * SLOTS;
-                const int e = P.id[q];
-                if (e > a.E) {
-                    fl |= MOE_DEVFLAG_BAD_ID;
-                } else {
-                    ok = true;
-                    for (int s2 = 0; s2 < s; ++s2) ok = ok && (int)P.id[t * SLOTS + s2] != e;
-                    if (ok) atomicMin(&P.owner[e], (uint32_t)q);
-                    else fl |= MOE_DEVFLAG_DUP_ID;
-                }
-            }
-            const uint64_t b = __ballot(ok);
-            if (lane == 0) P.valid[r] = b;
-        }
-        fl = (__ballot(fl & MOE_DEVFLAG_BAD_ID) ? MOE_DEVFLAG_BAD_ID : 0u) |
-             (__ballot(fl & MOE_DEVFLAG_DUP_ID) ? MOE_DEVFLAG_DUP_ID : 0u);
-    }
-    __syncthreads();
-    return fl;
+    for (int s2 = 0; s2 < SLOTS - 1; ++s2) dup = dup || (s2 < lane && __builtin_amdgcn_readlane(id, s2) == id);
+    fl = (__ballot(lane < SLOTS && id > E) ? MOE_DEVFLAG_BAD_ID : 0u) |
+         (__ballot(lane < SLOTS && id <= E && dup) ? MOE_DEVFLAG_DUP_ID : 0u);
+    return lane < SLOTS && id <= E && !dup;
 }
 
-// Wave 0: the pairs q < np for which pred(q) holds, ascending, into list[]; returns their
-// number (in wave 0).
-template <typename Pred>
-__device__ __forceinline__ int collect_pairs(int np, int lane, int *list, Pred pred) {
-    int n = 0;
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const int q = lane + 64 * r;
-        const bool m = q < np && pred(q);
-        const uint64_t b = __ballot(m);
-        if (m) list[n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u))] = q;
-        n += __popcll(b);
-    }
-    return n;
-}
-
-
-// ---------------------------------------------------------------- roles
-// gate/up: 4 waves per workgroup, RP row-pair steps per wave (4 up to M = 2, then 8: fewer
-// workgroups, each repeating the routing plan, for the same rows)
-constexpr int DEC_ROWS = 8;  // down: output rows per workgroup
-template <int H, int I, int RP = 4>
+// ---------------------------------------------------------------- down shape
+constexpr int DEC_ROWS = 8; // down: output rows per workgroup
+// Down: a W2 row (I weights) on LPR2 lanes, one 32-weight sub-block per lane; RPS2 rows per
+// wave step, STEPS steps for the workgroup's DEC_ROWS rows.
+template <int H, int I>
 struct DecShape {
-    static constexpr int SBR1 = H / QK, LPR1 = SBR1 * 8, RPS1 = 64 / LPR1, RPW1 = RP * RPS1;
-    static constexpr int NCHK = I / (4 * RPW1); // gate/up items per pair
-    static constexpr int NCH = H / 32;
     static constexpr int SBR2 = I / QK, LPR2 = SBR2 * 8, RPS2 = 64 / LPR2;
     static constexpr int STEPS = DEC_ROWS / RPS2 > 0 ? DEC_ROWS / RPS2 : 1;
-    static_assert(LPR1 <= 64 && 64 % LPR1 == 0 && LPR2 <= 64 && 64 % LPR2 == 0, "row must tile a wave");
-    static_assert(I % (4 * RPW1) == 0 && RPS2 * STEPS == DEC_ROWS && H % DEC_ROWS == 0, "item shapes");
-    static_assert(NCH <= 64, "chunk sums of squares: one per lane");
+    static_assert(LPR2 <= 64 && 64 % LPR2 == 0, "row must tile a wave");
+    static_assert(RPS2 * STEPS == DEC_ROWS && H % DEC_ROWS == 0, "item shapes");
 };
 
 // ---------------------------------------------------------------- gate/up
@@ -260,8 +186,8 @@ __device__ __forceinline__ float rms_factor(int rmsnorm, float ss_wave, int H) {
 
 // ---------------------------------------------------------------- gate/up, M = 1
 // No plan and no barrier: every wave routes the token itself (the top-8 code of
-// moe_router_topk, so all agree bit for bit) or reads its 9 ids, checks them by the rule of
-// build_plan, quantizes the lane's chunk of x into registers, and runs its steps.  Slot order
+// moe_router_topk, so all agree bit for bit) or reads its 9 ids, checks them by the pair rule,
+// quantizes the lane's chunk of x into registers, and runs its steps.  Slot order
 // puts the shared expert first: u = 0 is slot 8, u = 1.. the valid routed slots ascending.
 // Workgroup 0 publishes the routing (ids and w, for the caller and the down launch) or raises
 // the flags of invalid ids.
@@ -286,24 +212,15 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_m1(DecodeArgs a) {
     } else {
         id = lane < SLOTS ? (int)a.ids[lane] : 0;
     }
-    bool ok = lane < SLOTS && id <= a.E;
-    bool dup = false;
-#pragma unroll
-    for (int s2 = 0; s2 < SLOTS - 1; ++s2)
-        dup = dup || (s2 < lane && __builtin_amdgcn_readlane(id, s2) == id);
-    ok = ok && !dup;
+    uint32_t fl;
+    const bool ok = slot_kept(id, lane, a.E, fl);
     const uint32_t vm = (uint32_t)__ballot(ok) & 0x1FFu;
     if (blockIdx.x == 0 && wv == 0) {
-        if (a.logits) {
-            if (lane < SLOTS) {
-                a.ids[lane] = (uint16_t)id;
-                a.w[lane] = wt;
-            }
-        } else {
-            const uint32_t fl = (__ballot(lane < SLOTS && id > a.E) ? MOE_DEVFLAG_BAD_ID : 0u) |
-                                (__ballot(lane < SLOTS && id <= a.E && dup) ? MOE_DEVFLAG_DUP_ID : 0u);
-            if (lane == 0 && fl) set_flag(a.flags, fl);
+        if (a.logits && lane < SLOTS) {
+            a.ids[lane] = (uint16_t)id;
+            a.w[lane] = wt;
         }
+        if (lane == 0 && fl) set_flag(a.flags, fl);
     }
     // slot order, shared first: bit r of vr = rank position r, slot (r + 8) % 9
     const uint32_t vr = ((vm >> 8) & 1u) | ((vm & 0xFFu) << 1);
@@ -349,85 +266,119 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_m1(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------- prep, 2 <= M <= 8
-// One workgroup of eight waves, once per call: the routing (wave t routes token t when the call
-// passed logits, and the ids and weights are published), pair validity and the device flags of
-// invalid ids (build_plan), the selected experts in slot order with the tokens each serves,
-// every token's activations as int8 planes and its RMSNorm factor -- the plan block every
-// gate/up workgroup then copies instead of building it.
+// One workgroup of eight waves, once per call; wave t takes token t.  It routes the token
+// when the call passed logits (the top-8 code of moe_router_topk; ids and w are published),
+// or reads its ids; checks its pairs by the pair rule (raising the device flags of invalid
+// ids); and quantizes its activations, one chunk per lane, into int8 planes with its
+// RMSNorm factor.  One LDS round then finds each expert's first valid pair, and wave 0 numbers
+// the selected experts in slot order with the tokens each serves, and lists the valid pairs
+// for the down launch -- the plan block every later workgroup copies instead of building it.
 template <int H>
 struct PrepLds {
-    DecodePlan P;
-    float xss[MOE_DECODE_MAX_M][H / 32];
-    uint8_t uof[DEC_MAXP];
+    uint32_t owner[DEC_EMAX]; // first valid pair naming each expert (all ones: none)
+    uint16_t id[DEC_MAXP];
+    float wt[DEC_MAXP];
     DecPlan<H, MOE_DECODE_MAX_M> G;
 };
 
+// Pairs before q (q < 128) set in the two-word mask m.
+__device__ __forceinline__ int rank2(uint64_t m0, uint64_t m1, int q) {
+    return q < 64 ? __popcll(m0 & ((1ull << q) - 1ull)) : __popcll(m0) + __popcll(m1 & ((1ull << (q - 64)) - 1ull));
+}
+
 template <int H>
-__global__ __launch_bounds__(512) void k_dec_prep(DecodeArgs a) {
+__global__ __launch_bounds__(64 * MOE_DECODE_MAX_M) void k_dec_prep(DecodeArgs a) {
     constexpr int NCH = H / 32;
-    static_assert(MOE_DECODE_MAX_M * NCH <= 512 * 2, "two chunks per thread at most");
+    static_assert(NCH <= 64, "a token's chunks on one wave");
     __shared__ PrepLds<H> L;
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t = __builtin_amdgcn_readfirstlane(tid >> 6); // this wave's token
     const int np = a.M * SLOTS;
-    constexpr int SPT = (MOE_DECODE_MAX_M * NCH + 511) / 512;
-    // activation chunks, requested first
-    f32x4 v[SPT][8];
+    for (int e = tid; e < DEC_EMAX; e += 64 * MOE_DECODE_MAX_M) L.owner[e] = 0xFFFFFFFFu;
+    for (int u = tid; u < DEC_MAXP; u += 64 * MOE_DECODE_MAX_M) L.G.tmask[u] = 0u;
+    int id = 0;
+    bool ok = false;
+    if (t < a.M) {
+        // this lane's chunk of the token's activations, requested first
+        const int c = min(lane, NCH - 1);
+        f32x4 xv[8];
 #pragma unroll
-    for (int j = 0; j < SPT; ++j) {
-        const int i = min(tid + 512 * j, a.M * NCH - 1);
-        const int t = i / NCH, c = i - t * NCH;
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v[j][u] = ldg<f32x4>(a.x + (size_t)t * H + 32 * c + 4 * u);
-    }
-    const uint32_t fl = build_plan(a, L.P, true); // ends with a barrier
-    if (tid == 0 && fl) set_flag(a.flags, fl);
-#pragma unroll
-    for (int j = 0; j < SPT; ++j) {
-        const int i = tid + 512 * j;
-        if (i >= a.M * NCH) continue;
-        const int t = i / NCH, c = i - t * NCH;
+        for (int u = 0; u < 8; ++u) xv[u] = ldg<f32x4>(a.x + (size_t)t * H + 32 * c + 4 * u);
+        float wt = 0.f;
+        if (a.logits) {
+            route_wave<4>(a.logits + (size_t)t * a.E, a.E, a.renorm, lane, id, wt);
+            if (lane < SLOTS) {
+                a.ids[t * SLOTS + lane] = (uint16_t)id;
+                a.w[t * SLOTS + lane] = wt;
+            }
+        } else if (lane < SLOTS) {
+            id = (int)a.ids[t * SLOTS + lane];
+            wt = a.w[t * SLOTS + lane];
+        }
+        uint32_t fl;
+        ok = slot_kept(id, lane, a.E, fl);
+        const uint32_t vm = (uint32_t)__ballot(ok) & 0x1FFu;
+        if (lane < SLOTS) {
+            L.id[t * SLOTS + lane] = (uint16_t)id;
+            L.wt[t * SLOTS + lane] = wt;
+        }
+        // the activations as int8 planes, and the token's RMSNorm factor
         uint32_t xh[8], xl[8];
         float sx, ss;
-        quant_chunk(v[j], xh, xl, sx, ss);
-        u32x4 *dst = reinterpret_cast<u32x4 *>(&L.G.xq[t][c * XQS]);
-        dst[0] = u32x4{xh[0], xh[1], xh[2], xh[3]};
-        dst[1] = u32x4{xh[4], xh[5], xh[6], xh[7]};
-        dst[2] = u32x4{xl[0], xl[1], xl[2], xl[3]};
-        dst[3] = u32x4{xl[4], xl[5], xl[6], xl[7]};
-        L.G.xsc[t][c] = sx;
-        L.xss[t][c] = ss;
+        quant_chunk(xv, xh, xl, sx, ss);
+        if (lane < NCH) {
+            u32x4 *dst = reinterpret_cast<u32x4 *>(&L.G.xq[t][lane * XQS]);
+            dst[0] = u32x4{xh[0], xh[1], xh[2], xh[3]};
+            dst[1] = u32x4{xh[4], xh[5], xh[6], xh[7]};
+            dst[2] = u32x4{xl[0], xl[1], xl[2], xl[3]};
+            dst[3] = u32x4{xl[4], xl[5], xl[6], xl[7]};
+            L.G.xsc[t][lane] = sx;
+        }
+        const float inv = rms_factor(a.rmsnorm, wave_sum(lane < NCH ? ss : 0.f), H);
+        if (lane == 0) {
+            L.G.inv[t] = inv;
+            L.G.vt[t] = vm;
+            if (fl) set_flag(a.flags, fl);
+        }
     }
-    lds_barrier(); // the staged chunks, for the RMSNorm factors below
-    if (wv == 0) {
-        // the selected experts in slot order (each one's first valid pair, ascending) ...
-        int list[2];
-        const int U = collect_pairs(np, lane, reinterpret_cast<int *>(L.G.tmask), [&](int q) {
-            return pair_valid(L.P, q) && L.P.owner[L.P.id[q]] == (uint32_t)q;
-        });
-#pragma unroll
-        for (int r = 0; r < 2; ++r) list[r] = lane + 64 * r < U ? (int)L.G.tmask[lane + 64 * r] : 0;
-#pragma unroll
-        for (int r = 0; r < 2; ++r)
-            if (lane + 64 * r < U) {
-                L.uof[list[r]] = (uint8_t)(lane + 64 * r);
-                L.G.uexp[lane + 64 * r] = L.P.id[list[r]];
-                L.G.tmask[lane + 64 * r] = 0u;
-            }
-        // ... the tokens each serves, with their pairs ...
+    __syncthreads();
+    if (ok) atomicMin(&L.owner[id], (uint32_t)(t * SLOTS + lane));
+    __syncthreads();
+    if (t == 0) {
+        // pairs q = lane, lane + 64: validity, and whether q is its expert's first valid pair
+        int idq[2];
+        bool vq[2], own[2];
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
             const int q = lane + 64 * r;
-            if (q < np && pair_valid(L.P, q)) {
-                const int t = q / SLOTS, u = L.uof[L.P.owner[L.P.id[q]]];
-                atomicOr(&L.G.tmask[u], 1u << t);
-                L.G.tpair[u][t] = (uint8_t)q;
-            }
+            vq[r] = q < np && ((L.G.vt[min(q / SLOTS, MOE_DECODE_MAX_M - 1)] >> (q % SLOTS)) & 1u);
+            idq[r] = vq[r] ? (int)L.id[q] : 0;
         }
-        // ... and every token's RMSNorm factor
-        for (int t = 0; t < a.M; ++t)
-            L.G.inv[t] = rms_factor(a.rmsnorm, wave_sum(lane < NCH ? L.xss[t][lane] : 0.f), H);
-        if (lane == 0) L.G.U = U;
+        uint32_t ow[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            ow[r] = vq[r] ? L.owner[idq[r]] : 0u;
+            own[r] = vq[r] && ow[r] == (uint32_t)(lane + 64 * r);
+        }
+        const uint64_t om0 = __ballot(own[0]), om1 = __ballot(own[1]);
+        const uint64_t vb0 = __ballot(vq[0]), vb1 = __ballot(vq[1]);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            if (!vq[r]) continue;
+            const int q = lane + 64 * r, tq = q / SLOTS;
+            const int u = rank2(om0, om1, (int)ow[r]); // the slot-order number of q's expert
+            atomicOr(&L.G.tmask[u], 1u << tq);
+            L.G.tpair[u][tq] = (uint8_t)q;
+            if (own[r]) L.G.uexp[u] = idq[r];
+            const int k = rank2(vb0, vb1, q); // q's place among the valid pairs
+            L.G.epair[k] = (uint8_t)q;
+            L.G.eexp[k] = (uint16_t)idq[r];
+            L.G.ewt[k] = L.wt[q];
+        }
+        if (lane == 0) {
+            L.G.U = __popcll(om0) + __popcll(om1);
+            L.G.NV = __popcll(vb0) + __popcll(vb1);
+        }
     }
     __syncthreads();
     // the block out: the head, then the M token rows of the planes and of the scales
@@ -435,11 +386,12 @@ __global__ __launch_bounds__(512) void k_dec_prep(DecodeArgs a) {
     uint8_t *dst = reinterpret_cast<uint8_t *>(a.plan);
     constexpr int XQR = NCH * XQS * 4, XSR = NCH * 4;
     constexpr size_t XSO = DEC_PLAN_HEAD + (size_t)MOE_DECODE_MAX_M * XQR;
-    for (int i = 16 * tid; i < (int)DEC_PLAN_HEAD; i += 16 * 512)
+    constexpr int NT = 64 * MOE_DECODE_MAX_M;
+    for (int i = 16 * tid; i < (int)DEC_PLAN_HEAD; i += 16 * NT)
         *reinterpret_cast<u32x4 *>(dst + i) = *reinterpret_cast<const u32x4 *>(src + i);
-    for (int i = 16 * tid; i < a.M * XQR; i += 16 * 512)
+    for (int i = 16 * tid; i < a.M * XQR; i += 16 * NT)
         *reinterpret_cast<u32x4 *>(dst + DEC_PLAN_HEAD + i) = *reinterpret_cast<const u32x4 *>(src + DEC_PLAN_HEAD + i);
-    for (int i = 16 * tid; i < a.M * XSR; i += 16 * 512)
+    for (int i = 16 * tid; i < a.M * XSR; i += 16 * NT)
         *reinterpret_cast<u32x4 *>(dst + XSO + i) = *reinterpret_cast<const u32x4 *>(src + XSO + i);
 }
 
@@ -539,64 +491,40 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_mt(DecodeArgs a) {
 
 // ---------------------------------------------------------------- down, 2 <= M <= 8
 // Eight waves per workgroup of 8 output rows.  Every valid (token, slot) pair is one element:
-// the element's expert's W2 rows against the pair's h, times c * w, into LDS; the valid pairs
-// are dealt to the waves in ascending order, so the shared expert's M pairs -- and any two
-// tokens' shared routed expert -- go to different waves (repeated W2 rows are L2 hits).  A
-// wave requests the W2 rows of all its elements at once, then the h of its elements two
-// ahead.  Each wave checks pair validity itself, by the rule of build_plan, from the ids in
-// its own LDS region: no barrier until the slot-order sums.
+// the element's expert's W2 rows against the pair's h, times c * w, into LDS.  The plan block
+// lists the valid pairs in ascending order, and they are dealt to the waves in turn, so the
+// shared expert's M pairs -- and any two tokens' shared routed expert -- go to different
+// waves (repeated W2 rows are L2 hits).  A wave reads its elements from the plan in one
+// round, requests the h of its first elements and the W2 rows of all of them at once, then
+// the h of later elements two ahead.  No barrier until the slot-order sums.
 template <int H, int I, int MT>
 __global__ __launch_bounds__(512) void k_dec_down_mt(DecodeArgs a) {
     using S = DecShape<H, I>;
+    using PL = DecPlan<H, MOE_DECODE_MAX_M>;
     constexpr int SBR = S::SBR2, LPR = S::LPR2, RPS = S::RPS2, STEPS = S::STEPS;
     constexpr int NWV = 8, NPM = MT * SLOTS, MAXE = (NPM + NWV - 1) / NWV, HD = 2;
-    static_assert(NPM <= 128 && MT * DEC_ROWS <= 64 * NWV, "pairs in two registers, one output per thread");
+    static_assert(MAXE <= 64 && MT * DEC_ROWS <= 64 * NWV, "elements in one register, one output per thread");
     __shared__ float part[NPM][DEC_ROWS];
-    __shared__ uint16_t sid[NWV][NPM];
-    __shared__ float swt[NWV][NPM];
-    __shared__ uint8_t slist[NWV][MAXE];
-    __shared__ uint64_t svalid[2];
+    const PL *P = reinterpret_cast<const PL *>(a.plan);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int np = a.M * SLOTS;
     const int n0 = blockIdx.x * DEC_ROWS;
     float yres = 0.f;
-    if (a.accumulate && tid < a.M * DEC_ROWS) yres = a.y[(size_t)(tid / DEC_ROWS) * H + n0 + tid % DEC_ROWS];
-    // the routing into this wave's LDS region, then pair validity
-    int idr[2];
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const int q = lane + 64 * r;
-        idr[r] = q < np ? (int)a.ids[q] : 0;
-        if (q < np) {
-            sid[wv][q] = (uint16_t)idr[r];
-            swt[wv][q] = a.w[q];
-        }
+    uint32_t vt = 0u;
+    if (tid < a.M * DEC_ROWS) {
+        const int t = tid / DEC_ROWS;
+        if (a.accumulate) yres = a.y[(size_t)t * H + n0 + tid % DEC_ROWS];
+        vt = P->vt[t];
     }
-    uint64_t vb[2];
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const int q = lane + 64 * r;
-        bool ok = q < np && idr[r] <= a.E;
-        if (ok) {
-            const int t = q / SLOTS, s = q - t * SLOTS;
-            for (int s2 = 0; s2 < s; ++s2) ok = ok && (int)sid[wv][t * SLOTS + s2] != idr[r];
-        }
-        vb[r] = __ballot(ok);
-    }
-    // this wave's elements: the valid pairs of rank wv, wv + 8, ...
-    const int nv0 = __popcll(vb[0]), nv = nv0 + __popcll(vb[1]);
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        if ((vb[r] >> lane) & 1ull) {
-            const int rk = (r ? nv0 : 0) + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(vb[r] >> 32),
-                                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)vb[r], 0u));
-            if (rk % NWV == wv) slist[wv][rk / NWV] = (uint8_t)(lane + 64 * r);
-        }
-    }
-    if (wv == 0 && lane == 0) {
-        svalid[0] = vb[0];
-        svalid[1] = vb[1];
+    // this wave's elements (lane k: element wv + 8k) and their count
+    const int nv = P->NV;
+    int eq = 0, ee = 0;
+    float ew = 0.f;
+    if (lane < MAXE) {
+        const int el = min(wv + NWV * lane, DEC_MAXP - 1);
+        eq = P->epair[el];
+        ee = P->eexp[el];
+        ew = P->ewt[el];
     }
     const int ne = nv > wv ? (nv - wv + NWV - 1) / NWV : 0;
     const int gsb = lane % LPR, rr = lane / LPR, sb = gsb >> 3, ib = gsb & 7;
@@ -606,7 +534,7 @@ __global__ __launch_bounds__(512) void k_dec_down_mt(DecodeArgs a) {
         // what came before them, and its products overlap the later elements' W2 stream
         int qe[MAXE];
 #pragma unroll
-        for (int k = 0; k < MAXE; ++k) qe[k] = slist[wv][min(k, ne - 1)];
+        for (int k = 0; k < MAXE; ++k) qe[k] = __builtin_amdgcn_readlane(eq, min(k, ne - 1));
         float hv[HD][32];
 #pragma unroll
         for (int j = 0; j < HD; ++j) load32(a.hbuf + (size_t)qe[min(j, MAXE - 1)] * I + 32 * gsb, hv[j]);
@@ -614,7 +542,7 @@ __global__ __launch_bounds__(512) void k_dec_down_mt(DecodeArgs a) {
         u32x2 hd[MAXE][STEPS];
 #pragma unroll
         for (int k = 0; k < MAXE; ++k) {
-            const int e = sid[wv][qe[k]];
+            const int e = __builtin_amdgcn_readlane(ee, min(k, ne - 1));
             const uint8_t *W2 = expert_w(a.L.w2, a.L.s2, a.L.sw2, e, a.E);
 #pragma unroll
             for (int st = 0; st < STEPS; ++st) {
@@ -630,7 +558,7 @@ __global__ __launch_bounds__(512) void k_dec_down_mt(DecodeArgs a) {
                 float hs = 0.f;
 #pragma unroll
                 for (int i = 0; i < 32; ++i) hs += hv[k % HD][i];
-                const float wq = a.c * swt[wv][q];
+                const float wq = a.c * __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ew), k));
 #pragma unroll
                 for (int st = 0; st < STEPS; ++st) {
                     uint32_t kv[8];
@@ -649,17 +577,15 @@ __global__ __launch_bounds__(512) void k_dec_down_mt(DecodeArgs a) {
         const int t = tid / DEC_ROWS, r = tid - t * DEC_ROWS;
         float sum = 0.f;
 #pragma unroll
-        for (int s = 0; s < SLOTS; ++s) {
-            const int q = t * SLOTS + s;
-            if ((svalid[q >> 6] >> (q & 63)) & 1ull) sum += part[q][r];
-        }
+        for (int s = 0; s < SLOTS; ++s)
+            if ((vt >> s) & 1u) sum += part[t * SLOTS + s][r];
         a.y[(size_t)t * H + n0 + r] = yres + sum;
     }
 }
 
 // ---------------------------------------------------------------- down, M = 1
 // Wave s takes slot s: it reads the 9 ids itself (no plan, no barrier before the weight
-// loads), drops its slot by the rule of build_plan (an id above n_experts, or one an earlier
+// loads), drops its slot by the pair rule (an id above n_experts, or one an earlier
 // slot names), and writes c * w_s * (W2_e h_s) for the workgroup's 8 output rows to LDS; the
 // 9 contributions are then summed in slot order with the residual.
 template <int H, int I>
@@ -728,7 +654,7 @@ static hipError_t launch_decode_t(const DecodeArgs &a, hipStream_t st, KernelTim
     DecodeArgs b = a;
     if (a.M >= 2) {
         TimedLaunch tl(T, MOE_K_DECODE_PREP, st);
-        hipLaunchKernelGGL((k_dec_prep<H>), dim3(1), dim3(512), 0, st, a);
+        hipLaunchKernelGGL((k_dec_prep<H>), dim3(1), dim3(64 * MOE_DECODE_MAX_M), 0, st, a);
         b.logits = nullptr;
     }
     {
