@@ -185,9 +185,10 @@ __device__ __forceinline__ float rms_factor(int rmsnorm, float ss_wave, int H) {
 }
 
 // ---------------------------------------------------------------- gate/up, M = 1
-// No plan and no barrier: every wave routes the token itself (the top-8 code of
-// moe_router_topk, so all agree bit for bit) or reads its 9 ids, checks them by the pair rule,
-// quantizes the lane's chunk of x into registers, and runs its steps.  Slot order
+// No plan: the four waves of each workgroup route the token together (route_wg4, which agrees
+// with moe_router_topk bit for bit; two LDS-only barriers) or every wave reads the 9 ids; each
+// wave checks them by the pair rule, quantizes the lane's chunk of x into registers, and runs
+// its steps.  Slot order
 // puts the shared expert first: u = 0 is slot 8, u = 1.. the valid routed slots ascending.
 // Workgroup 0 publishes the routing (ids and w, for the caller and the down launch) or raises
 // the flags of invalid ids.
@@ -208,7 +209,8 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_m1(DecodeArgs a) {
     int id;
     float wt = 1.0f;
     if (a.logits) {
-        route_wave<4>(a.logits, a.E, a.renorm, lane, id, wt);
+        __shared__ RouteLds R;
+        route_wg4(a.logits, a.E, a.renorm, lane, wv, R, id, wt);
     } else {
         id = lane < SLOTS ? (int)a.ids[lane] : 0;
     }

@@ -27,13 +27,34 @@ __global__ __launch_bounds__(64) void k_router_topk(const float *__restrict__ lo
     }
 }
 
+// The same with four waves per token (route_wg4, the same results): about 2.5 times less
+// latency per token, for small M where latency, not throughput, is what a launch costs.
+__global__ __launch_bounds__(256) void k_router_topk_wg4(const float *__restrict__ logits, int M, int E, int renorm,
+                                                         uint16_t *__restrict__ ids, float *__restrict__ w) {
+    __shared__ RouteLds R;
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int t = blockIdx.x;
+    int id;
+    float wt;
+    route_wg4(logits + (size_t)t * E, E, renorm, lane, wv, R, id, wt);
+    if (wv == 0 && lane < SLOTS) {
+        ids[(size_t)t * SLOTS + lane] = (uint16_t)id;
+        w[(size_t)t * SLOTS + lane] = wt;
+    }
+}
+
+constexpr int ROUTER_WG4_MAX_M = 256;
+
 hipError_t launch_router_topk(const float *logits, int M, int E, int renorm, uint16_t *ids, float *w,
                               hipStream_t st, KernelTimer *T) {
     if (M <= 0) return hipSuccess;
     if (E < TOPK || E > 256) return hipErrorInvalidValue;
     {
         TimedLaunch tl(T, MOE_K_ROUTER_TOPK, st);
-        hipLaunchKernelGGL(k_router_topk, dim3((unsigned)M), dim3(64), 0, st, logits, M, E, renorm, ids, w);
+        if (M <= ROUTER_WG4_MAX_M)
+            hipLaunchKernelGGL(k_router_topk_wg4, dim3((unsigned)M), dim3(256), 0, st, logits, M, E, renorm, ids, w);
+        else
+            hipLaunchKernelGGL(k_router_topk, dim3((unsigned)M), dim3(64), 0, st, logits, M, E, renorm, ids, w);
     }
     return hipGetLastError();
 }

@@ -807,12 +807,14 @@ __global__ void k_stack_prep(StackArgs a, uint64_t words) {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words / 4;
          i += (uint64_t)gridDim.x * blockDim.x)
         p4[i] = u32x4{0u, 0u, 0u, 0u};
-    if ((int)blockIdx.x < a.n_layers && threadIdx.x < 64) {
-        const int li = blockIdx.x, lane = threadIdx.x;
+    if ((int)blockIdx.x < a.n_layers) {
+        // the four waves route layer li together (the whole workgroup: route_wg4 has barriers)
+        __shared__ RouteLds R;
+        const int li = blockIdx.x, lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
         int id;
         float wt;
-        route_wave<4>(a.logits + (size_t)li * a.E, a.E, a.renorm, lane, id, wt);
-        if (lane < SLOTS) {
+        route_wg4(a.logits + (size_t)li * a.E, a.E, a.renorm, lane, wv, R, id, wt);
+        if (wv == 0 && lane < SLOTS) {
             a.rid[(size_t)li * SLOTS + lane] = (uint16_t)id;
             a.rwt[(size_t)li * SLOTS + lane] = wt;
             if (a.ids_out) {

@@ -337,6 +337,12 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g));
 // The same with v_rcp_f32 (1 ulp) in place of the IEEE division sequence.
 __device__ __forceinline__ float silu_rcp(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
+// Workgroup barrier for LDS traffic only.  __syncthreads() also waits for every global
+// load the wave has in flight (the barrier's release fence needs vmcnt(0)), which would
+// stall on weight loads issued ahead of use.  Use it where the workgroup exchanges data
+// through LDS only.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // ---------------------------------------------------------------- router (one wave)
 __device__ __forceinline__ float router_key(float v) {
     if (v != v) v = -INFINITY; // NaN never wins and weighs 0 unless every logit is -inf/NaN
@@ -366,9 +372,10 @@ __device__ __forceinline__ void load_logits(const float *__restrict__ l, int E, 
 // renorm); lane 8 and above with the shared expert (id E, weight 1).
 // A round: each lane's best remaining key, its wave max in lane 63, a ballot of the lanes
 // holding it.  One lane: it wins with its lowest such index.  An exact tie across lanes:
-// the smallest index among the holders, by a min reduction.  The sums keep one order
-// (Z: lane terms j = 0..NV-1, then wave_sum; the top-8 sum: rank 0..7), so weights do not
-// depend on which lane computed them.
+// the smallest index among the holders, by a min reduction.  The sums keep one order --
+// Z = (...(z_0 + z_1) + ...) + z_{NV-1}, z_j the wave_sum of the terms of logits 64j..64j+63;
+// the top-8 sum over ranks 0..7 -- which route_wg4 keeps too, so every routing site agrees bit
+// for bit.
 template <int NV>
 __device__ __forceinline__ void route_values(const float (&raw)[NV], int E, int renorm, int lane, int &id,
                                              float &wt) {
@@ -417,10 +424,9 @@ __device__ __forceinline__ void route_values(const float (&raw)[NV], int E, int 
             my_e = e;
         }
     }
-    float zs = 0.f;
+    float Z = wave_sum(ex[0]);
 #pragma unroll
-    for (int j = 0; j < NV; ++j) zs += ex[j];
-    const float Z = wave_sum(zs);
+    for (int j = 1; j < NV; ++j) Z += wave_sum(ex[j]);
     id = my_id;
     wt = (lane < TOPK) ? my_e / (renorm ? s8 : Z) : 1.0f;
 }
@@ -431,6 +437,67 @@ __device__ __forceinline__ void route_wave(const float *__restrict__ l, int E, i
     float raw[NV];
     load_logits<NV>(l, E, lane, raw);
     route_values<NV>(raw, E, renorm, lane, id, wt);
+}
+
+// The same routing by the four waves of a workgroup, wave w taking logits 64w..64w+63, one per
+// lane; every wave ends as route_values ends (lane r < 8: rank r and its weight; lane 8 and
+// above: the shared expert), with bit-identical ids and weights.  Each wave ranks its own
+// logits (a round: one wave max, a ballot, the winner's lane cleared -- the lowest lane holding the max is
+// the lowest index), then every wave merges the 32 candidates from LDS, wave-major, so lane
+// order is index order among equal keys.  Two LDS-only barriers; all 256 threads must call it.
+struct RouteLds {
+    uint32_t key[4][TOPK], idx[4][TOPK];
+    float z[4];
+};
+__device__ __forceinline__ void route_wg4(const float *__restrict__ l, int E, int renorm, int lane, int wv,
+                                          RouteLds &R, int &id, float &wt) {
+    const int i = 64 * wv + lane;
+    const float kf = (i < E) ? router_key(ldg<float>(l + min(i, E - 1))) : -INFINITY;
+    uint32_t o = (i < E) ? ord32(kf) : 0u; // 0 sorts below every real key
+    uint32_t mk = 0u, mi = 0u;
+#pragma unroll
+    for (int r = 0; r < TOPK; ++r) {
+        const uint32_t K = wave_max_last_u32(o);
+        const int w = (int)__builtin_ctzll(__ballot(o == K));
+        o = lane == w ? 0u : o;
+        if (lane == r) {
+            mk = K;
+            mi = (uint32_t)(64 * wv + w);
+        }
+    }
+    if (lane < TOPK) {
+        R.key[wv][lane] = mk;
+        R.idx[wv][lane] = mi;
+    }
+    lds_barrier();
+    uint32_t c = lane < 4 * TOPK ? R.key[lane / TOPK][lane % TOPK] : 0u;
+    const uint32_t ci = lane < 4 * TOPK ? R.idx[lane / TOPK][lane % TOPK] : 0u;
+    // the global max, then this wave's part of the softmax sum
+    const float m = unord32(wave_max_last_u32(c));
+    const float zw = wave_sum((i < E) ? ((kf == m) ? 1.0f : expf(kf - m)) : 0.0f);
+    if (lane == 0) R.z[wv] = zw;
+    int my_id = E;
+    uint32_t my_k = 0u;
+#pragma unroll
+    for (int r = 0; r < TOPK; ++r) {
+        const uint32_t K = wave_max_last_u32(c);
+        const int w = (int)__builtin_ctzll(__ballot(c == K));
+        const int idx = __builtin_amdgcn_readlane((int)ci, w);
+        c = lane == w ? 0u : c;
+        if (lane == r) {
+            my_id = idx;
+            my_k = K;
+        }
+    }
+    lds_barrier();
+    const float Z = ((R.z[0] + R.z[1]) + R.z[2]) + R.z[3];
+    const float kr = unord32(my_k);
+    const float e = (lane < TOPK) ? ((kr == m) ? 1.0f : expf(kr - m)) : 1.0f;
+    float s8 = 0.f;
+#pragma unroll
+    for (int r = 0; r < TOPK; ++r) s8 += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), r));
+    id = my_id;
+    wt = (lane < TOPK) ? e / (renorm ? s8 : Z) : 1.0f;
 }
 
 // ---------------------------------------------------------------- expert table
@@ -481,12 +548,6 @@ __device__ __forceinline__ u32x4 remote_quad(const u32x4 *p) {
     return u32x4{(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
 }
 __device__ __forceinline__ uint32_t quad_tagged(u32x4 v) { return v[0] & v[1] & v[2] & v[3] & 1u; }
-
-// Workgroup barrier for LDS traffic only.  __syncthreads() also waits for every global
-// load the wave has in flight (the barrier's release fence needs vmcnt(0)), which would
-// stall on weight loads issued ahead of use.  Use it where the workgroup exchanges data
-// through LDS only.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ void set_flag(uint32_t *flags, uint32_t f) {
     if (flags) __hip_atomic_fetch_or((MOE_GLOBAL uint32_t *)flags, f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
