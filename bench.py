@@ -186,8 +186,8 @@ def leg_decode(torch, pkg, ctx, K, W, eager):
 
 def leg_config0(torch, pkg, ctx, routers, eager):
     """Config 0: one layer, M = 1 -- moe_ffn_route (routing inside the decode launch); and the
-    activation-routed variant moe_router_gemv_topk + moe_ffn.  Layers cycle over the 40
-    resident ones, so the selected experts come from HBM."""
+    activation-routed variant: moe_router_gemv_topk for the logits only, then moe_ffn_route.
+    Layers cycle over the 40 resident ones, so the selected experts come from HBM."""
     dev = torch.device("cuda:0")
     n, warm = 8 + 160, 8
     x0 = pkg.gen_normal(H, pkg.seed_for(0, 0, pkg.TAG_X)).view(1, H)
@@ -195,14 +195,14 @@ def leg_config0(torch, pkg, ctx, routers, eager):
     l0 = pkg.gen_logits(n, E, pkg.seed_for(0, 0, pkg.TAG_L)).view(n, 1, E)
     i0 = torch.empty((n, 1, 9), dtype=torch.uint16, device=dev)
     w0 = torch.empty((n, 1, 9), dtype=torch.float32, device=dev)
+    g0 = torch.empty((n, 1, E), dtype=torch.float32, device=dev)
 
     def step(s):
         ctx.ffn_route(s % LAYERS, x0, l0[s], y=y0, ids=i0[s], w=w0[s], rmsnorm=True)
 
     def step_gemv(s):
-        _, ids, w = ctx.router_gemv_topk(routers[s % LAYERS], x0, rmsnorm=True, ids=i0[s], w=w0[s],
-                                         want_logits=False)
-        ctx.ffn(s % LAYERS, x0, ids, w, y=y0, rmsnorm=True)
+        lg, _, _ = ctx.router_gemv_topk(routers[s % LAYERS], x0, rmsnorm=True, logits=g0[s], want_ids=False)
+        ctx.ffn_route(s % LAYERS, x0, lg, y=y0, ids=i0[s], w=w0[s], rmsnorm=True)
 
     step(0)
     step_gemv(0)
@@ -234,8 +234,9 @@ def leg_config0(torch, pkg, ctx, routers, eager):
                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
                          "bytes_per_launch": DECODE_GATE_UP_BYTES, "avg_us": gu},
             "kernels": kern,
-            "activation_routed": {"what": "moe_router_gemv_topk (x . Wg over an IQ4_XS [256][2048] gate "
-                                          "matrix per layer, then top-8) + moe_ffn",
+            "activation_routed": {"what": "moe_router_gemv_topk for the logits only (x . Wg over an IQ4_XS "
+                                          "[256][2048] gate matrix per layer) + moe_ffn_route (the top-8 "
+                                          "inside the decode launch)",
                                   "us_per_step": round(us_g, 3), "gbs": round(gbs_g, 1),
                                   "bytes_per_step": DECODE_BYTES_PER_LAYER + ROUTER_BYTES, "kernels": kern_g}}
 

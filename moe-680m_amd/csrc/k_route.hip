@@ -63,15 +63,14 @@ hipError_t launch_router_topk(const float *logits, int M, int E, int renorm, uin
 // logits[t][e] = sum_k xin[t][k] * Wg[e][k], xin = x or RMSNorm(x); Wg IQ4_XS [E][H] in the
 // caller's (GGML) layout, rows = experts.  Replaces shaders/router.comp:21-61 (dispatched at
 // src/inference.rs:598-605), whose 64x8 f32 tiles re-dequantized every weight per tile.
-// One wave per (expert row, group of RG_TM tokens), four waves per workgroup: lane l owns
+// One wave per (expert row, group of TM tokens: 1, 2 or 4 by M), four waves per workgroup: lane l owns
 // sub-block l of the row (32 weights; H = 2048 is one sub-block per lane), decodes it once
 // into biased codebook bytes and one f32 scale, then for each token takes one f32 dot of 32
 // against x (loaded for all the group's tokens before any is used) and a wave sum.  All f32:
 // the weights are exact, so the logits differ from an f64 sum by f32 rounding only.
-constexpr int RG_TM = 4;    // tokens per wave
 constexpr int RG_WAVES = 4; // experts per workgroup
 
-template <int H>
+template <int H, int RG_TM>
 __global__ __launch_bounds__(64 * RG_WAVES) void k_router_gemv(const uint8_t *__restrict__ wg,
                                                                const float *__restrict__ x, int M, int E,
                                                                int rmsnorm, float *__restrict__ logits) {
@@ -116,19 +115,30 @@ __global__ __launch_bounds__(64 * RG_WAVES) void k_router_gemv(const uint8_t *__
     }
 }
 
+template <int H, int TM>
+static void launch_router_gemv_t(const void *wg, const float *x, int M, int E, int rmsnorm, float *logits,
+                                 hipStream_t st) {
+    const dim3 grid((unsigned)((E + RG_WAVES - 1) / RG_WAVES), (unsigned)((M + TM - 1) / TM));
+    hipLaunchKernelGGL((k_router_gemv<H, TM>), grid, dim3(64 * RG_WAVES), 0, st, (const uint8_t *)wg, x, M, E, rmsnorm,
+                       logits);
+}
+
+template <int H>
+static void launch_router_gemv_h(const void *wg, const float *x, int M, int E, int rmsnorm, float *logits,
+                                 hipStream_t st) {
+    // a wave's tokens past M repeat the last one: at small M fewer tokens per wave
+    if (M == 1) launch_router_gemv_t<H, 1>(wg, x, M, E, rmsnorm, logits, st);
+    else if (M == 2) launch_router_gemv_t<H, 2>(wg, x, M, E, rmsnorm, logits, st);
+    else launch_router_gemv_t<H, 4>(wg, x, M, E, rmsnorm, logits, st);
+}
+
 hipError_t launch_router_gemv(int H, const void *wg, const float *x, int M, int E, int rmsnorm, float *logits,
                               hipStream_t st, KernelTimer *T) {
     if (M <= 0) return hipSuccess;
-    const dim3 grid((unsigned)((E + RG_WAVES - 1) / RG_WAVES), (unsigned)((M + RG_TM - 1) / RG_TM));
+    if (H != 2048 && H != 512) return hipErrorInvalidValue;
     TimedLaunch tl(T, MOE_K_ROUTER_GEMV, st);
-    if (H == 2048)
-        hipLaunchKernelGGL(k_router_gemv<2048>, grid, dim3(64 * RG_WAVES), 0, st, (const uint8_t *)wg, x, M, E, rmsnorm,
-                           logits);
-    else if (H == 512)
-        hipLaunchKernelGGL(k_router_gemv<512>, grid, dim3(64 * RG_WAVES), 0, st, (const uint8_t *)wg, x, M, E, rmsnorm,
-                           logits);
-    else
-        return hipErrorInvalidValue;
+    if (H == 2048) launch_router_gemv_h<2048>(wg, x, M, E, rmsnorm, logits, st);
+    else launch_router_gemv_h<512>(wg, x, M, E, rmsnorm, logits, st);
     return hipGetLastError();
 }
 
