@@ -216,6 +216,45 @@ def test_duplicate_and_bad_ids_same_at_decode_and_prefill(gpu, orc, full):
     assert normwise_err(ref, ref0) <= 1e-12
 
 
+@pytest.mark.parametrize("route", [False, True])
+def test_duplicate_and_bad_ids_decode_batch(gpu, orc, full, route):
+    """The pair rule on the 2 <= M <= 8 decode path (its prep launch): token 0 names one expert
+    twice and has an id above n_experts, token 2 repeats its shared slot's id in slot 3; the
+    later / bad slots are dropped, the flags raised, and the other tokens untouched -- the
+    oracle applies the same rule.  With route=True the valid routing comes from moe_ffn_route
+    and must equal moe_router_topk's bit for bit."""
+    import torch
+    ctx, layer = full
+    M = 4
+    x = gpu.gen_normal(M * H, 3401).view(M, H)
+    logits = gpu.gen_logits(M, E, 3402)
+    ids, w = ctx.router_topk(logits)
+    if route:
+        y, ids2, w2 = ctx.ffn_route(0, x, logits)
+        torch.cuda.synchronize()
+        assert torch.equal(ids, ids2) and torch.equal(w.view(torch.int32), w2.view(torch.int32))
+        assert ctx.device_flags() == 0
+        ref = orc.moe_ffn(layer.host(), x.cpu().numpy(), ids.cpu().numpy(), w.cpu().numpy(), 1.0 / 9)
+        assert normwise_err(y.cpu().numpy(), ref) <= TOL_DECODE
+        return
+    ids_bad = ids.clone()
+    ids_bad[0, 5] = ids_bad[0, 2]       # duplicate inside token 0
+    ids_bad[0, 7] = E + 3               # out of range
+    ids_bad[2, 3] = E                   # token 2 names the shared expert in a routed slot ...
+    torch.cuda.synchronize()
+    y = ctx.ffn(0, x, ids_bad, w).clone()
+    assert ctx.device_flags() == (gpu.DEVFLAG_BAD_ID | gpu.DEVFLAG_DUP_ID)
+    ref = orc.moe_ffn(layer.host(), x.cpu().numpy(), ids_bad.cpu().numpy(), w.cpu().numpy(), 1.0 / 9)
+    assert normwise_err(y.cpu().numpy(), ref) <= TOL_DECODE
+    # ... so its slot 8 (the shared id again) is the repeat that is dropped
+    w_zero = w.cpu().numpy().copy()
+    w_zero[0, 5] = w_zero[0, 7] = w_zero[2, 8] = 0.0
+    ids_fix = ids.cpu().numpy().copy()
+    ids_fix[2, 3] = E
+    ref0 = orc.moe_ffn(layer.host(), x.cpu().numpy(), ids_fix, w_zero, 1.0 / 9)
+    assert normwise_err(ref, ref0) <= 1e-12
+
+
 def test_prefill_zero_block_small_activations(gpu, orc):
     """A 64-row block of W3 with d = 0 (h = 0 over a whole column block) and activations
     small enough that a row's max|h| is below 0.5: the prefill down kernel's rescale of that
