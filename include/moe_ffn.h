@@ -157,7 +157,8 @@ moe_status moe_ffn_route(moe_ctx *ctx, int layer, const float *x, const float *l
 moe_status moe_ffn_noalloc(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids, const float *w,
                            int M, float *y, int flags, void *stream);
 
-/* One token (M = 1) through n_layers consecutive MoE layers in one persistent launch:
+/* One token (M = 1) through n_layers consecutive MoE layers in one persistent launch (the
+ * routing of every layer runs inside it; nothing else is launched):
  *   for l in layer0 .. layer0+n_layers-1:
  *       (ids_l, w_l) = top8(softmax(logits[l - layer0]))      (as moe_router_topk)
  *       x = x + c * sum_{s<9} w_l[s] * FFN_{ids_l[s]}(xin),  xin = RMSNorm(x) if asked
@@ -169,7 +170,9 @@ moe_status moe_ffn_noalloc(moe_ctx *ctx, int layer, const float *x, const uint16
  * Every wait inside the launch is bounded: one that expires sets MOE_DEVFLAG_TIMEOUT, every
  * workgroup then stops publishing and leaves, and y is left unwritten -- it is written only
  * after every row of the last layer is complete -- so an x that y aliases keeps its value.
- * Check the flag with moe_device_flags or, without a host sync, moe_device_flags_async.
+ * Check the flag with moe_device_flags or, without a host sync, moe_device_flags_async; both
+ * also reset the stack's internal state when they find it, and until then later launches may
+ * fail the same way (never with a silently wrong y).
  * Replaces, for the MoE path of one decode token, the per-layer sequence
  * record_and_submit_layer's RouterTopk dispatch -> do_route -> record_and_submit_moe of
  * InferenceEngine::forward_single (src/inference.rs:296-301, 608-616, 622-766). */
@@ -215,11 +218,10 @@ enum {
     MOE_K_PREFILL_GATE_UP = 4,
     MOE_K_PREFILL_DOWN = 5,
     MOE_K_PREFILL_COMBINE = 6,
-    MOE_K_DECODE_STACK = 7,    /* moe_decode_stack: the persistent launch */
-    MOE_K_STACK_PREP = 8,      /* moe_decode_stack: the routing + clearing launch before it */
-    MOE_K_ROUTER_GEMV = 9,     /* moe_router_gemv_topk: the GEMV launch (its top-8 is ROUTER_TOPK) */
-    MOE_K_DECODE_PREP = 10,    /* moe_ffn / moe_ffn_route, 2 <= M <= 8: routing, plan, int8 activations */
-    MOE_K_COUNT = 11
+    MOE_K_DECODE_STACK = 7,    /* moe_decode_stack: its one persistent launch (routing included) */
+    MOE_K_ROUTER_GEMV = 8,     /* moe_router_gemv_topk: the GEMV launch (its top-8 is ROUTER_TOPK) */
+    MOE_K_DECODE_PREP = 9,     /* moe_ffn / moe_ffn_route, 2 <= M <= 8: routing, plan, int8 activations */
+    MOE_K_COUNT = 10
 };
 moe_status moe_timing_enable(moe_ctx *ctx, int capacity);
 moe_status moe_timing_read(moe_ctx *ctx, int counts[MOE_K_COUNT], double total_ms[MOE_K_COUNT]);

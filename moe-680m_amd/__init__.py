@@ -47,7 +47,7 @@ EXPORTS = (
 )
 
 KERNELS = ("router_topk", "bucket_fill", "decode_gate_up", "decode_down", "prefill_gate_up",
-           "prefill_down", "prefill_combine", "decode_stack", "stack_prep", "router_gemv", "decode_prep")
+           "prefill_down", "prefill_combine", "decode_stack", "router_gemv", "decode_prep")
 
 
 class MoeError(RuntimeError):

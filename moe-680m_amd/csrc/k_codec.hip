@@ -233,12 +233,27 @@ hipError_t launch_repack_split(const void *src, uint64_t src_stride, const void 
     return hipGetLastError();
 }
 
-__global__ void k_flags_take(uint32_t *flags, uint32_t *dst) {
-    *dst = __hip_atomic_exchange((MOE_GLOBAL uint32_t *)flags, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// One workgroup: thread 0 swaps the flags out; after an expired decode-stack wait, all
+// threads zero the stack's control words and exchange sets (an error path: its speed does not
+// matter, and the usual call only reads and clears one word).
+__global__ __launch_bounds__(1024) void k_flags_take(uint32_t *flags, uint32_t *dst, u32x4 *stack,
+                                                     uint64_t stack_quads) {
+    __shared__ uint32_t s_v;
+    if (threadIdx.x == 0) {
+        const uint32_t v =
+            __hip_atomic_exchange((MOE_GLOBAL uint32_t *)flags, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *dst = v;
+        s_v = v;
+    }
+    __syncthreads();
+    if (s_v & MOE_DEVFLAG_TIMEOUT)
+        for (uint64_t q = threadIdx.x; q < stack_quads; q += blockDim.x)
+            *(MOE_GLOBAL u32x4 *)(stack + q) = u32x4{0u, 0u, 0u, 0u};
 }
 
-hipError_t launch_flags_take(uint32_t *flags, uint32_t *dst, hipStream_t st) {
-    hipLaunchKernelGGL(k_flags_take, dim3(1), dim3(1), 0, st, flags, dst);
+hipError_t launch_flags_take(uint32_t *flags, uint32_t *dst, uint32_t *stack, size_t stack_words, hipStream_t st) {
+    hipLaunchKernelGGL(k_flags_take, dim3(1), dim3(1024), 0, st, flags, dst, reinterpret_cast<u32x4 *>(stack),
+                       (uint64_t)(stack_words / 4));
     return hipGetLastError();
 }
 

@@ -11,9 +11,10 @@
 // and its two data dependencies (x -> h -> next x) are global.  On MI355X a kernel boundary
 // costs ~1.6 us and an atomic grid barrier over 256 workgroups ~8 us, so both the HBM
 // latency and the synchronisation must come off the critical path:
-//   - the routing of every layer is computed before the launch (k_stack_prep: the logits
-//     are inputs); during layer l a router wave turns layer l+2's expert id into weight
-//     pointers, and every compute wave keeps its weights in flight in registers: layer
+//   - the routing is computed inside the launch ahead of use (the logits are inputs):
+//     layers 0 and 1 by the compute waves at the start (four waves per layer), layer l+3 by
+//     the router wave while the pollers end layer l, into a ring of three slots of expert
+//     pointers; every compute wave keeps its weights in flight in registers: layer
 //     l+1's phase-A weights are requested when phase A of l is done, layer l's phase-B
 //     weights when phase A of l starts (so no weight stream competes with the
 //     latency-bound cross-XCD exchange at the end of a layer).  The weights are read from
@@ -21,10 +22,14 @@
 //     header load per wave and layer, and their codebook lookups are done in the waits --
 //     layer l+1's phase-A weights after B3 of l, layer l's phase-B weights after its
 //     phase A -- so the phases themselves run only the dot products;
-//   - activations move between workgroups through per-layer buffers cleared to zero
-//     before the launch; producers store each f32 with its mantissa LSB forced to 1
-//     (<= 1 ulp), consumers poll exactly the words they need until every word carries the
-//     tag.  No atomics, no fences, no grid barrier.
+//   - activations move between workgroups through per-layer buffers that start zeroed;
+//     producers store each f32 with its mantissa LSB forced to 1 (<= 1 ulp), consumers poll
+//     exactly the words they need until every word carries the tag.  No atomics, no
+//     fences, no grid barrier.  There are two sets of these buffers: a launch uses set
+//     (epoch & 1), clears what the previous launch wrote into the other set (its router
+//     waves, spread over the layers), and its last XCD-0 reducer to leave advances the
+//     epoch -- so no clearing launch precedes the stack, and consecutive launches (graph
+//     replays included) alternate sets.
 //
 // Work split, mapped onto the eight XCDs (each with its own L2).  Workgroup (k, j) runs on
 // XCD k (read from the hardware register, so the roles follow where the dispatcher put the
@@ -103,11 +108,17 @@ struct LocalQuads {
 typedef volatile __attribute__((address_space(3))) int lds_flag;
 
 // Expiry of a bounded wait: the sticky TIMEOUT flag, the launch's abort word (every other
-// waiter stops at its next check) and this workgroup's own abort flag.
-__device__ __forceinline__ void stack_abort(uint32_t *flags, lds_flag *s_abort) {
+// waiter stops at its next check) and this workgroup's own abort flag.  The abort word holds
+// the tag of the launch that raised it (atag, from the launch epoch), so a later launch never
+// mistakes an earlier launch's abort for its own and nothing has to clear it.
+__device__ __forceinline__ void stack_abort(uint32_t *flags, uint32_t atag, lds_flag *s_abort) {
     set_flag(flags, MOE_DEVFLAG_TIMEOUT);
-    set_flag(flags + 1, 1u);
+    __hip_atomic_store((MOE_GLOBAL uint32_t *)(flags + 1), atag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *s_abort = 1;
+}
+__device__ __forceinline__ bool launch_aborted(const uint32_t *flags, uint32_t atag) {
+    return __hip_atomic_load((const MOE_GLOBAL uint32_t *)(flags + 1), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT) == atag;
 }
 
 // Bounded wait until every quad in v[] is tagged, reloading only the untagged ones.  All
@@ -118,8 +129,8 @@ __device__ __forceinline__ void stack_abort(uint32_t *flags, lds_flag *s_abort) 
 // -- with the abort flag set and the caller's data invalid -- when it gave up.
 template <int MAXQ, typename LD, typename TAG = LsbTag>
 __device__ __forceinline__ bool poll_until_tagged(u32x4 (&v)[MAXQ], const int (&q)[MAXQ], const LD &ld,
-                                                  uint32_t *flags, uint32_t spin_max, lds_flag *s_abort,
-                                                  TAG tag = TAG{}) {
+                                                  uint32_t *flags, uint32_t atag, uint32_t spin_max,
+                                                  lds_flag *s_abort, TAG tag = TAG{}) {
     uint32_t spins = 0;
     while (true) {
         uint32_t t = 1u;
@@ -129,13 +140,12 @@ __device__ __forceinline__ bool poll_until_tagged(u32x4 (&v)[MAXQ], const int (&
         ++spins;
         if ((spins & 31u) == 0 || spins > spin_max) {
             if (*s_abort) return false;
-            if (__hip_atomic_load((const MOE_GLOBAL uint32_t *)(flags + 1), __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT)) {
+            if (launch_aborted(flags, atag)) {
                 *s_abort = 1;
                 return false;
             }
             if (spins > spin_max) {
-                stack_abort(flags, s_abort);
+                stack_abort(flags, atag, s_abort);
                 return false;
             }
         }
@@ -148,7 +158,7 @@ __device__ __forceinline__ bool poll_until_tagged(u32x4 (&v)[MAXQ], const int (&
 // Bounded wait (same limits as poll_until_tagged) until the XCD-local counter reaches
 // target; returns the count seen, or 0 when the wait expired or the launch aborted.
 __device__ __forceinline__ uint32_t wait_count(const uint32_t *ctr, uint32_t target, uint32_t *flags,
-                                               uint32_t spin_max, lds_flag *s_abort) {
+                                               uint32_t atag, uint32_t spin_max, lds_flag *s_abort) {
     uint32_t spins = 0;
     while (true) {
         const uint32_t c = (uint32_t)__builtin_amdgcn_readfirstlane((int)__hip_atomic_load(
@@ -157,13 +167,12 @@ __device__ __forceinline__ uint32_t wait_count(const uint32_t *ctr, uint32_t tar
         ++spins;
         if ((spins & 31u) == 0 || spins > spin_max) {
             if (*s_abort) return 0u;
-            if (__hip_atomic_load((const MOE_GLOBAL uint32_t *)(flags + 1), __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT)) {
+            if (launch_aborted(flags, atag)) {
                 *s_abort = 1;
                 return 0u;
             }
             if (spins > spin_max) {
-                stack_abort(flags, s_abort);
+                stack_abort(flags, atag, s_abort);
                 return 0u;
             }
         }
@@ -205,6 +214,14 @@ __device__ __forceinline__ void store_quad(uint32_t *xq, int q, u32x4 v) {
     *reinterpret_cast<u32x2 *>(c + 8) =
         u32x2{__builtin_amdgcn_perm(v[1], v[0], 0x06040200u), __builtin_amdgcn_perm(v[3], v[2], 0x06040200u)};
 }
+
+// 16-byte quads of one layer block of an exchange set (stack_layer_words / 4).
+template <int H, int I>
+__host__ __device__ constexpr uint64_t stack_layer_quads() {
+    return (uint64_t)STK_NX * (3 * I + H + H / 2 + H / 32 + H / 64) / 4;
+}
+static_assert(stack_layer_quads<2048, 512>() * 4 == (uint64_t)STK_NX * (3 * 512 + 2048 + 1024 + 64 + 32),
+              "whole quads per layer block");
 
 template <int H, int I>
 __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
@@ -262,74 +279,142 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     __shared__ const uint8_t *rt_p[3][2][3]; // W1, W3, W2 of the routed expert / shared
     __shared__ int s_abort;
     __shared__ int s_j;
+    __shared__ uint32_t s_ep;
+    __shared__ RouteLds s_route[2]; // layers 0 and 1, routed by four waves each
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     // HW_REG_XCC_ID (readfirstlane: the compiler then knows the value is wave-uniform)
     const int k = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & (NX - 1));
     const int n = a.n_layers;
     lds_flag *abort_lds = (lds_flag *)&s_abort;
-    // j: this workgroup's rank among the workgroups that started on XCD k, from a per-XCD
-    // ticket (not from blockIdx, so no assumption on the dispatch order).  An XCD that
-    // receives more than NJ workgroups leaves another XCD short: the surplus ones raise the
-    // timeout and leave, and the others' bounded waits end the launch with y untouched.
-    if (tid == 0) {
-        const uint32_t t = __hip_atomic_fetch_add((MOE_GLOBAL uint32_t *)(a.ctl + k), 1u, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-        s_j = t < (uint32_t)NJ ? (int)t : -1;
-        s_abort = 0;
+    auto ctl = [&](int w) { return a.ctl + (size_t)w * STK_CTL_STRIDE; };
+
+    // Layer r's routing into ring slot r % 3: the id and weight of slot k (lane s of a routing
+    // result holds rank s; lanes 8 and up the shared expert) and the weight pointers; the
+    // first workgroup also publishes the layer's ids and weights.
+    auto ring_write = [&](int r, int id, float wt, const LayerPtrs &L) __attribute__((always_inline)) {
+        const int idk = __builtin_amdgcn_readlane(id, k);
+        const float wk = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wt), k));
+        if (lane < 2) {
+            const int e = lane == 0 ? idk : a.E;
+            rt_w[r % 3][lane] = lane == 0 ? wk : 1.0f;
+            rt_p[r % 3][lane][0] = expert_w(L.w1, L.s1, L.sw1, e, a.E);
+            rt_p[r % 3][lane][1] = expert_w(L.w3, L.s3, L.sw3, e, a.E);
+            rt_p[r % 3][lane][2] = expert_w(L.w2, L.s2, L.sw2, e, a.E);
+        }
+        if (blockIdx.x == 0 && a.ids_out && lane < SLOTS) {
+            a.ids_out[(size_t)r * SLOTS + lane] = (uint16_t)id;
+            a.w_out[(size_t)r * SLOTS + lane] = wt;
+        }
+    };
+
+    // Start: compute waves 0-3 route layer 0 and waves 4-7 layer 1 (route_wg4: two LDS
+    // barriers, which every wave of the workgroup passes); the router wave takes this
+    // workgroup's rank j among the workgroups that started on XCD k -- a per-XCD ticket, not
+    // blockIdx, so no assumption on the dispatch order -- and the launch epoch meanwhile.  An
+    // XCD that receives more than NJ workgroups leaves another XCD short: the surplus ones
+    // raise the timeout and leave, and the others' bounded waits end the launch with y
+    // untouched.
+    if (wv < NCW) {
+        const int grp = wv >> 2, r = grp < n ? grp : 0;
+        const LayerPtrs L = load_layer(a.layers + a.layer0 + r);
+        int id;
+        float wt;
+        route_wg4(a.logits + (size_t)r * a.E, a.E, a.renorm, lane, wv & 3, s_route[grp], id, wt);
+        if ((wv & 3) == 0 && grp < n) ring_write(grp, id, wt, L);
+    } else {
+        // the ticket and the epoch are requested first and waited for only after the routing
+        // waves' two barriers
+        const bool tk = wv == NCW && lane == 0;
+        uint32_t t = 0u, e0 = 0u;
+        if (tk) {
+            t = __hip_atomic_fetch_add((MOE_GLOBAL uint32_t *)ctl(k), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            e0 = __hip_atomic_load((const MOE_GLOBAL uint32_t *)ctl(STK_CTL_EPOCH), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+        lds_barrier();
+        lds_barrier();
+        if (tk) {
+            s_j = t < (uint32_t)NJ ? (int)t : -1;
+            s_ep = e0;
+            s_abort = 0;
+        }
     }
-    __syncthreads();
+    lds_barrier(); // B0: routing of layers 0 and 1, ticket and epoch in LDS
     const int j = s_j;
+    const uint32_t ep = s_ep;
+    const uint32_t atag = ep | 0x80000000u; // this launch's abort-word value (never 0)
+    uint32_t *const xset = a.xs + (size_t)(ep & 1u) * a.set_words;
+
+    // The other exchange set: the previous launch used it; this launch clears the layer blocks
+    // it wrote, in n + 1 pieces (one per router-wave window), workgroup b taking an equal,
+    // 512-byte aligned share -- by blockIdx, so surplus workgroups do theirs too.
+    uint32_t dirty_o = 0u; // layer blocks of the other set to clear (read by the router wave)
+    if (wv == NCW)
+        dirty_o = min(ldg<uint32_t>(ctl(STK_CTL_DIRTY + (int)((ep & 1u) ^ 1u))), (uint32_t)a.n_max);
+    auto clear_other = [&](int piece, int pieces) __attribute__((always_inline)) {
+        const uint32_t o = (ep & 1u) ^ 1u;
+        const uint64_t Q = (uint64_t)dirty_o * stack_layer_quads<H, I>();
+        const uint64_t per = ((Q + NB - 1) / NB + 31) & ~(uint64_t)31;
+        const uint64_t q0 = min((uint64_t)blockIdx.x * per, Q), q1 = min(q0 + per, Q);
+        const uint64_t b0 = q0 + (q1 - q0) * (uint64_t)piece / pieces, b1 = q0 + (q1 - q0) * (uint64_t)(piece + 1) / pieces;
+        u32x4 *dst = reinterpret_cast<u32x4 *>(a.xs + (size_t)o * a.set_words);
+        for (uint64_t q = b0 + lane; q < b1; q += 64) *(MOE_GLOBAL u32x4 *)(dst + q) = u32x4{0u, 0u, 0u, 0u};
+    };
     if (j < 0) {
-        if (tid == 0) stack_abort(a.flags, abort_lds);
+        if (wv == NCW) {
+            clear_other(0, 1);
+            if (lane == 0) stack_abort(a.flags, atag, abort_lds);
+        }
         return;
     }
 
-    // exchange buffers of (layer li, XCD k)
-    auto hbuf = [&](int li) { return a.hx + ((size_t)li * NX + k) * HXG; };
-    auto pbuf = [&](int li) { return a.px + (size_t)li * NX * H; };
-    auto xbuf = [&](int li) { return a.xx + ((size_t)li * NX + k) * (4 * XQ); }; // x_{li+1}
+    // exchange buffers of (layer li, XCD k) in this launch's set: one block per layer
+    constexpr size_t LW = 4 * stack_layer_quads<H, I>();
+    auto hbuf = [&](int li) { return xset + (size_t)li * LW + (size_t)k * HXG; };
+    auto pbuf = [&](int li) { return xset + (size_t)li * LW + (size_t)NX * HXG; };
+    auto xbuf = [&](int li) { return xset + (size_t)li * LW + (size_t)NX * (HXG + H) + (size_t)k * (4 * XQ); }; // x_{li+1}
 
     if (wv == NCW) {
-        // ---------------- router wave: expert pointers two layers ahead into the LDS ring.
-        // The routing of every layer was computed by k_stack_prep; the id, weight and
-        // layer-table entry of the next layer are loaded one layer ahead, so this wave
-        // never waits on memory.
-        int id;
-        float wt;
+        // ---------------- router wave: routes layer r + 3 into ring slot r % 3 while the
+        // pollers end layer r (after B3; that slot was last read in phase B of r and is next
+        // read at B2 of r + 2), layer 2 right after B0; clears the other exchange set.
+        float raw[4];
         LayerPtrs L;
-        auto fetch = [&](int li) __attribute__((always_inline)) {
-            id = a.rid[(size_t)li * SLOTS + k];
-            wt = a.rwt[(size_t)li * SLOTS + k];
-            L = load_layer(a.layers + a.layer0 + li);
+        auto fetch = [&](int r) __attribute__((always_inline)) {
+            load_logits<4>(a.logits + (size_t)r * a.E, a.E, lane, raw);
+            L = load_layer(a.layers + a.layer0 + r);
         };
-        auto route = [&](int li) __attribute__((always_inline)) {
-            if (lane < 2) {
-                const int e = lane == 0 ? id : a.E;
-                rt_w[li % 3][lane] = lane == 0 ? wt : 1.0f;
-                rt_p[li % 3][lane][0] = expert_w(L.w1, L.s1, L.sw1, e, a.E);
-                rt_p[li % 3][lane][1] = expert_w(L.w3, L.s3, L.sw3, e, a.E);
-                rt_p[li % 3][lane][2] = expert_w(L.w2, L.s2, L.sw2, e, a.E);
-            }
-            if (li + 1 < n) fetch(li + 1);
+        auto route = [&](int r) __attribute__((always_inline)) {
+            int id;
+            float wt;
+            route_values<4>(raw, a.E, a.renorm, lane, id, wt);
+            ring_write(r, id, wt, L);
+            if (r + 1 < n) fetch(r + 1);
         };
-        fetch(0);
-        route(0);
-        if (n > 1) route(1);
-        // ring slots not yet routed hold layer 0's pointers: the compute waves' prefetches
-        // are unconditional (see below) and must always find valid addresses
-        for (int r = n > 1 ? 2 : 1; r < 3; ++r)
-            if (lane < 2) {
-                rt_w[r][lane] = rt_w[0][lane];
-                for (int m = 0; m < 3; ++m) rt_p[r][lane][m] = rt_p[0][lane][m];
+        if (blockIdx.x == 0 && lane == 0)
+            __hip_atomic_store((MOE_GLOBAL uint32_t *)ctl(STK_CTL_DIRTY + (int)(ep & 1u)), (uint32_t)n,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (n > 2) fetch(2);
+        // window 0 follows B0, window li + 1 follows B3 of layer li; window w routes layer w + 2
+        for (int wdw = 0; wdw <= n; ++wdw) {
+            if (wdw > 0) {
+                lds_barrier();             // B1 of layer wdw - 1
+                lds_barrier();             // B2
+                // every workgroup of the XCD published its h of layer 0 (the wait before B2
+                // succeeded), so all took their tickets: reset the XCD's counter for the next
+                // launch
+                if (wdw == 1 && j == 0 && lane == 0 && !*abort_lds)
+                    __hip_atomic_store((MOE_GLOBAL uint32_t *)ctl(k), 0u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                lds_barrier();             // B3
             }
-        lds_barrier(); // B0
-        for (int li = 0; li < n; ++li) {
-            lds_barrier();                 // B1
-            // ring slot (li+2)%3 was last read before B3 of li-1, and is next read after B2
-            if (li + 2 < n) route(li + 2);
-            lds_barrier();                 // B2
-            lds_barrier();                 // B3
+            // at the priority of the compute waves' phases: at 0 the routing took issue slots
+            // behind the compute waves' lookups and reached B1 late (measured +0.5 us per layer)
+            __builtin_amdgcn_s_setprio(3);
+            if (wdw + 2 < n) route(wdw + 2);
+            __builtin_amdgcn_s_setprio(0);
+            clear_other(wdw, n + 1);
         }
         return;
     }
@@ -365,7 +450,6 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         }
         // the reducer's own 64 rows of the residual, kept in f32
         float xres = first ? a.x[ROWS * j + lane] : 0.f;
-        lds_barrier(); // B0
         for (int li = 0; li < n; ++li) {
             lds_barrier(); // B1: x_li in LDS
             // the h exchange: ahead of the compute waves' phase-B lookups (priority 0), level
@@ -384,7 +468,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                     q[m] = first ? I / 4 + 4 * lane + m : lane + 64 * m;
                     v[m] = ok ? ld(q[m]) : u32x4{1u, 1u, 1u, 1u};
                 }
-                got = poll_until_tagged<4>(v, q, ld, a.flags, a.spin_max, abort_lds) && got;
+                got = poll_until_tagged<4>(v, q, ld, a.flags, atag, a.spin_max, abort_lds) && got;
                 if (first) {
                     if (lane < I / NX) {
                         float g = 0.f, u = 0.f;
@@ -431,7 +515,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 const int m = lane >> 4, qq = lane & 15;
                 int q[2] = {m * (H / 4) + qq, (m + 4) * (H / 4) + qq};
                 u32x4 v[2] = {ld(q[0]), ld(q[1])};
-                got = poll_until_tagged<2>(v, q, ld, a.flags, a.spin_max, abort_lds) && got;
+                got = poll_until_tagged<2>(v, q, ld, a.flags, atag, a.spin_max, abort_lds) && got;
                 *reinterpret_cast<f32x4 *>(&ps[m][4 * qq]) = __builtin_bit_cast(f32x4, v[0]);
                 *reinterpret_cast<f32x4 *>(&ps[m + 4][4 * qq]) = __builtin_bit_cast(f32x4, v[1]);
                 // lanes read what other lanes of this wave wrote: LDS keeps a wave's
@@ -475,13 +559,34 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                     // expired wait anywhere in the launch -- every later wait on what it would
                     // have published expires too -- thus leaves y, and an x it aliases, as it
                     // was.
-                    uint32_t *done = a.ctl + STK_CTL_DONE;
+                    uint32_t *done = ctl(STK_CTL_DONE);
                     const bool sound = got && !*abort_lds;
                     if (lane == 0)
                         __hip_atomic_fetch_add((MOE_GLOBAL uint32_t *)done, sound ? 1u : STK_DONE_ABORT,
                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    if (wait_count(done, (uint32_t)NJ, a.flags, a.spin_max, abort_lds) == (uint32_t)NJ)
+                    const uint32_t c = wait_count(done, (uint32_t)NJ, a.flags, atag, a.spin_max, abort_lds);
+                    if (c == (uint32_t)NJ)
                         *(MOE_GLOBAL float *)(a.y + row) = x1;
+                    else if (c != 0u && lane == 0)
+                        set_flag(a.flags, MOE_DEVFLAG_TIMEOUT); // a count past NJ: not every reducer was sound
+                    // The last of XCD 0's reducers to leave resets the two counts and advances
+                    // the epoch, which switches the next launch to the exchange set this launch
+                    // cleared.  By then every workgroup of the launch has started (each of them
+                    // published a partial this XCD gathered, or left the gathers waiting) and
+                    // read the epoch, and every reducer of XCD 0 has passed its wait on `done`.
+                    if (lane == 0) {
+                        uint32_t *ex = ctl(STK_CTL_EXIT);
+                        const uint32_t t = __hip_atomic_fetch_add((MOE_GLOBAL uint32_t *)ex, 1u, __ATOMIC_RELAXED,
+                                                                  __HIP_MEMORY_SCOPE_AGENT);
+                        if (t == (uint32_t)NJ - 1u) {
+                            __hip_atomic_store((MOE_GLOBAL uint32_t *)done, 0u, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                            __hip_atomic_store((MOE_GLOBAL uint32_t *)ex, 0u, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                            __hip_atomic_store((MOE_GLOBAL uint32_t *)ctl(STK_CTL_EPOCH), ep + 1u,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        }
+                    }
                 }
             }
             if (li + 1 < n) {
@@ -496,7 +601,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 }
                 // pair words are tagged by being nonzero; the scales and sums of squares
                 // are LSB-tagged f32 words, which are nonzero too
-                got = poll_until_tagged<XP>(v, q, ld, a.flags, a.spin_max, abort_lds, NonzeroTag{}) && got;
+                got = poll_until_tagged<XP>(v, q, ld, a.flags, atag, a.spin_max, abort_lds, NonzeroTag{}) && got;
 #pragma unroll
                 for (int m = 0; m < XP; ++m) {
                     if (q[m] < XD) {
@@ -690,7 +795,6 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         asm volatile("" : "+v"(sbk[0]), "+v"(sbk[1]), "+v"(bs), "+v"(sbs));
     };
 
-    lds_barrier(); // B0: routing of layers 0 and 1 is in LDS
     prefetch_a(0);
     decode_a();
 
@@ -797,52 +901,14 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     }
 }
 
-// Before a stack launch: clears the tagged exchange buffers and the abort word (a kernel,
-// not hipMemsetAsync, so the sequence can be captured into a graph), and routes every layer
-// -- the logits are an input, so the top-8 of all layers is computed here in parallel, one
-// wave per layer, instead of on the stack's critical path.
-__global__ void k_stack_prep(StackArgs a, uint64_t words) {
-    if (blockIdx.x == 0 && threadIdx.x == 0) a.flags[1] = 0u;
-    u32x4 *p4 = reinterpret_cast<u32x4 *>(a.hx);
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words / 4;
-         i += (uint64_t)gridDim.x * blockDim.x)
-        p4[i] = u32x4{0u, 0u, 0u, 0u};
-    if ((int)blockIdx.x < a.n_layers) {
-        // the four waves route layer li together (the whole workgroup: route_wg4 has barriers)
-        __shared__ RouteLds R;
-        const int li = blockIdx.x, lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-        int id;
-        float wt;
-        route_wg4(a.logits + (size_t)li * a.E, a.E, a.renorm, lane, wv, R, id, wt);
-        if (wv == 0 && lane < SLOTS) {
-            a.rid[(size_t)li * SLOTS + lane] = (uint16_t)id;
-            a.rwt[(size_t)li * SLOTS + lane] = wt;
-            if (a.ids_out) {
-                a.ids_out[(size_t)li * SLOTS + lane] = (uint16_t)id;
-                a.w_out[(size_t)li * SLOTS + lane] = wt;
-            }
-        }
-    }
-}
-
-// Per layer and XCD: h (3I words), the XCD's partial of every row (H), and x' as int8
-// pair words + chunk scales + per-workgroup sums of squares (H/2 + H/32 + H/64); then the
-// STK_CTL_WORDS control words (tickets, done count).
-size_t stack_exchange_words(int H, int I, int n_layers) {
-    return (size_t)n_layers * STK_NX * (3 * (size_t)I + (size_t)H + (size_t)(H / 2 + H / 32 + H / 64)) + STK_CTL_WORDS;
+size_t stack_layer_words(int H, int I) {
+    return (size_t)STK_NX * (3 * (size_t)I + (size_t)H + (size_t)(H / 2 + H / 32 + H / 64));
 }
 
 template <int H, int I>
 static hipError_t launch_stack_t(const StackArgs &a, hipStream_t st, KernelTimer *T) {
-    const uint64_t words = stack_exchange_words(H, I, a.n_layers);
-    {
-        TimedLaunch tl(T, MOE_K_STACK_PREP, st);
-        hipLaunchKernelGGL(k_stack_prep, dim3(max(512, a.n_layers)), dim3(256), 0, st, a, words);
-    }
-    {
-        TimedLaunch tl(T, MOE_K_DECODE_STACK, st);
-        hipLaunchKernelGGL((k_decode_stack<H, I>), dim3(H / 8), dim3(64 * STK_WAVES), 0, st, a);
-    }
+    TimedLaunch tl(T, MOE_K_DECODE_STACK, st);
+    hipLaunchKernelGGL((k_decode_stack<H, I>), dim3(H / 8), dim3(64 * STK_WAVES), 0, st, a);
     return hipGetLastError();
 }
 

@@ -41,9 +41,8 @@ struct moe_ctx {
     uint32_t *chunk = nullptr;   // [ceil(m_max/64)][E+1]
     Tile *tiles = nullptr;       // [tile_max(m_max) + stile_max]
     LayerPtrs *dlayers = nullptr; // device layer table of the split copies (decode stack)
-    uint32_t *xtag = nullptr;    // decode stack exchange buffers
-    uint16_t *srid = nullptr;    // decode stack: routing of every layer
-    float *srw = nullptr;
+    uint32_t *xtag = nullptr;    // decode stack: control words, then its two exchange sets
+    size_t xtag_words = 0;
     int stack_ok = 0;            // all stack workgroups fit on the device at once
     int ncu = 0;                 // compute units of the device
     uint32_t spin_max = STK_SPIN_DEFAULT; // decode stack: poll rounds before a wait expires
@@ -153,9 +152,7 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
         {(void **)&c->chunk, nchunk * E1 * 4},
         {(void **)&c->tiles, (tmax + (size_t)stile_max_for((int)E1)) * sizeof(Tile)},
         {(void **)&c->dlayers, (size_t)cfg->n_layers * sizeof(LayerPtrs)},
-        {(void **)&c->xtag, stack_exchange_words(H, I, cfg->n_layers) * 4},
-        {(void **)&c->srid, (size_t)cfg->n_layers * SLOTS * 2},
-        {(void **)&c->srw, (size_t)cfg->n_layers * SLOTS * 4},
+        {(void **)&c->xtag, (STK_CTL_WORDS + 2 * (size_t)cfg->n_layers * stack_layer_words(H, I)) * 4},
     };
     size_t total = 0;
     for (auto &p : parts) total += align_up(p.bytes, 256);
@@ -183,8 +180,11 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
                         hipGetErrorString(he));
         }
     }
+    c->xtag_words = STK_CTL_WORDS + 2 * (size_t)cfg->n_layers * stack_layer_words(H, I);
     he = hipMemset(c->flags, 0, 256);
     if (he == hipSuccess) he = hipMemset(c->dlayers, 0, (size_t)cfg->n_layers * sizeof(LayerPtrs));
+    // the decode stack's control words and both exchange sets start zeroed
+    if (he == hipSuccess) he = hipMemset(c->xtag, 0, c->xtag_words * 4);
     if (he == hipSuccess) he = hipDeviceSynchronize();
     if (he != hipSuccess) {
         if (c->spk) (void)hipFree(c->spk);
@@ -473,12 +473,10 @@ moe_status moe_decode_stack(moe_ctx *ctx, int layer0, int n_layers, const float 
     a.y = y;
     a.ids_out = ids;
     a.w_out = w;
-    a.hx = ctx->xtag;
-    a.px = a.hx + (size_t)n_layers * 8 * 3 * I;
-    a.xx = a.px + (size_t)n_layers * 8 * H;
-    a.ctl = a.hx + stack_exchange_words(ctx->cfg.hidden, ctx->cfg.inter, n_layers) - STK_CTL_WORDS;
-    a.rid = ctx->srid;
-    a.rwt = ctx->srw;
+    a.ctl = ctx->xtag;
+    a.xs = ctx->xtag + STK_CTL_WORDS;
+    a.n_max = ctx->cfg.n_layers;
+    a.set_words = (size_t)ctx->cfg.n_layers * stack_layer_words(H, I);
     a.flags = ctx->flags;
     a.spin_max = ctx->spin_max;
     a.E = ctx->cfg.n_experts;
@@ -563,6 +561,9 @@ moe_status moe_device_flags(moe_ctx *ctx, void *stream, uint32_t *flags) {
     he = hipMemcpy(&v, ctx->flags, 4, hipMemcpyDeviceToHost);
     if (he != hipSuccess) return hip_fail(he, "moe_device_flags: hipMemcpy");
     he = hipMemset(ctx->flags, 0, 4);
+    // after an expired wait the decode stack's control words and exchange sets may be in any
+    // state (a launch that saw one does not advance them reliably): start them over
+    if (he == hipSuccess && (v & MOE_DEVFLAG_TIMEOUT)) he = hipMemset(ctx->xtag, 0, ctx->xtag_words * 4);
     if (he == hipSuccess) he = hipDeviceSynchronize();
     if (he != hipSuccess) return hip_fail(he, "moe_device_flags: clearing");
     *flags = v;
@@ -572,7 +573,7 @@ moe_status moe_device_flags(moe_ctx *ctx, void *stream, uint32_t *flags) {
 moe_status moe_device_flags_async(moe_ctx *ctx, uint32_t *dst, void *stream) {
     if (!ctx || !dst) return fail(MOE_EINVAL, "moe_device_flags_async: null argument");
     if ((uintptr_t)dst & 3u) return fail(MOE_EINVAL, "moe_device_flags_async: dst not 4-byte aligned");
-    hipError_t he = launch_flags_take(ctx->flags, dst, as_stream(stream));
+    hipError_t he = launch_flags_take(ctx->flags, dst, ctx->xtag, ctx->xtag_words, as_stream(stream));
     if (he != hipSuccess) return hip_fail(he, "moe_device_flags_async: launch");
     return ok();
 }

@@ -120,24 +120,27 @@ struct StackArgs {
     float *y;                // [H] output activation (may alias x)
     uint16_t *ids_out;       // [n_layers][9] or null
     float *w_out;            // [n_layers][9] or null
-    // tagged exchange buffers (stack_exchange_words words from hx on, cleared per launch)
-    uint32_t *hx;            // [n_layers][8 XCDs][3I] h of each XCD's rows (shared rows as partials)
-    uint32_t *px;            // [n_layers][8 XCDs][H] each XCD's partial of the layer output
-    uint32_t *xx;            // [n_layers][8 XCDs][H] x_{l+1}, one copy per XCD
-    uint32_t *ctl;           // control words: per-XCD workgroup tickets, the done count
-    uint16_t *rid;           // [n_layers][9] routing of every layer (k_stack_prep)
-    float *rwt;              // [n_layers][9]
-    uint32_t *flags;         // [0] sticky device flags, [1] abort word
+    // Two sets of tagged exchange buffers, set_words words each (n_max layer blocks of
+    // stack_layer_words(H, I)): a launch uses set (epoch & 1), which the previous launch
+    // cleared, and clears the other one for the next launch.
+    uint32_t *xs;
+    size_t set_words;
+    int n_max;               // layer blocks per set (the context's n_layers)
+    uint32_t *ctl;           // control words, STK_CTL_STRIDE apart (STK_CTL_*)
+    uint32_t *flags;         // [0] sticky device flags, [1] abort word (tagged with the epoch)
     uint32_t spin_max;       // poll rounds before a bounded wait expires
     int E, rmsnorm, renorm;
     float c;
 };
 
 constexpr uint32_t STK_SPIN_DEFAULT = 1u << 16;
-// Control words after the stack's exchange buffers: one workgroup ticket counter per XCD,
-// then the count of last-layer reducers done (cleared with the buffers before every launch).
-constexpr int STK_CTL_WORDS = 16;
-constexpr int STK_CTL_DONE = 8;
+// Control words of the decode stack, each on its own 128-byte line: one workgroup ticket
+// counter per XCD, the count of last-layer reducers done and of those that left (XCD 0), the
+// launch epoch (its parity picks the exchange set) and the number of layer blocks each set
+// may hold written words in.  All zero at moe_create and after a recovery.
+constexpr int STK_CTL_STRIDE = 32;
+constexpr int STK_CTL_DONE = 8, STK_CTL_EXIT = 9, STK_CTL_EPOCH = 10, STK_CTL_DIRTY = 11; // DIRTY + set
+constexpr int STK_CTL_WORDS = 16 * STK_CTL_STRIDE;
 
 // Optional per-kernel timing (moe_timing_enable): each launch is bracketed by two HIP
 // events recorded on the launch's own stream.  Events are created when timing is enabled,
@@ -187,11 +190,16 @@ hipError_t launch_decode(int H, int I, const DecodeArgs &a, hipStream_t st, Kern
 // Bucket fill and prep (one launch), gate/up, down, combine.
 hipError_t launch_prefill(int H, int I, const BucketArgs &b, const PrefillArgs &a, hipStream_t st, KernelTimer *T);
 hipError_t launch_stack(int H, int I, const StackArgs &a, hipStream_t st, KernelTimer *T);
-// *dst = the sticky device flags, which are cleared (one thread, stream ordered).
-hipError_t launch_flags_take(uint32_t *flags, uint32_t *dst, hipStream_t st);
+// *dst = the sticky device flags, which are cleared (stream ordered).  When they hold
+// MOE_DEVFLAG_TIMEOUT, the decode stack's state -- `stack_words` words from `stack` on, its
+// control words and both exchange sets -- is zeroed as well (recovery after an expired wait).
+hipError_t launch_flags_take(uint32_t *flags, uint32_t *dst, uint32_t *stack, size_t stack_words, hipStream_t st);
 hipError_t stack_occupancy(int H, int I, int *blocks_per_cu);
 int stack_blocks(int H);
-size_t stack_exchange_words(int H, int I, int n_layers);
+// Words of one layer block of a decode-stack exchange set: per XCD the h words (3I), the
+// partial of every output row (H), and x' as int8 pair words + chunk scales + per-workgroup
+// sums of squares (H/2 + H/32 + H/64).
+size_t stack_layer_words(int H, int I);
 
 // Big tiles: PF_BM-slot tiles of every expert plus remainders above PF_SMALL_MAX slots.
 // Small tiles: remainders of 1..PF_SMALL_MAX slots, one tile per expert.
