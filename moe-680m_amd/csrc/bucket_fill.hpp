@@ -16,7 +16,7 @@ namespace moe {
 // reference's cursor fill.  Up to 16 chunks (1024 tokens) one 1024-thread workgroup does it
 // all; beyond that the chunks are spread over workgroups (bucket_count_chunk, bucket_scan_wg,
 // bucket_scatter_chunk).
-// The same pass writes the grouped-GEMM tile lists (see tile_max_for / stile_max_for).
+// The same pass writes the grouped-GEMM tile lists (see tile_max_for).
 constexpr int BF_THREADS = 1024;
 constexpr int BF_BITMAP_BYTES = 48 * 1024;
 
@@ -177,8 +177,10 @@ __device__ __forceinline__ void bucket_scan_and_lists(const BucketArgs &a, CntLa
 
     for (int e = tid; e <= E1; e += BF_THREADS) a.ranges[e] = S.rg[e];
     if (a.tiles) {
-        const uint32_t nfull = S.ts[E1];
-        Tile *small = a.tiles + a.tile_max;
+        // one list: full tiles, big remainders, then small remainders, then empty entries up to
+        // tile_max (every expert has at most one remainder, so the tiles never exceed it)
+        const uint32_t nfull = S.ts[E1], nbig = nfull + S.tp[E1];
+        Tile *small = a.tiles + nbig;
         for (int e = tid; e < E1; e += BF_THREADS) {
             const int n = (int)S.tot[e];
             const int nf = n / PF_BM, rem = n % PF_BM;
@@ -189,8 +191,7 @@ __device__ __forceinline__ void bucket_scan_and_lists(const BucketArgs &a, CntLa
                 small[S.tsm[e]] = Tile{e, (int)S.rg[e] + nf * PF_BM, rem, 0};
             }
         }
-        for (int i = (int)(nfull + S.tp[E1]) + tid; i < a.tile_max; i += BF_THREADS) a.tiles[i] = Tile{-1, 0, 0, 0};
-        for (int i = (int)S.tsm[E1] + tid; i < a.stile_max; i += BF_THREADS) small[i] = Tile{-1, 0, 0, 0};
+        for (int i = (int)(nbig + S.tsm[E1]) + tid; i < a.tile_max; i += BF_THREADS) a.tiles[i] = Tile{-1, 0, 0, 0};
     }
     __syncthreads();
 }

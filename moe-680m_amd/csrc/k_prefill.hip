@@ -422,12 +422,15 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
     const int n = lane & 15, g = lane >> 4;
     const int cw = SPLIT ? (wv & 3) : wv, p = SPLIT ? (wv >> 2) : 0; // column group, stage parity
     const int c0 = blockIdx.x * NGU + cw * 16; // this wave's h columns
-    // the tile's tokens and their 1/scale (rows past nrows repeat the last token)
+    // the tile's tokens (rows past nrows repeat the last token); their 1/scale is requested
+    // here but only waited for, and put in LDS, before the epilogue: A's loads depend on the
+    // tokens, not on it
+    float inv_t = 0.0f;
     if (tid < PF_BM) {
         const int t = a.sorted_tok[row0 + (tid < nrows ? tid : nrows - 1)];
         s_tok[tid] = t;
-        s_inv[tid] = a.xinv[t];
         rowmax[tid] = 0u;
+        inv_t = a.xinv[t];
     }
     lds_barrier();
     // Weights: rows c0 + n of W1 (gate) and W3 (up).
@@ -487,6 +490,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
             load_a(c, HALF, PER);
             store_a(HALF, PER);
         };
+        if (tid < PF_BM) s_inv[tid] = inv_t;
         if constexpr (SPLIT) {
             gemm_resident_split<NCH, RD, SBR, 2, MT>(ws, rows, As, n, g, p, acc, stage_a);
             // the odd-stage wave hands its sums to its partner through the (now free) A chunk
@@ -508,6 +512,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
             }
         } else {
             gemm_resident<NCH, RD, SBR, 2, MT>(ws, rows, As, n, g, acc, stage_a);
+            lds_barrier(); // s_inv
         }
 
         // epilogue (even-stage waves): h = silu(g) * u with the token scale undone; per-row max|h| of the block,
@@ -522,7 +527,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
                 hv[mt][i] = 0.0f;
                 if (m < nrows && !p) {
                     const float inv = s_inv[m];
-                    hv[mt][i] = silu(acc[mt][0][i] * inv) * (acc[mt][1][i] * inv);
+                    hv[mt][i] = silu_rcp(acc[mt][0][i] * inv) * (acc[mt][1][i] * inv);
                 }
                 const float rm = max16(fabsf(hv[mt][i]));
                 if (n == 0 && !p) atomicMax(&rowmax[m], __builtin_bit_cast(uint32_t, rm));
@@ -555,7 +560,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
     static_assert(I % QK == 0 && H % PF_ND == 0 && PF_KC * 2 == QK, "down shape");
     static_assert(pf_kch<NCH, 4>() == NCH, "all of K = inter resident in one chunk");
     __shared__ __attribute__((aligned(16))) _Float16 As[PF_AS_HALVES];
-    __shared__ float s_inv[PF_BM];
+    __shared__ float s_sc[PF_BM];
 
     const Tile tl = a.tiles[blockIdx.y];
     if (tl.expert < 0) return;
@@ -577,7 +582,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
         constexpr int NIT = 16 * MT * BPR, IPT = (NIT + 64 * PF_WAVES - 1) / (64 * PF_WAVES);
         static_assert(NGU % 32 == 0, "max blocks of whole 32-blocks");
         u32x4 hq[IPT][4];
-        float hm[IPT][NHB];
+        float hm[IPT][NHB], sw[IPT];
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
             const int it = j * 64 * PF_WAVES + tid;
@@ -589,6 +594,8 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
                 for (int i = 0; i < 4; ++i) hq[j][i] = ldg<u32x4>(src + i);
 #pragma unroll
                 for (int b = 0; b < NHB; ++b) hm[j][b] = a.hmax[(size_t)slot * NHB + b];
+                // the slot's weight, for the epilogue (loaded with the h rows, not after the GEMM)
+                sw[j] = ab == 0 ? a.sorted_w[slot] : 0.0f;
             }
         }
         constexpr int RD = 4; // weight ring depth: three stages ahead
@@ -606,7 +613,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
                 const float sc = pow2_scale(ar < nrows ? mx : 0.0f, &inv);
                 const float hb = hm[j][ab / (NGU / 32)];
                 (void)pow2_scale(hb, &inv_b);
-                if (ab == 0) s_inv[ar] = inv;
+                if (ab == 0) s_sc[ar] = ar < nrows ? a.c * sw[j] * inv : 0.0f; // the row's epilogue factor
                 // 2^-j, j >= 0, for a block with a nonzero max; a block whose max is 0 holds
                 // only zeros, and its factor is 0 (sc alone can exceed the f16 range when the
                 // row's max is small: 0 * inf would be NaN)
@@ -646,7 +653,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int m = 16 * mt + 4 * g + i;
-                const float sc = m < nrows ? a.c * a.sorted_w[row0 + m] * s_inv[m] : 0.0f;
+                const float sc = s_sc[m]; // c * w * 2^-s_row (0 past nrows)
                 float v[NTW], mx = 0.0f;
 #pragma unroll
                 for (int t = 0; t < NTW; ++t) {
@@ -727,8 +734,9 @@ static hipError_t launch_prefill_t(const BucketArgs &b, const PrefillArgs &a, hi
             hipLaunchKernelGGL(k_pf_scatter, dim3((unsigned)nch), dim3(BF_CHUNK_THREADS), smem, st, b);
         }
     }
-    // one launch over both tile lists (full and big remainder tiles, then small remainders)
-    const int ntiles = a.tile_max + a.stile_max;
+    // one launch over the tile list (full and big remainder tiles, then small remainders, then
+    // empty entries, which exit at once)
+    const int ntiles = a.tile_max;
     const bool split = a.M <= PF_SPLIT_MAX_M;
     {
         TimedLaunch tl(T, MOE_K_PREFILL_GATE_UP, st);

@@ -39,7 +39,7 @@ struct moe_ctx {
     float *sw = nullptr;         // [9 m_max]
     uint32_t *pos = nullptr;     // [m_max][9]
     uint32_t *chunk = nullptr;   // [ceil(m_max/64)][E+1]
-    Tile *tiles = nullptr;       // [tile_max(m_max) + stile_max]
+    Tile *tiles = nullptr;       // [tile_max(m_max)]
     LayerPtrs *dlayers = nullptr; // device layer table of the split copies (decode stack)
     uint32_t *xtag = nullptr;    // decode stack: control words, then its two exchange sets
     size_t xtag_words = 0;
@@ -150,7 +150,7 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
         {(void **)&c->sw, SLOTS * mm * 4},
         {(void **)&c->pos, mm * SLOTS * 4},
         {(void **)&c->chunk, nchunk * E1 * 4},
-        {(void **)&c->tiles, (tmax + (size_t)stile_max_for((int)E1)) * sizeof(Tile)},
+        {(void **)&c->tiles, tmax * sizeof(Tile)},
         {(void **)&c->dlayers, (size_t)cfg->n_layers * sizeof(LayerPtrs)},
         {(void **)&c->xtag, (STK_CTL_WORDS + 2 * (size_t)cfg->n_layers * stack_layer_words(H, I)) * 4},
     };
@@ -322,7 +322,6 @@ moe_status moe_bucket_fill(moe_ctx *ctx, const uint16_t *ids, const float *w, in
     a.chunk_cnt = ctx->chunk;
     a.tiles = nullptr;
     a.tile_max = 0;
-    a.stile_max = 0;
     a.flags = ctx->flags;
     hipError_t he = launch_bucket_fill(a, as_stream(stream), timer_for(ctx, as_stream(stream)));
     if (he != hipSuccess) return hip_fail(he, "moe_bucket_fill: launch");
@@ -392,7 +391,6 @@ static moe_status ffn_call(const char *fn, moe_ctx *ctx, int layer, const float 
     b.chunk_cnt = ctx->chunk;
     b.tiles = ctx->tiles;
     b.tile_max = tile_max_for(M, E + 1);
-    b.stile_max = stile_max_for(E + 1);
     b.flags = ctx->flags;
     PrefillArgs p{};
     p.L = ctx->slayers[layer];
@@ -413,7 +411,6 @@ static moe_status ffn_call(const char *fn, moe_ctx *ctx, int layer, const float 
     p.accumulate = (flags & MOE_FFN_ACCUMULATE) ? 1 : 0;
     p.rmsnorm = (flags & MOE_FFN_RMSNORM) ? 1 : 0;
     p.tile_max = b.tile_max;
-    p.stile_max = b.stile_max;
     p.c = c;
     he = launch_prefill(H, I, b, p, st, T);
     if (he != hipSuccess) return fail(MOE_EHIP, "%s: prefill launch: %s", fn, hipGetErrorString(he));

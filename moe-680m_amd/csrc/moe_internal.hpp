@@ -81,8 +81,8 @@ struct BucketArgs {
     float *sorted_w;      // [9M]
     uint32_t *pos;        // [M][9] or null
     uint32_t *chunk_cnt;  // workspace: ceil(M/64) * E1 chunk counts
-    Tile *tiles;          // [tile_max] big tiles (full first), then [stile_max] small tiles; or null
-    int tile_max, stile_max;
+    Tile *tiles;          // [tile_max]: full tiles, big remainders, small remainders, empty; or null
+    int tile_max;
     uint32_t *flags;
 };
 
@@ -105,7 +105,7 @@ struct PrefillArgs {
                          // stored side by side
     int8_t *pexp;        // [9M][H/32] those exponents
     float *y;
-    int M, E, accumulate, rmsnorm, tile_max, stile_max;
+    int M, E, accumulate, rmsnorm, tile_max;
     float c;
 };
 
@@ -201,10 +201,9 @@ int stack_blocks(int H);
 // sums of squares (H/2 + H/32 + H/64).
 size_t stack_layer_words(int H, int I);
 
-// Big tiles: PF_BM-slot tiles of every expert plus remainders above PF_SMALL_MAX slots.
-// Small tiles: remainders of 1..PF_SMALL_MAX slots, one tile per expert.
+// Tiles: the PF_BM-slot tiles of every expert, then each expert's remainder (above
+// PF_SMALL_MAX slots a big tile, else a small one): at most one remainder per expert.
 inline int tile_max_for(int M, int E1) { return (9 * M + PF_BM - 1) / PF_BM + E1; }
-inline int stile_max_for(int E1) { return E1; }
 
 } // namespace moe
 
