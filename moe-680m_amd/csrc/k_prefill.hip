@@ -122,12 +122,19 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
+// Max over the 16 lanes of a DPP row, for non-negative floats (ordered as their bit patterns,
+// so each step is one v_max_u32 with a DPP source).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
+}
 __device__ __forceinline__ float max16(float v) {
-    v = fmaxf(v, dpp_f<0xB1>(v));
-    v = fmaxf(v, dpp_f<0x4E>(v));
-    v = fmaxf(v, dpp_f<0x141>(v));
-    v = fmaxf(v, dpp_f<0x140>(v));
-    return v;
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    u = max(u, dpp_u<0xB1>(u));
+    u = max(u, dpp_u<0x4E>(u));
+    u = max(u, dpp_u<0x141>(u));
+    u = max(u, dpp_u<0x140>(u));
+    return __builtin_bit_cast(float, u);
 }
 
 // ---------------------------------------------------------------- prep
@@ -418,7 +425,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
     const Tile tl = a.tiles[blockIdx.y];
     if (tl.expert < 0) return;
     const int e = tl.expert, row0 = tl.row0, nrows = tl.nrows;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform (SGPR)
     const int n = lane & 15, g = lane >> 4;
     const int cw = SPLIT ? (wv & 3) : wv, p = SPLIT ? (wv >> 2) : 0; // column group, stage parity
     const int c0 = blockIdx.x * NGU + cw * 16; // this wave's h columns
@@ -491,60 +498,63 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
             store_a(HALF, PER);
         };
         if (tid < PF_BM) s_inv[tid] = inv_t;
+        // the wave's elements: el = 4 mt + i is row 16 mt + 4 g + i of the tile, column c0 + n.
+        // With SPLIT the two partner waves (stage parities 0 and 1) each finish half of them:
+        // parity 0 elements el < NE/2, parity 1 the rest, after handing each other the partial
+        // sums of the partner's half through the (then free) A chunk.
+        constexpr int NE = 4 * MT, NOWN = SPLIT ? NE / 2 : NE;
+        const int el0 = SPLIT && p ? NE / 2 : 0;
         if constexpr (SPLIT) {
             gemm_resident_split<NCH, RD, SBR, 2, MT>(ws, rows, As, n, g, p, acc, stage_a);
-            // the odd-stage wave hands its sums to its partner through the (now free) A chunk
             lds_barrier();
-            f32x4 *red = reinterpret_cast<f32x4 *>(As);
-            static_assert(4 * MT * 2 * 64 * 16 <= PF_AS_HALVES * 2, "the pair sums fit the A chunk");
-            if (p) {
+            float *red = reinterpret_cast<float *>(As);
+            static_assert(4 * NE * 2 * 64 * 4 <= PF_AS_HALVES * 2, "the pair sums fit the A chunk");
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
+            for (int el = 0; el < NE; ++el)
+                if ((el < NE / 2) == (p != 0))
 #pragma unroll
-                    for (int r = 0; r < 2; ++r) red[((cw * MT + mt) * 2 + r) * 64 + lane] = acc[mt][r];
-            }
+                    for (int r = 0; r < 2; ++r) red[((cw * NE + el) * 2 + r) * 64 + lane] = acc[el / 4][r][el % 4];
             lds_barrier();
-            if (!p) {
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
+            for (int el = 0; el < NE; ++el)
+                if ((el < NE / 2) == (p == 0))
 #pragma unroll
-                    for (int r = 0; r < 2; ++r) acc[mt][r] += red[((cw * MT + mt) * 2 + r) * 64 + lane];
-            }
+                    for (int r = 0; r < 2; ++r) acc[el / 4][r][el % 4] += red[((cw * NE + el) * 2 + r) * 64 + lane];
         } else {
             gemm_resident<NCH, RD, SBR, 2, MT>(ws, rows, As, n, g, acc, stage_a);
             lds_barrier(); // s_inv
         }
 
-        // epilogue (even-stage waves): h = silu(g) * u with the token scale undone; per-row max|h| of the block,
-        // then h as f16 scaled by the power of two that puts that max in [2^14, 2^15), stored
-        // in the down kernel's K order (perm32_pos inside every 32-column block)
-        float hv[MT][4];
+        // epilogue: h = silu(g) * u with the token scale undone; per-row max|h| of the item's
+        // columns, then h as f16 scaled by the power of two that puts that max in [2^14, 2^15),
+        // stored in the down kernel's K order (perm32_pos inside every 32-column block)
+        float hv[NOWN];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = 16 * mt + 4 * g + i;
-                hv[mt][i] = 0.0f;
-                if (m < nrows && !p) {
-                    const float inv = s_inv[m];
-                    hv[mt][i] = silu_rcp(acc[mt][0][i] * inv) * (acc[mt][1][i] * inv);
-                }
-                const float rm = max16(fabsf(hv[mt][i]));
-                if (n == 0 && !p) atomicMax(&rowmax[m], __builtin_bit_cast(uint32_t, rm));
+        for (int j = 0; j < NOWN; ++j) {
+            const int el = el0 + j, m = 16 * (el / 4) + 4 * g + el % 4;
+            // element j of this wave's half (selected, not indexed: acc stays in registers)
+            constexpr int JH = SPLIT ? NE / 2 : 0;
+            const float gv = SPLIT && p ? acc[(JH + j) / 4][0][(JH + j) % 4] : acc[j / 4][0][j % 4];
+            const float uv = SPLIT && p ? acc[(JH + j) / 4][1][(JH + j) % 4] : acc[j / 4][1][j % 4];
+            hv[j] = 0.0f;
+            if (m < nrows) {
+                const float inv = s_inv[m];
+                hv[j] = silu_rcp(gv * inv) * (uv * inv);
             }
+            const float rm = max16(fabsf(hv[j]));
+            if (n == 0) atomicMax(&rowmax[m], __builtin_bit_cast(uint32_t, rm));
+        }
         lds_barrier();
         const int col = c0 + n, hcol = (col & ~31) + perm32_pos(col & 31);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = 16 * mt + 4 * g + i;
-                if (m < nrows && !p) {
-                    float unused;
-                    const float sc = pow2_scale(__builtin_bit_cast(float, rowmax[m]), &unused);
-                    a.hh[(size_t)(row0 + m) * I + hcol] = (_Float16)(hv[mt][i] * sc);
-                }
+        for (int j = 0; j < NOWN; ++j) {
+            const int el = el0 + j, m = 16 * (el / 4) + 4 * g + el % 4;
+            if (m < nrows) {
+                float unused;
+                const float sc = pow2_scale(__builtin_bit_cast(float, rowmax[m]), &unused);
+                a.hh[(uint32_t)((row0 + m) * I + hcol)] = (_Float16)(hv[j] * sc); // < 2^31: 9 m_max I
             }
+        }
     });
     if (tid < nrows) a.hmax[(size_t)(row0 + tid) * (I / NGU) + blockIdx.x] = __builtin_bit_cast(float, rowmax[tid]);
 }
@@ -565,7 +575,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
     const Tile tl = a.tiles[blockIdx.y];
     if (tl.expert < 0) return;
     const int e = tl.expert, row0 = tl.row0, nrows = tl.nrows;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform (SGPR)
     const int n = lane & 15, g = lane >> 4;
     const int r0 = blockIdx.x * PF_ND + wv * 32; // this wave's output rows r0 .. r0+31
     const uint8_t *w2 = expert_w(a.L.w2, a.L.s2, a.L.sw2, e, a.E);
