@@ -496,21 +496,34 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_mt(DecodeArgs a) {
 // the element's expert's W2 rows against the pair's h, times c * w, into LDS.  The plan block
 // lists the valid pairs in ascending order, and they are dealt to the waves in turn, so the
 // shared expert's M pairs -- and any two tokens' shared routed expert -- go to different
-// waves (repeated W2 rows are L2 hits).  A wave reads its elements from the plan in one
-// round, requests the h of its first elements and the W2 rows of all of them at once, then
-// the h of later elements two ahead.  No barrier until the slot-order sums.
+// waves (repeated W2 rows are L2 hits).  The h of every pair (M * 9 rows of I, at most 144 KB)
+// is copied into LDS by the whole workgroup, its loads requested before the W2 rows, so each
+// element's h is one LDS read away instead of an L2 round trip behind the previous ones; a
+// wave reads its elements from the plan in one round and requests the W2 rows of all of them
+// at once.  One barrier after the copy, one before the slot-order sums.
 template <int H, int I, int MT>
 __global__ __launch_bounds__(512) void k_dec_down_mt(DecodeArgs a) {
     using S = DecShape<H, I>;
     using PL = DecPlan<H, MOE_DECODE_MAX_M>;
     constexpr int SBR = S::SBR2, LPR = S::LPR2, RPS = S::RPS2, STEPS = S::STEPS;
-    constexpr int NWV = 8, NPM = MT * SLOTS, MAXE = (NPM + NWV - 1) / NWV, HD = 2;
+    constexpr int NWV = 8, NPM = MT * SLOTS, MAXE = (NPM + NWV - 1) / NWV;
+    constexpr int HQ = NPM * I / 4, QPT = (HQ + 64 * NWV - 1) / (64 * NWV); // h quads, per thread
     static_assert(MAXE <= 64 && MT * DEC_ROWS <= 64 * NWV, "elements in one register, one output per thread");
+    static_assert(I % 32 == 0 && (I / 4) % 8 == 0, "h rows of whole 32-element chunks");
     __shared__ float part[NPM][DEC_ROWS];
+    __shared__ __attribute__((aligned(16))) float hl[NPM * I];
     const PL *P = reinterpret_cast<const PL *>(a.plan);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n0 = blockIdx.x * DEC_ROWS;
+    // the h rows of the M * 9 pairs (those of dropped pairs are copied and never read)
+    const int nq = a.M * SLOTS * (I / 4);
+    u32x4 hq[QPT];
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+        const int qi = min(tid + 64 * NWV * i, nq - 1); // past the end: a valid re-read, not stored
+        hq[i] = ldg<u32x4>(a.hbuf + 4 * (size_t)qi);
+    }
     float yres = 0.f;
     uint32_t vt = 0u;
     if (tid < a.M * DEC_ROWS) {
@@ -530,18 +543,11 @@ __global__ __launch_bounds__(512) void k_dec_down_mt(DecodeArgs a) {
     }
     const int ne = nv > wv ? (nv - wv + NWV - 1) / NWV : 0;
     const int gsb = lane % LPR, rr = lane / LPR, sb = gsb >> 3, ib = gsb & 7;
+    // W2 rows of every element (past the last one: a valid re-read), requested after the h
+    // loads: loads complete in order, so the copy below waits for h only
+    u32x4 qs[MAXE][STEPS];
+    u32x2 hd[MAXE][STEPS];
     if (ne > 0) {
-        // h of the first HD elements, then W2 rows of every element (past the last one: a valid
-        // re-read): loads complete in order, so element k waits only for its own W2 rows and
-        // what came before them, and its products overlap the later elements' W2 stream
-        int qe[MAXE];
-#pragma unroll
-        for (int k = 0; k < MAXE; ++k) qe[k] = __builtin_amdgcn_readlane(eq, min(k, ne - 1));
-        float hv[HD][32];
-#pragma unroll
-        for (int j = 0; j < HD; ++j) load32(a.hbuf + (size_t)qe[min(j, MAXE - 1)] * I + 32 * gsb, hv[j]);
-        u32x4 qs[MAXE][STEPS];
-        u32x2 hd[MAXE][STEPS];
 #pragma unroll
         for (int k = 0; k < MAXE; ++k) {
             const int e = __builtin_amdgcn_readlane(ee, min(k, ne - 1));
@@ -553,25 +559,47 @@ __global__ __launch_bounds__(512) void k_dec_down_mt(DecodeArgs a) {
                 hd[k][st] = ldg<u32x2>(W2 + split_hdr<H, SBR>(row, sb));
             }
         }
+    }
+    // quad qo of chunk c of a row stored at position qo ^ ((c >> 1) & 7) of the chunk: the
+    // lanes of a W2 row, which read the same quad of chunks 0, 1, ..., then hit different bank
+    // groups
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+        const int qi = tid + 64 * NWV * i;
+        const int cb = qi / 8, c = cb % (I / 32), qo = qi % 8; // chunk of the block, of the row; quad
+        if (QPT * 64 * NWV == HQ || qi < nq)
+            *reinterpret_cast<u32x4 *>(hl + 32 * cb + 4 * (qo ^ ((c >> 1) & 7))) = hq[i];
+    }
+    lds_barrier();
+    if (ne > 0) {
 #pragma unroll
         for (int k = 0; k < MAXE; ++k) {
             if (k < ne) {
-                const int q = qe[k];
+                const int q = __builtin_amdgcn_readlane(eq, k);
+                // the lane's 32 h values: chunk gsb of the pair's row
+                float hr[32];
+                const float *hp = hl + (size_t)q * I + 32 * gsb;
+                const int sw = (gsb >> 1) & 7;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const f32x4 v = *reinterpret_cast<const f32x4 *>(hp + 4 * (i ^ sw));
+#pragma unroll
+                    for (int e4 = 0; e4 < 4; ++e4) hr[4 * i + e4] = v[e4];
+                }
                 float hs = 0.f;
 #pragma unroll
-                for (int i = 0; i < 32; ++i) hs += hv[k % HD][i];
+                for (int i = 0; i < 32; ++i) hs += hr[i];
                 const float wq = a.c * __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ew), k));
 #pragma unroll
                 for (int st = 0; st < STEPS; ++st) {
                     uint32_t kv[8];
 #pragma unroll
                     for (int d = 0; d < 4; ++d) kv_biased8(qs[k][st][d], kv[2 * d], kv[2 * d + 1]);
-                    float d = sub_scale(hd[k][st], ib) * subblock_dot(kv, hv[k % HD], hs);
+                    float d = sub_scale(hd[k][st], ib) * subblock_dot(kv, hr, hs);
                     d = group_sum<LPR>(d);
                     if (gsb == 0) part[q][st * RPS + rr] = wq * d;
                 }
             }
-            if (k + HD < MAXE) load32(a.hbuf + (size_t)qe[k + HD] * I + 32 * gsb, hv[k % HD]);
         }
     }
     __syncthreads();
