@@ -492,124 +492,116 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_mt(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------- down, 2 <= M <= 8
-// Eight waves per workgroup of 8 output rows.  Every valid (token, slot) pair is one element:
-// the element's expert's W2 rows against the pair's h, times c * w, into LDS.  The plan block
-// lists the valid pairs in ascending order, and they are dealt to the waves in turn, so the
-// shared expert's M pairs -- and any two tokens' shared routed expert -- go to different
-// waves (repeated W2 rows are L2 hits).  The h of every pair (M * 9 rows of I, at most 144 KB)
-// is copied into LDS by the whole workgroup, its loads requested before the W2 rows, so each
-// element's h is one LDS read away instead of an L2 round trip behind the previous ones; a
-// wave reads its elements from the plan in one round and requests the W2 rows of all of them
-// at once.  One barrier after the copy, one before the slot-order sums.
+// Token-major: workgroup (t, b) writes output rows b*R .. b*R + R-1 (R = 8 * MT) of token t.
+// Its units are (k-th valid slot of t, 8-row block j of the R): the slot's expert's W2 rows
+// against the pair's h, times c * w, into LDS; units are dealt to the eight waves in turn and
+// a wave requests the W2 rows of all its units at once.  The token's 9 h rows are quantized
+// into int8 planes in LDS, one 32-element chunk per lane, exactly as gate/up stages its
+// activations (their loads issued before the W2 rows), so a sub-block dot is 16
+// v_dot4_i32_i8.  The slot sums then run in slot order with the residual.  Workgroup index
+// t * NRB + b: with NRB a multiple of 8 every token's copy of row block b sits on one XCD, so
+// the W2 rows of an expert two tokens share (the shared expert's always) are read from HBM
+// once and are L2 hits for the other tokens.
 template <int H, int I, int MT>
 __global__ __launch_bounds__(512) void k_dec_down_mt(DecodeArgs a) {
     using S = DecShape<H, I>;
     using PL = DecPlan<H, MOE_DECODE_MAX_M>;
     constexpr int SBR = S::SBR2, LPR = S::LPR2, RPS = S::RPS2, STEPS = S::STEPS;
-    constexpr int NWV = 8, NPM = MT * SLOTS, MAXE = (NPM + NWV - 1) / NWV;
-    constexpr int HQ = NPM * I / 4, QPT = (HQ + 64 * NWV - 1) / (64 * NWV); // h quads, per thread
-    static_assert(MAXE <= 64 && MT * DEC_ROWS <= 64 * NWV, "elements in one register, one output per thread");
-    static_assert(I % 32 == 0 && (I / 4) % 8 == 0, "h rows of whole 32-element chunks");
-    __shared__ float part[NPM][DEC_ROWS];
-    __shared__ __attribute__((aligned(16))) float hl[NPM * I];
+    constexpr int NWV = 8, R = DEC_ROWS * MT, NRB = H / R, MAXU = (SLOTS * MT + NWV - 1) / NWV;
+    constexpr int CPR = I / 32, NCK = SLOTS * CPR; // h chunks per row, of the token
+    static_assert(I % 32 == 0 && CPR == LPR, "one h chunk per W2 sub-block lane");
+    static_assert(NCK <= 64 * NWV && R <= 64 * NWV && H % R == 0, "one chunk, one output per thread");
+    __shared__ __attribute__((aligned(16))) uint32_t xq[NCK * XQS];
+    __shared__ float xs[NCK];
+    __shared__ float part[SLOTS][R];
     const PL *P = reinterpret_cast<const PL *>(a.plan);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n0 = blockIdx.x * DEC_ROWS;
-    // the h rows of the M * 9 pairs (those of dropped pairs are copied and never read)
-    const int nq = a.M * SLOTS * (I / 4);
-    u32x4 hq[QPT];
+    const int t = (int)blockIdx.x / NRB, n0 = ((int)blockIdx.x % NRB) * R;
+    // chunk tid of the token's 9 h rows (row s chunk c is chunk s * CPR + c), requested first
+    f32x4 hv[8];
+    if (tid < NCK) {
+        const float *src = a.hbuf + (size_t)t * SLOTS * I + 32 * tid;
 #pragma unroll
-    for (int i = 0; i < QPT; ++i) {
-        const int qi = min(tid + 64 * NWV * i, nq - 1); // past the end: a valid re-read, not stored
-        hq[i] = ldg<u32x4>(a.hbuf + 4 * (size_t)qi);
+        for (int u = 0; u < 8; ++u) hv[u] = ldg<f32x4>(src + 4 * u);
     }
     float yres = 0.f;
-    uint32_t vt = 0u;
-    if (tid < a.M * DEC_ROWS) {
-        const int t = tid / DEC_ROWS;
-        if (a.accumulate) yres = a.y[(size_t)t * H + n0 + tid % DEC_ROWS];
-        vt = P->vt[t];
+    if (a.accumulate && tid < R) yres = a.y[(size_t)t * H + n0 + tid];
+    // the token's valid slots: lane k < nvs holds the k-th one's slot, expert and weight
+    const uint32_t vt = __builtin_amdgcn_readfirstlane(P->vt[t]);
+    const int nvs = __popc(vt), nun = nvs * MT;
+    int ks = 0, ke = 0;
+    float kw = 0.f;
+    if (lane < nvs) {
+        uint32_t m = vt;
+        for (int i = 0; i < lane; ++i) m &= m - 1u;
+        ks = __builtin_ctz(m);
+        ke = (int)a.ids[t * SLOTS + ks];
+        kw = a.w[t * SLOTS + ks];
     }
-    // this wave's elements (lane k: element wv + 8k) and their count
-    const int nv = P->NV;
-    int eq = 0, ee = 0;
-    float ew = 0.f;
-    if (lane < MAXE) {
-        const int el = min(wv + NWV * lane, DEC_MAXP - 1);
-        eq = P->epair[el];
-        ee = P->eexp[el];
-        ew = P->ewt[el];
-    }
-    const int ne = nv > wv ? (nv - wv + NWV - 1) / NWV : 0;
+    const int nu = nun > wv ? (nun - wv + NWV - 1) / NWV : 0; // this wave's units wv, wv + 8, ...
     const int gsb = lane % LPR, rr = lane / LPR, sb = gsb >> 3, ib = gsb & 7;
-    // W2 rows of every element (past the last one: a valid re-read), requested after the h
-    // loads: loads complete in order, so the copy below waits for h only
-    u32x4 qs[MAXE][STEPS];
-    u32x2 hd[MAXE][STEPS];
-    if (ne > 0) {
+    // W2 rows of every unit (past the last one: a valid re-read); loads complete in order, so
+    // the quantization below waits for h only
+    u32x4 qs[MAXU][STEPS];
+    u32x2 hd[MAXU][STEPS];
+    if (nu > 0) {
 #pragma unroll
-        for (int k = 0; k < MAXE; ++k) {
-            const int e = __builtin_amdgcn_readlane(ee, min(k, ne - 1));
+        for (int i = 0; i < MAXU; ++i) {
+            const int j = min(wv + NWV * i, nun - 1);
+            const int e = __builtin_amdgcn_readlane(ke, j / MT);
             const uint8_t *W2 = expert_w(a.L.w2, a.L.s2, a.L.sw2, e, a.E);
 #pragma unroll
             for (int st = 0; st < STEPS; ++st) {
-                const int row = n0 + st * RPS + rr;
-                qs[k][st] = ldg<u32x4>(W2 + split_qs<SBR>(row, sb) + 16 * ib);
-                hd[k][st] = ldg<u32x2>(W2 + split_hdr<H, SBR>(row, sb));
+                const int row = n0 + (j % MT) * DEC_ROWS + st * RPS + rr;
+                qs[i][st] = ldg<u32x4>(W2 + split_qs<SBR>(row, sb) + 16 * ib);
+                hd[i][st] = ldg<u32x2>(W2 + split_hdr<H, SBR>(row, sb));
             }
         }
     }
-    // quad qo of chunk c of a row stored at position qo ^ ((c >> 1) & 7) of the chunk: the
-    // lanes of a W2 row, which read the same quad of chunks 0, 1, ..., then hit different bank
-    // groups
-#pragma unroll
-    for (int i = 0; i < QPT; ++i) {
-        const int qi = tid + 64 * NWV * i;
-        const int cb = qi / 8, c = cb % (I / 32), qo = qi % 8; // chunk of the block, of the row; quad
-        if (QPT * 64 * NWV == HQ || qi < nq)
-            *reinterpret_cast<u32x4 *>(hl + 32 * cb + 4 * (qo ^ ((c >> 1) & 7))) = hq[i];
+    if (tid < NCK) {
+        uint32_t h8[8], l8[8];
+        float sx, ss;
+        quant_chunk(hv, h8, l8, sx, ss);
+        u32x4 *dst = reinterpret_cast<u32x4 *>(&xq[tid * XQS]);
+        dst[0] = u32x4{h8[0], h8[1], h8[2], h8[3]};
+        dst[1] = u32x4{h8[4], h8[5], h8[6], h8[7]};
+        dst[2] = u32x4{l8[0], l8[1], l8[2], l8[3]};
+        dst[3] = u32x4{l8[4], l8[5], l8[6], l8[7]};
+        xs[tid] = sx;
     }
     lds_barrier();
-    if (ne > 0) {
 #pragma unroll
-        for (int k = 0; k < MAXE; ++k) {
-            if (k < ne) {
-                const int q = __builtin_amdgcn_readlane(eq, k);
-                // the lane's 32 h values: chunk gsb of the pair's row
-                float hr[32];
-                const float *hp = hl + (size_t)q * I + 32 * gsb;
-                const int sw = (gsb >> 1) & 7;
+    for (int i = 0; i < MAXU; ++i) {
+        if (i < nu) {
+            const int j = wv + NWV * i, k = j / MT;
+            const int s = __builtin_amdgcn_readlane(ks, k);
+            const float cw = a.c * __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, kw), k));
+            // the pair's chunk gsb as planes
+            const int c = s * CPR + gsb;
+            const u32x4 *cq = reinterpret_cast<const u32x4 *>(&xq[c * XQS]);
+            const u32x4 c0 = cq[0], c1 = cq[1], c2 = cq[2], c3 = cq[3];
+            const uint32_t xh[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+            const uint32_t xl[8] = {c2[0], c2[1], c2[2], c2[3], c3[0], c3[1], c3[2], c3[3]};
+            const float sx = xs[c];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const f32x4 v = *reinterpret_cast<const f32x4 *>(hp + 4 * (i ^ sw));
+            for (int st = 0; st < STEPS; ++st) {
+                uint32_t kv[8];
 #pragma unroll
-                    for (int e4 = 0; e4 < 4; ++e4) hr[4 * i + e4] = v[e4];
-                }
-                float hs = 0.f;
-#pragma unroll
-                for (int i = 0; i < 32; ++i) hs += hr[i];
-                const float wq = a.c * __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ew), k));
-#pragma unroll
-                for (int st = 0; st < STEPS; ++st) {
-                    uint32_t kv[8];
-#pragma unroll
-                    for (int d = 0; d < 4; ++d) kv_biased8(qs[k][st][d], kv[2 * d], kv[2 * d + 1]);
-                    float d = sub_scale(hd[k][st], ib) * subblock_dot(kv, hr, hs);
-                    d = group_sum<LPR>(d);
-                    if (gsb == 0) part[q][st * RPS + rr] = wq * d;
-                }
+                for (int d = 0; d < 4; ++d) kv_signed8(qs[i][st][d], kv[2 * d], kv[2 * d + 1]);
+                float d = sub_scale(hd[i][st], ib) * sx * subblock_idot(kv, xh, xl);
+                d = group_sum<LPR>(d);
+                if (gsb == 0) part[s][(j % MT) * DEC_ROWS + st * RPS + rr] = cw * d;
             }
         }
     }
     __syncthreads();
-    if (tid < a.M * DEC_ROWS) {
-        const int t = tid / DEC_ROWS, r = tid - t * DEC_ROWS;
+    if (tid < R) {
         float sum = 0.f;
 #pragma unroll
         for (int s = 0; s < SLOTS; ++s)
-            if ((vt >> s) & 1u) sum += part[t * SLOTS + s][r];
-        a.y[(size_t)t * H + n0 + r] = yres + sum;
+            if ((vt >> s) & 1u) sum += part[s][tid];
+        a.y[(size_t)t * H + n0 + tid] = yres + sum;
     }
 }
 
@@ -701,9 +693,9 @@ static hipError_t launch_decode_t(const DecodeArgs &a, hipStream_t st, KernelTim
     {
         TimedLaunch tl(T, MOE_K_DECODE_DOWN, st);
         if (a.M == 1) hipLaunchKernelGGL((k_dec_down_m1<H, I>), dim3(H / DEC_ROWS), dim3(64 * SLOTS), 0, st, b);
-        else if (a.M == 2) hipLaunchKernelGGL((k_dec_down_mt<H, I, 2>), dim3(H / DEC_ROWS), dim3(512), 0, st, b);
-        else if (a.M <= 4) hipLaunchKernelGGL((k_dec_down_mt<H, I, 4>), dim3(H / DEC_ROWS), dim3(512), 0, st, b);
-        else hipLaunchKernelGGL((k_dec_down_mt<H, I, 8>), dim3(H / DEC_ROWS), dim3(512), 0, st, b);
+        else if (a.M == 2) hipLaunchKernelGGL((k_dec_down_mt<H, I, 2>), dim3(a.M * H / (DEC_ROWS * 2)), dim3(512), 0, st, b);
+        else if (a.M <= 4) hipLaunchKernelGGL((k_dec_down_mt<H, I, 4>), dim3(a.M * H / (DEC_ROWS * 4)), dim3(512), 0, st, b);
+        else hipLaunchKernelGGL((k_dec_down_mt<H, I, 8>), dim3(a.M * H / (DEC_ROWS * 8)), dim3(512), 0, st, b);
     }
     return hipGetLastError();
 }
