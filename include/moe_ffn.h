@@ -148,7 +148,7 @@ moe_status moe_ffn_route(moe_ctx *ctx, int layer, const float *x, const float *l
                          float *y, uint16_t *ids, float *w, int flags, void *stream);
 
 /* moe_ffn for M <= MOE_DECODE_MAX_M whose h scratch is a static device array of the library
- * (192,256 bytes per GPU, held until the process ends) instead of the context's workspace:
+ * (191,744 bytes per GPU, held until the process ends) instead of the context's workspace:
  * nothing in this call allocates, frees or calls an allocating library routine.  No
  * counterpart in the reference; it is for callers that cannot allocate device memory
  * (work under graph capture, tight serving loops, harnesses that forbid allocation).

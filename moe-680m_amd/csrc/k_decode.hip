@@ -268,133 +268,91 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_m1(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------- prep, 2 <= M <= 8
-// One workgroup of eight waves, once per call; wave t takes token t.  It routes the token
-// when the call passed logits (the top-8 code of moe_router_topk; ids and w are published),
-// or reads its ids; checks its pairs by the pair rule (raising the device flags of invalid
-// ids); and quantizes its activations, one chunk per lane, into int8 planes with its
-// RMSNorm factor.  One LDS round then finds each expert's first valid pair, and wave 0 numbers
-// the selected experts in slot order with the tokens each serves, and lists the valid pairs
-// for the down launch -- the plan block every later workgroup copies instead of building it.
+// One 4-wave workgroup per token t, once per call: it routes the token when the call passed
+// logits (route_wg4, the top-8 of moe_router_topk; ids and w are published) or reads its ids,
+// checks its slots by the pair rule (raising the device flags of invalid ids), and quantizes
+// its activations into the int8 planes, LPC lanes per 32-element chunk, with its RMSNorm
+// factor -- written to the token's rows of the plan block with its valid-slot mask.  The
+// logits are requested before the activations, so the routing waits for them only.
 template <int H>
-struct PrepLds {
-    uint32_t owner[DEC_EMAX]; // first valid pair naming each expert (all ones: none)
-    uint16_t id[DEC_MAXP];
-    float wt[DEC_MAXP];
-    DecPlan<H, MOE_DECODE_MAX_M> G;
-};
+__global__ __launch_bounds__(256) void k_dec_prep(DecodeArgs a) {
+    using PL = DecPlan<H, MOE_DECODE_MAX_M>;
+    constexpr int NCH = H / 32, LPC = 256 / NCH < 8 ? 256 / NCH : 8; // lanes per chunk
+    constexpr int QPL = 8 / LPC;                                      // quads per lane
+    static_assert(NCH * LPC <= 256 && (LPC & (LPC - 1)) == 0 && QPL >= 1 && QPL <= 2, "chunk lanes");
+    __shared__ RouteLds R;
+    __shared__ float s_ss[4];
+    PL *P = reinterpret_cast<PL *>(a.plan);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t = blockIdx.x;
+    const int c = tid / LPC, p = tid % LPC; // chunk, part of it
+    const bool act = c < NCH;
+    const float raw = a.logits ? ldg<float>(a.logits + (size_t)t * a.E + min(64 * wv + lane, a.E - 1)) : 0.f;
+    f32x4 xv[QPL];
+#pragma unroll
+    for (int u = 0; u < QPL; ++u)
+        xv[u] = ldg<f32x4>(a.x + (size_t)t * H + 32 * min(c, NCH - 1) + 4 * (QPL * p + u));
+    int id = 0;
+    float wt = 0.f;
+    if (a.logits) {
+        route_wg4v(raw, a.E, a.renorm, lane, wv, R, id, wt);
+        if (wv == 0 && lane < SLOTS) {
+            a.ids[t * SLOTS + lane] = (uint16_t)id;
+            a.w[t * SLOTS + lane] = wt;
+        }
+    } else if (wv == 0 && lane < SLOTS) {
+        id = (int)a.ids[t * SLOTS + lane];
+    }
+    if (wv == 0) {
+        uint32_t fl;
+        const bool ok = slot_kept(id, lane, a.E, fl);
+        const uint32_t vm = (uint32_t)__ballot(ok) & 0x1FFu;
+        if (lane == 0) {
+            P->vt[t] = vm;
+            if (fl) set_flag(a.flags, fl);
+        }
+    }
+    // the chunk's max |x| over its LPC lanes (a non-finite value counts as +inf), the planes
+    float am = 0.f, ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < QPL; ++u)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+            const float f = fabsf(xv[u][e4]);
+            am = fmaxf(am, f <= 3.4028234e38f ? f : INFINITY);
+            ss = __builtin_fmaf(xv[u][e4], xv[u][e4], ss);
+        }
+#pragma unroll
+    for (int m = 1; m < LPC; m <<= 1) am = fmaxf(am, __shfl_xor(am, m, 64));
+    const float rq = quant_ratio(am);
+    uint32_t xh[QPL], xl[QPL];
+#pragma unroll
+    for (int u = 0; u < QPL; ++u) quant4(xv[u], rq, xh[u], xl[u]);
+    if (act) {
+        uint32_t *dst = &P->xq[t][c * XQS + QPL * p];
+        if constexpr (QPL == 2) {
+            *reinterpret_cast<u32x2 *>(dst) = u32x2{xh[0], xh[1]};
+            *reinterpret_cast<u32x2 *>(dst + 8) = u32x2{xl[0], xl[1]};
+        } else {
+            dst[0] = xh[0];
+            dst[8] = xl[0];
+        }
+        if (p == 0) P->xsc[t][c] = am <= 3.4028234e38f ? am * (1.0f / 127.0f) : __builtin_nanf("");
+    }
+    if (a.rmsnorm) {
+        const float sw = wave_sum(act ? ss : 0.f);
+        if (lane == 0) s_ss[wv] = sw;
+        lds_barrier();
+        if (tid == 0) P->inv[t] = rms_factor(1, ((s_ss[0] + s_ss[1]) + s_ss[2]) + s_ss[3], H);
+    } else if (tid == 0) {
+        P->inv[t] = 1.0f;
+    }
+}
 
 // Pairs before q (q < 128) set in the two-word mask m.
 __device__ __forceinline__ int rank2(uint64_t m0, uint64_t m1, int q) {
     return q < 64 ? __popcll(m0 & ((1ull << q) - 1ull)) : __popcll(m0) + __popcll(m1 & ((1ull << (q - 64)) - 1ull));
-}
-
-template <int H>
-__global__ __launch_bounds__(64 * MOE_DECODE_MAX_M) void k_dec_prep(DecodeArgs a) {
-    constexpr int NCH = H / 32;
-    static_assert(NCH <= 64, "a token's chunks on one wave");
-    __shared__ PrepLds<H> L;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int t = __builtin_amdgcn_readfirstlane(tid >> 6); // this wave's token
-    const int np = a.M * SLOTS;
-    for (int e = tid; e < DEC_EMAX; e += 64 * MOE_DECODE_MAX_M) L.owner[e] = 0xFFFFFFFFu;
-    for (int u = tid; u < DEC_MAXP; u += 64 * MOE_DECODE_MAX_M) L.G.tmask[u] = 0u;
-    int id = 0;
-    bool ok = false;
-    if (t < a.M) {
-        // this lane's chunk of the token's activations, requested first
-        const int c = min(lane, NCH - 1);
-        f32x4 xv[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) xv[u] = ldg<f32x4>(a.x + (size_t)t * H + 32 * c + 4 * u);
-        float wt = 0.f;
-        if (a.logits) {
-            route_wave<4>(a.logits + (size_t)t * a.E, a.E, a.renorm, lane, id, wt);
-            if (lane < SLOTS) {
-                a.ids[t * SLOTS + lane] = (uint16_t)id;
-                a.w[t * SLOTS + lane] = wt;
-            }
-        } else if (lane < SLOTS) {
-            id = (int)a.ids[t * SLOTS + lane];
-            wt = a.w[t * SLOTS + lane];
-        }
-        uint32_t fl;
-        ok = slot_kept(id, lane, a.E, fl);
-        const uint32_t vm = (uint32_t)__ballot(ok) & 0x1FFu;
-        if (lane < SLOTS) {
-            L.id[t * SLOTS + lane] = (uint16_t)id;
-            L.wt[t * SLOTS + lane] = wt;
-        }
-        // the activations as int8 planes, and the token's RMSNorm factor
-        uint32_t xh[8], xl[8];
-        float sx, ss;
-        quant_chunk(xv, xh, xl, sx, ss);
-        if (lane < NCH) {
-            u32x4 *dst = reinterpret_cast<u32x4 *>(&L.G.xq[t][lane * XQS]);
-            dst[0] = u32x4{xh[0], xh[1], xh[2], xh[3]};
-            dst[1] = u32x4{xh[4], xh[5], xh[6], xh[7]};
-            dst[2] = u32x4{xl[0], xl[1], xl[2], xl[3]};
-            dst[3] = u32x4{xl[4], xl[5], xl[6], xl[7]};
-            L.G.xsc[t][lane] = sx;
-        }
-        const float inv = rms_factor(a.rmsnorm, wave_sum(lane < NCH ? ss : 0.f), H);
-        if (lane == 0) {
-            L.G.inv[t] = inv;
-            L.G.vt[t] = vm;
-            if (fl) set_flag(a.flags, fl);
-        }
-    }
-    __syncthreads();
-    if (ok) atomicMin(&L.owner[id], (uint32_t)(t * SLOTS + lane));
-    __syncthreads();
-    if (t == 0) {
-        // pairs q = lane, lane + 64: validity, and whether q is its expert's first valid pair
-        int idq[2];
-        bool vq[2], own[2];
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int q = lane + 64 * r;
-            vq[r] = q < np && ((L.G.vt[min(q / SLOTS, MOE_DECODE_MAX_M - 1)] >> (q % SLOTS)) & 1u);
-            idq[r] = vq[r] ? (int)L.id[q] : 0;
-        }
-        uint32_t ow[2];
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            ow[r] = vq[r] ? L.owner[idq[r]] : 0u;
-            own[r] = vq[r] && ow[r] == (uint32_t)(lane + 64 * r);
-        }
-        const uint64_t om0 = __ballot(own[0]), om1 = __ballot(own[1]);
-        const uint64_t vb0 = __ballot(vq[0]), vb1 = __ballot(vq[1]);
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            if (!vq[r]) continue;
-            const int q = lane + 64 * r, tq = q / SLOTS;
-            const int u = rank2(om0, om1, (int)ow[r]); // the slot-order number of q's expert
-            atomicOr(&L.G.tmask[u], 1u << tq);
-            L.G.tpair[u][tq] = (uint8_t)q;
-            if (own[r]) L.G.uexp[u] = idq[r];
-            const int k = rank2(vb0, vb1, q); // q's place among the valid pairs
-            L.G.epair[k] = (uint8_t)q;
-            L.G.eexp[k] = (uint16_t)idq[r];
-            L.G.ewt[k] = L.wt[q];
-        }
-        if (lane == 0) {
-            L.G.U = __popcll(om0) + __popcll(om1);
-            L.G.NV = __popcll(vb0) + __popcll(vb1);
-        }
-    }
-    __syncthreads();
-    // the block out: the head, then the M token rows of the planes and of the scales
-    const uint8_t *src = reinterpret_cast<const uint8_t *>(&L.G);
-    uint8_t *dst = reinterpret_cast<uint8_t *>(a.plan);
-    constexpr int XQR = NCH * XQS * 4, XSR = NCH * 4;
-    constexpr size_t XSO = DEC_PLAN_HEAD + (size_t)MOE_DECODE_MAX_M * XQR;
-    constexpr int NT = 64 * MOE_DECODE_MAX_M;
-    for (int i = 16 * tid; i < (int)DEC_PLAN_HEAD; i += 16 * NT)
-        *reinterpret_cast<u32x4 *>(dst + i) = *reinterpret_cast<const u32x4 *>(src + i);
-    for (int i = 16 * tid; i < a.M * XQR; i += 16 * NT)
-        *reinterpret_cast<u32x4 *>(dst + DEC_PLAN_HEAD + i) = *reinterpret_cast<const u32x4 *>(src + DEC_PLAN_HEAD + i);
-    for (int i = 16 * tid; i < a.M * XSR; i += 16 * NT)
-        *reinterpret_cast<u32x4 *>(dst + XSO + i) = *reinterpret_cast<const u32x4 *>(src + XSO + i);
 }
 
 // ---------------------------------------------------------------- gate/up, 2 <= M <= 8
@@ -406,39 +364,80 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_mt(DecodeArgs a) {
     constexpr int LPR = S::LPR, RPS = S::RPS, SPE = S::SPE, NCH = S::NCH;
     constexpr int G = 4;
     constexpr int XQR = NCH * XQS * 4, XSR = NCH * 4;
-    constexpr int PLB = (int)DEC_PLAN_HEAD + MT * (XQR + XSR); // plan bytes this launch copies
-    constexpr int CPT = (PLB / 16 + 255) / 256;                  // 16-byte pieces per thread
+    constexpr int PLB = 8 * MOE_DECODE_MAX_M + MT * (XQR + XSR); // plan bytes this launch copies
+    constexpr int CPT = (PLB / 16 + 255) / 256;                     // 16-byte pieces per thread
     __shared__ DecPlan<H, MT> L;
+    __shared__ uint32_t owner[DEC_EMAX]; // first valid pair naming each expert (all ones: none)
+    __shared__ uint16_t pid[DEC_MAXP];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int gw = (int)blockIdx.x * 4 + wv, NW = (int)gridDim.x * 4;
+    const int np = a.M * SLOTS;
+    static_assert(DEC_MAXP <= 256, "one pair per thread");
     {
-        // the head, the M rows of planes and the M rows of scales (global rows are
-        // MOE_DECODE_MAX_M apart, local ones MT): all loads in flight, then the stores
+        // the tokens' factors and valid-slot masks, the M rows of planes and the M rows of
+        // scales (global rows are MOE_DECODE_MAX_M apart, local ones MT), and the pairs' ids:
+        // all loads in flight, then the stores
+        using LP = DecPlan<H, MT>;
+        constexpr int H0 = (int)offsetof(LP, inv), HL = (int)offsetof(LP, uexp) - H0;
+        static_assert(H0 % 16 == 0 && HL == 8 * MOE_DECODE_MAX_M, "head rows of whole 16-byte pieces");
         const uint8_t *src = reinterpret_cast<const uint8_t *>(a.plan);
         uint8_t *dst = reinterpret_cast<uint8_t *>(&L);
-        const int nq = (int)DEC_PLAN_HEAD / 16 + a.M * (XQR + XSR) / 16;
+        const int nq = HL / 16 + a.M * (XQR + XSR) / 16;
         u32x4 cv[CPT];
         int co[CPT];
 #pragma unroll
         for (int j = 0; j < CPT; ++j) {
             const int k = min(tid + 256 * j, nq - 1);
             int gi, li; // byte offsets
-            if (k < (int)DEC_PLAN_HEAD / 16) {
-                gi = li = 16 * k;
-            } else if (k < (int)DEC_PLAN_HEAD / 16 + a.M * XQR / 16) {
-                gi = li = 16 * k;
+            if (k < HL / 16) {
+                gi = li = H0 + 16 * k;
+            } else if (k < HL / 16 + a.M * XQR / 16) {
+                gi = li = (int)DEC_PLAN_HEAD + 16 * k - HL;
             } else {
-                const int r = 16 * k - (int)DEC_PLAN_HEAD - a.M * XQR;
+                const int r = 16 * k - HL - a.M * XQR;
                 gi = (int)DEC_PLAN_HEAD + MOE_DECODE_MAX_M * XQR + r;
                 li = (int)DEC_PLAN_HEAD + MT * XQR + r;
             }
             co[j] = tid + 256 * j < nq ? li : -1;
             cv[j] = ldg<u32x4>(src + gi);
         }
+        const int idq = tid < np ? (int)a.ids[tid] : 0;
+        for (int e = tid; e < DEC_EMAX; e += 256) owner[e] = 0xFFFFFFFFu;
+        if (tid < DEC_MAXP) L.tmask[tid] = 0u;
 #pragma unroll
         for (int j = 0; j < CPT; ++j)
             if (co[j] >= 0) *reinterpret_cast<u32x4 *>(dst + co[j]) = cv[j];
+        if (tid < np) pid[tid] = (uint16_t)idq;
+    }
+    __syncthreads();
+    // each expert's first valid pair, then wave 0 numbers the selected experts in slot order
+    // with the tokens each serves and their pairs
+    if (tid < np && ((L.vt[tid / SLOTS] >> (tid % SLOTS)) & 1u)) atomicMin(&owner[pid[tid]], (uint32_t)tid);
+    __syncthreads();
+    if (wv == 0) {
+        int idr[2];
+        bool vq[2], own[2];
+        uint32_t ow[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int q = lane + 64 * r;
+            vq[r] = q < np && ((L.vt[min(q / SLOTS, MT - 1)] >> (q % SLOTS)) & 1u);
+            idr[r] = vq[r] ? (int)pid[q] : 0;
+            ow[r] = vq[r] ? owner[idr[r]] : 0u;
+            own[r] = vq[r] && ow[r] == (uint32_t)q;
+        }
+        const uint64_t om0 = __ballot(own[0]), om1 = __ballot(own[1]);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            if (!vq[r]) continue;
+            const int q = lane + 64 * r, tq = q / SLOTS;
+            const int u = rank2(om0, om1, (int)ow[r]); // the slot-order number of q's expert
+            atomicOr(&L.tmask[u], 1u << tq);
+            L.tpair[u][tq] = (uint8_t)q;
+            if (own[r]) L.uexp[u] = idr[r];
+        }
+        if (lane == 0) L.U = __popcll(om0) + __popcll(om1);
     }
     __syncthreads();
     const int gsb = lane % LPR, rr = lane / LPR, sb = gsb >> 3, ib = gsb & 7;
@@ -676,7 +675,7 @@ static hipError_t launch_decode_t(const DecodeArgs &a, hipStream_t st, KernelTim
     DecodeArgs b = a;
     if (a.M >= 2) {
         TimedLaunch tl(T, MOE_K_DECODE_PREP, st);
-        hipLaunchKernelGGL((k_dec_prep<H>), dim3(1), dim3(64 * MOE_DECODE_MAX_M), 0, st, a);
+        hipLaunchKernelGGL((k_dec_prep<H>), dim3(a.M), dim3(256), 0, st, a);
         b.logits = nullptr;
     }
     {

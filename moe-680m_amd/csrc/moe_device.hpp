@@ -449,10 +449,11 @@ struct RouteLds {
     uint32_t key[4][TOPK], idx[4][TOPK];
     float z[4];
 };
-__device__ __forceinline__ void route_wg4(const float *__restrict__ l, int E, int renorm, int lane, int wv,
-                                          RouteLds &R, int &id, float &wt) {
+// raw: logit 64 * wv + lane, already loaded (any value past E).
+__device__ __forceinline__ void route_wg4v(float raw, int E, int renorm, int lane, int wv, RouteLds &R, int &id,
+                                           float &wt) {
     const int i = 64 * wv + lane;
-    const float kf = (i < E) ? router_key(ldg<float>(l + min(i, E - 1))) : -INFINITY;
+    const float kf = (i < E) ? router_key(raw) : -INFINITY;
     uint32_t o = (i < E) ? ord32(kf) : 0u; // 0 sorts below every real key
     uint32_t mk = 0u, mi = 0u;
 #pragma unroll
@@ -498,6 +499,10 @@ __device__ __forceinline__ void route_wg4(const float *__restrict__ l, int E, in
     for (int r = 0; r < TOPK; ++r) s8 += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), r));
     id = my_id;
     wt = (lane < TOPK) ? e / (renorm ? s8 : Z) : 1.0f;
+}
+__device__ __forceinline__ void route_wg4(const float *__restrict__ l, int E, int renorm, int lane, int wv,
+                                          RouteLds &R, int &id, float &wt) {
+    route_wg4v(ldg<float>(l + min(64 * wv + lane, E - 1)), E, renorm, lane, wv, R, id, wt);
 }
 
 // ---------------------------------------------------------------- expert table

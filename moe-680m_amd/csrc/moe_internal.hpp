@@ -39,28 +39,24 @@ struct DecodeArgs {
 
 constexpr int DEC_MAXP = MOE_DECODE_MAX_M * SLOTS; // (token, slot) pairs of one decode call
 
-// Plan block of the 2 <= M <= 8 decode launches: written once per call by k_dec_prep, copied
-// into LDS by every gate/up workgroup.  The selected experts in slot order (each one's first
-// valid pair ascending), the tokens each serves with their pairs, every token's RMSNorm factor,
-// and the activations as int8 planes with their chunk scales (MT token rows of each).
+// Plan block of the 2 <= M <= 8 decode launches.  In the scratch k_dec_prep writes each
+// token's row: its RMSNorm factor, its valid slots, and its activations as int8 planes with
+// their chunk scales.  Every gate/up workgroup copies those rows into an LDS DecPlan<H, MT>
+// and fills the rest of the head itself: the selected experts in slot order (each one's first
+// valid pair ascending), the tokens each serves and their pairs.
 template <int H, int MT>
 struct DecPlan {
-    int U;                                     // selected experts
-    int NV;                                    // valid pairs
-    int pad_[2];
+    int U;                                     // selected experts (LDS copy only)
+    int pad_[3];
     float inv[MOE_DECODE_MAX_M];               // RMSNorm factor per token
     uint32_t vt[MOE_DECODE_MAX_M];             // valid slots per token (bit s)
-    int uexp[DEC_MAXP];                        // expert id of selected expert u
-    uint32_t tmask[DEC_MAXP];                  // tokens it serves
-    uint8_t tpair[DEC_MAXP][MOE_DECODE_MAX_M]; // ... and each one's pair
-    float ewt[DEC_MAXP];                       // the valid pairs ascending: weight,
-    uint16_t eexp[DEC_MAXP];                   // expert id,
-    uint8_t epair[DEC_MAXP];                   // pair
-    uint8_t pad2_[8];
+    int uexp[DEC_MAXP];                        // expert id of selected expert u (LDS copy only)
+    uint32_t tmask[DEC_MAXP];                  // tokens it serves (LDS copy only)
+    uint8_t tpair[DEC_MAXP][MOE_DECODE_MAX_M]; // ... and each one's pair (LDS copy only)
     uint32_t xq[MT][(H / 32) * XQS]; // int8 planes per token (chunk c at XQS * c)
     float xsc[MT][H / 32];           // chunk scales
 };
-constexpr size_t DEC_PLAN_HEAD = 16 + 8 * MOE_DECODE_MAX_M + 8 * DEC_MAXP + DEC_MAXP * MOE_DECODE_MAX_M + 7 * DEC_MAXP + 8;
+constexpr size_t DEC_PLAN_HEAD = 16 + 8 * MOE_DECODE_MAX_M + 8 * DEC_MAXP + DEC_MAXP * MOE_DECODE_MAX_M;
 static_assert(DEC_PLAN_HEAD % 16 == 0, "plan rows start 16-byte aligned");
 constexpr size_t DEC_MAX_H = 2048; // the largest hidden size the decode kernels are built for
 // Floats of the decode path's scratch: h [9 * MOE_DECODE_MAX_M][I] f32, then the plan block.

@@ -5,7 +5,7 @@
 // context allocated).  No counterpart in the reference.
 //
 // `scratch` holds the decode path's h values, [9 * MOE_DECODE_MAX_M][inter <= 512] f32, and
-// the plan block of its 2 <= M <= 8 launches (hidden <= 2048): 192,256 bytes; each GPU the
+// the plan block of its 2 <= M <= 8 launches (hidden <= 2048): 191,744 bytes; each GPU the
 // library runs on keeps its own copy until the process ends.  On
 // the host the array's name is only a stand-in for the symbol: host code never passes it to a
 // kernel or a copy, but the device address hipGetSymbolAddress returns for it, looked up once
@@ -26,7 +26,7 @@ constexpr int NOALLOC_MAX_INTER = 512;
 constexpr size_t NOALLOC_FLOATS = decode_hbuf_floats(NOALLOC_MAX_INTER) + decode_plan_floats(DEC_MAX_H);
 constexpr size_t NOALLOC_SCRATCH_BYTES = NOALLOC_FLOATS * sizeof(float);
 static __device__ __align__(256) float scratch[NOALLOC_FLOATS];
-static_assert(NOALLOC_FLOATS * sizeof(float) == 192256, "the size the header and the docs state");
+static_assert(NOALLOC_FLOATS * sizeof(float) == 191744, "the size the header and the docs state");
 
 constexpr int SCRATCH_MAX_DEVICES = 64;
 std::mutex scratch_mu;
