@@ -130,9 +130,9 @@ moe_status moe_bucket_fill(moe_ctx *ctx, const uint16_t *ids, const float *w, in
  * c = 1/9 (MOE_W_REF) or 1 (MOE_W_RENORM).  x and y may be the same buffer.  A slot whose
  * id exceeds n_experts, or repeats an id of an earlier slot of its token, is dropped
  * (MOE_DEVFLAG_BAD_ID / MOE_DEVFLAG_DUP_ID), for every M.
- * M <= 8 runs the decode path, one launch of IQ4_XS GEMVs (activations as two int8 planes
- * per 32-element chunk, f32 accumulation; each selected expert's weights read once however
- * many tokens chose it); larger M runs bucket fill + grouped f16-MFMA GEMMs (f32
+ * M <= 8 runs the decode path, IQ4_XS GEMV launches (activations -- and, at M >= 2, the
+ * down product's h -- as two int8 planes per 32-element chunk, f32 accumulation; each
+ * selected expert's weights read once however many tokens chose it); larger M runs bucket fill + grouped f16-MFMA GEMMs (f32
  * accumulate) + combine.  Replaces record_and_submit_moe (src/inference.rs:663-766): shaders
  * w1_w3_fused(_m1).comp, silu_mult.comp, w2(_scatter)(_m1).comp, moe_combine.comp. */
 moe_status moe_ffn(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids, const float *w,

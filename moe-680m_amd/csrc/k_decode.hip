@@ -6,10 +6,10 @@
 // into the down projection and the combine done as an f16 read-modify-write of the hidden
 // state.  Here one layer is two launches at M = 1 and three at 2 <= M <= 8, with no waits
 // between workgroups:
-//   prep (M >= 2) = one workgroup, once per call: the routing when the call passed logits
-//            (wave t routes token t; ids and w are published), pair validity, the selected
-//            experts in slot order with the tokens each serves, every token's activations as
-//            int8 planes (quant4) and its RMSNorm factor -- a plan block in the scratch.
+//   prep (M >= 2) = one workgroup per token, once per call: its routing when the call passed
+//            logits (ids and w are published), its pair validity, its activations as int8
+//            planes (quant4) and its RMSNorm factor -- the token's row of a plan block in the
+//            scratch.
 //   gate/up = one workgroup per CU at M = 1, two beyond.  A step is one W1 row and the same
 //            W3 row (16 rows at hidden 512) of one selected expert; wave gw of NW takes
 //            steps gw, gw + NW, ..., so every SIMD does an equal share and the shared
@@ -17,14 +17,16 @@
 //            and decoded once per call, whatever the number of tokens sharing it.  At M = 1
 //            every wave routes the token itself (the top-8 code of moe_router_topk, so all
 //            agree bit for bit) and quantizes x into registers: no plan, no barrier, and the
-//            shared expert first in slot order.  Beyond, each workgroup copies the plan block
-//            into LDS and keeps two rounds of loads in flight.  h = silu(g) * u goes to a
+//            shared expert first in slot order.  Beyond, each workgroup copies the tokens'
+//            plan rows into LDS, numbers the selected experts in slot order with the tokens
+//            each serves, and keeps two rounds of loads in flight.  h = silu(g) * u goes to a
 //            [9M][I] f32 scratch.
-//   down    = 8 output rows per workgroup for every token.  At M = 1 wave s takes slot s; beyond,
-//            the valid pairs are dealt to eight waves, each requesting all its W2 rows at once.
-//            Every pair's contribution c * w * (W2 h) goes to LDS and a token's 9 contributions
-//            are summed in slot order (deterministic, no atomics), the residual added in the
-//            same store.
+//   down    = at M = 1, 8 output rows per workgroup, wave s taking slot s; beyond, one
+//            workgroup per (token, 8 * MT output rows), the token's h rows quantized into
+//            int8 planes in LDS and its (slot, 8-row block) units dealt to eight waves, each
+//            requesting all its W2 rows at once.  Every pair's contribution c * w * (W2 h)
+//            goes to LDS and a token's 9 contributions are summed in slot order
+//            (deterministic, no atomics), the residual added in the same store.
 // A single launch with a device-side h exchange between the two roles was built and measured
 // (28 us per M = 1 layer against 23 for two launches): every down item needs every expert's
 // h, so ~256 workgroups poll and read the same few cache lines past their L2, and memory
