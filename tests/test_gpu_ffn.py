@@ -80,7 +80,7 @@ def test_config0_decode_m1(gpu, orc, full):
     assert err <= TOL_DECODE
 
 
-@pytest.mark.parametrize("M", [2, 4, 8])
+@pytest.mark.parametrize("M", [2, 3, 4, 5, 6, 7, 8])
 def test_config3_decode_small_batch(gpu, orc, full, M):
     ctx, layer = full
     log(f"config 3: decode M={M}")
@@ -253,6 +253,43 @@ def test_duplicate_and_bad_ids_decode_batch(gpu, orc, full, route):
     ids_fix[2, 3] = E
     ref0 = orc.moe_ffn(layer.host(), x.cpu().numpy(), ids_fix, w_zero, 1.0 / 9)
     assert normwise_err(ref, ref0) <= 1e-12
+
+
+@pytest.mark.parametrize("acc", [False, True])
+def test_decode_batch_tokens_without_valid_slots(gpu, orc, full, acc):
+    """2 <= M <= 8 with tokens left with few or no valid slots: token 3 names only ids above
+    n_experts (every slot dropped: its output is the residual, or zero), token 5 names one
+    expert in all nine slots (only slot 0 kept), token 6 has every slot valid.  The token-major
+    down launch then has workgroups with no work unit and workgroups with one."""
+    import torch
+    ctx, layer = full
+    M = 7
+    x = gpu.gen_normal(M * H, 3501).view(M, H)
+    ids, w = ctx.router_topk(gpu.gen_logits(M, E, 3502))
+    ids_bad = ids.clone()
+    ids_bad[3, :] = E + 7
+    ids_bad[5, :] = ids_bad[5, 0]
+    y0 = gpu.gen_normal(M * H, 3503).view(M, H)
+    y = y0.clone()
+    torch.cuda.synchronize()
+    ctx.ffn(0, x, ids_bad, w, y=y, accumulate=acc)
+    torch.cuda.synchronize()
+    assert ctx.device_flags() == (gpu.DEVFLAG_BAD_ID | gpu.DEVFLAG_DUP_ID)
+    y_h, y0_h = y.cpu().numpy(), y0.cpu().numpy()
+    ref = orc.moe_ffn(layer.host(), x.cpu().numpy(), ids_bad.cpu().numpy(), w.cpu().numpy(), 1.0 / 9,
+                      1 if acc else 0, y=y0_h if acc else None)
+    if acc:
+        assert normwise_err(y_h - y0_h, ref - y0_h) <= TOL_DECODE
+        assert np.array_equal(y_h[3], y0_h[3])
+    else:
+        assert normwise_err(y_h, ref) <= TOL_DECODE
+        assert not np.any(y_h[3])
+    # the oracle keeps token 5's slot 0 alone
+    w5 = np.zeros((1, 9), dtype=np.float32)
+    w5[0, 0] = w[5, 0].item()
+    ref5 = orc.moe_ffn(layer.host(), x[5:6].cpu().numpy(), ids_bad[5:6].cpu().numpy(), w5, 1.0 / 9)
+    part5 = (y_h[5] - y0_h[5]) if acc else y_h[5]
+    assert normwise_err(part5[None], ref5) <= TOL_DECODE
 
 
 def test_prefill_zero_block_small_activations(gpu, orc):
