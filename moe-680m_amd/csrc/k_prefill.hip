@@ -734,7 +734,7 @@ static hipError_t launch_prefill_t(const BucketArgs &b, const PrefillArgs &a, hi
         TimedLaunch tl(T, MOE_K_BUCKET_FILL, st);
         if (bucket_one_wg(b.M, b.E1)) {
             const dim3 grid((unsigned)(1 + (a.M + BF_THREADS / 64 - 1) / (BF_THREADS / 64)));
-            hipLaunchKernelGGL((k_pf_route_prep<H, true>), grid, dim3(BF_THREADS), bucket_smem(b.E1, true), st, b, a);
+            hipLaunchKernelGGL((k_pf_route_prep<H, true>), grid, dim3(BF_THREADS), bucket_smem_one(b.E1, b.M), st, b, a);
         } else {
             const int nch = (b.M + 63) / 64;
             const size_t smem = bucket_chunk_smem(b.E1);

@@ -152,7 +152,7 @@ hipError_t launch_bucket_fill(const BucketArgs &a, hipStream_t st, KernelTimer *
     if (a.M < 0) return hipSuccess; // M == 0 still writes all-zero ranges
     TimedLaunch tl(T, MOE_K_BUCKET_FILL, st);
     if (bucket_one_wg(a.M, a.E1)) {
-        hipLaunchKernelGGL(k_bucket_fill, dim3(1), dim3(BF_THREADS), bucket_smem(a.E1, true), st, a);
+        hipLaunchKernelGGL(k_bucket_fill, dim3(1), dim3(BF_THREADS), bucket_smem_one(a.E1, a.M), st, a);
     } else {
         const dim3 grid((unsigned)((a.M + 63) / 64));
         const size_t smem = bucket_chunk_smem(a.E1);
