@@ -203,7 +203,9 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_m1(DecodeArgs a) {
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int gw = (int)blockIdx.x * 4 + wv, NW = (int)gridDim.x * 4;
     const int gsb = lane % LPR, rr = lane / LPR, sb = gsb >> 3, ib = gsb & 7;
-    // this lane's chunk of x, requested first
+    // the token's logit of this lane, then this lane's chunk of x (loads complete in order:
+    // the routing waits for the logit only)
+    const float raw = a.logits ? ldg<float>(a.logits + min(64 * wv + lane, a.E - 1)) : 0.f;
     f32x4 xv[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) xv[u] = ldg<f32x4>(a.x + 32 * gsb + 4 * u);
@@ -212,7 +214,7 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_m1(DecodeArgs a) {
     float wt = 1.0f;
     if (a.logits) {
         __shared__ RouteLds R;
-        route_wg4(a.logits, a.E, a.renorm, lane, wv, R, id, wt);
+        route_wg4v(raw, a.E, a.renorm, lane, wv, R, id, wt);
     } else {
         id = lane < SLOTS ? (int)a.ids[lane] : 0;
     }
