@@ -360,8 +360,10 @@ __device__ __forceinline__ int rank2(uint64_t m0, uint64_t m1, int q) {
 }
 
 // ---------------------------------------------------------------- gate/up, 2 <= M <= 8
-// Each workgroup copies the plan block into LDS (one round of loads), then each wave runs its
-// steps with two rounds of G steps' loads in flight.
+// Each workgroup copies the tokens' rows of the plan block and the pairs' ids into LDS (one
+// round of loads), numbers the selected experts in slot order with the tokens each serves
+// (k_dec_prep left that to it, so no prep workgroup waits for another), then each wave runs
+// its steps with two rounds of G steps' loads in flight.
 template <int H, int I, int MT>
 __global__ __launch_bounds__(256) void k_dec_gate_up_mt(DecodeArgs a) {
     using S = GuShape<H, I>;
