@@ -233,8 +233,8 @@ hipError_t launch_repack_split(const void *src, uint64_t src_stride, const void 
     return hipGetLastError();
 }
 
-// One workgroup: thread 0 swaps the flags out; after an expired decode-stack wait, all
-// threads zero the stack's control words and exchange sets (an error path: its speed does not
+// One workgroup: thread 0 swaps the flags out; after an expired decode-stack wait, thread 0
+// clears the abort word and all threads zero the stack's control words and exchange sets (an error path: its speed does not
 // matter, and the usual call only reads and clears one word).
 __global__ __launch_bounds__(1024) void k_flags_take(uint32_t *flags, uint32_t *dst, u32x4 *stack,
                                                      uint64_t stack_quads) {
@@ -246,6 +246,10 @@ __global__ __launch_bounds__(1024) void k_flags_take(uint32_t *flags, uint32_t *
         s_v = v;
     }
     __syncthreads();
+    // the abort word (flags[1]) goes too: the control words restart the epoch at 0, and an
+    // abort tag left from a launch at epoch 0 would otherwise match the next epoch-0 launch
+    if ((s_v & MOE_DEVFLAG_TIMEOUT) && threadIdx.x == 0)
+        __hip_atomic_store((MOE_GLOBAL uint32_t *)(flags + 1), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (s_v & MOE_DEVFLAG_TIMEOUT)
         for (uint64_t q = threadIdx.x; q < stack_quads; q += blockDim.x)
             *(MOE_GLOBAL u32x4 *)(stack + q) = u32x4{0u, 0u, 0u, 0u};

@@ -705,20 +705,23 @@ __global__ __launch_bounds__(256) void k_pf_combine(PrefillArgs a) {
         u32x4 q[SLOTS];
         float f[SLOTS];
 #pragma unroll
-        for (int s = 0; s < SLOTS; ++s) { // all loads first; dropped slots read slot 0 and add 0
+        for (int s = 0; s < SLOTS; ++s) { // all loads first; a dropped slot loads row 0, unused
             const uint32_t p = ps[s] != 0xFFFFFFFFu ? ps[s] : 0u;
             q[s] = ldg<u32x4>(a.part + (size_t)p * H + 8 * c8);
-            f[s] = ps[s] != 0xFFFFFFFFu ? __builtin_amdgcn_ldexpf(1.0f, -(int)a.pexp[(size_t)p * (H / 32) + c8 / 4]) : 0.0f;
+            f[s] = __builtin_amdgcn_ldexpf(1.0f, -(int)a.pexp[(size_t)p * (H / 32) + c8 / 4]);
         }
         f32x4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
 #pragma unroll
-        for (int s = 0; s < SLOTS; ++s)
+        for (int s = 0; s < SLOTS; ++s) {
+            // a dropped slot adds nothing (not 0 times row 0, which may be non-finite or stale)
+            const bool on = ps[s] != 0xFFFFFFFFu;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const f16x2 h2 = __builtin_bit_cast(f16x2, (uint32_t)q[s][j]);
-                lo[j] += (float)h2[0] * f[s];
-                hi[j] += (float)h2[1] * f[s];
+                lo[j] = on ? lo[j] + (float)h2[0] * f[s] : lo[j];
+                hi[j] = on ? hi[j] + (float)h2[1] * f[s] : hi[j];
             }
+        }
         float *yb = a.y + (size_t)t * H + 32 * (c8 / 4) + 4 * (c8 % 4);
         f32x4 *y0 = reinterpret_cast<f32x4 *>(yb), *y1 = reinterpret_cast<f32x4 *>(yb + 16);
         const f32x4 b0 = a.accumulate ? *y0 : f32x4{0, 0, 0, 0};

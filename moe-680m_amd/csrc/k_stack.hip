@@ -109,8 +109,9 @@ typedef volatile __attribute__((address_space(3))) int lds_flag;
 
 // Expiry of a bounded wait: the sticky TIMEOUT flag, the launch's abort word (every other
 // waiter stops at its next check) and this workgroup's own abort flag.  The abort word holds
-// the tag of the launch that raised it (atag, from the launch epoch), so a later launch never
-// mistakes an earlier launch's abort for its own and nothing has to clear it.
+// the tag of the launch that raised it (atag, from the launch epoch), so a later launch of a
+// different epoch never mistakes an earlier launch's abort for its own.  A recovery restarts
+// the epoch at 0, so it clears the abort word too (moe_device_flags, k_flags_take).
 __device__ __forceinline__ void stack_abort(uint32_t *flags, uint32_t atag, lds_flag *s_abort) {
     set_flag(flags, MOE_DEVFLAG_TIMEOUT);
     __hip_atomic_store((MOE_GLOBAL uint32_t *)(flags + 1), atag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -199,6 +199,10 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
     c->ncu = ncu;
     if (stack_occupancy(H, I, &per_cu) == hipSuccess)
         c->stack_ok = (per_cu >= 1 && (long)per_cu * ncu >= stack_blocks(H) && E <= 256) ? 1 : 0;
+    // moe_ffn_noalloc's static scratch: its device address looked up now, with the device
+    // current, so that entry point never makes the lookup itself (a failure here is not
+    // fatal: that entry point retries and reports it)
+    (void)noalloc_prepare(device);
     *out = c;
     return ok();
 }
@@ -557,9 +561,11 @@ moe_status moe_device_flags(moe_ctx *ctx, void *stream, uint32_t *flags) {
     uint32_t v = 0;
     he = hipMemcpy(&v, ctx->flags, 4, hipMemcpyDeviceToHost);
     if (he != hipSuccess) return hip_fail(he, "moe_device_flags: hipMemcpy");
-    he = hipMemset(ctx->flags, 0, 4);
     // after an expired wait the decode stack's control words and exchange sets may be in any
-    // state (a launch that saw one does not advance them reliably): start them over
+    // state (a launch that saw one does not advance them reliably): start them over, and
+    // clear the abort word (flags[1]) with them -- the epoch restarts at 0, and the tag of an
+    // aborted epoch-0 launch would match the next epoch-0 launch
+    he = hipMemset(ctx->flags, 0, (v & MOE_DEVFLAG_TIMEOUT) ? 8 : 4);
     if (he == hipSuccess && (v & MOE_DEVFLAG_TIMEOUT)) he = hipMemset(ctx->xtag, 0, ctx->xtag_words * 4);
     if (he == hipSuccess) he = hipDeviceSynchronize();
     if (he != hipSuccess) return hip_fail(he, "moe_device_flags: clearing");

@@ -210,6 +210,9 @@ namespace moe {
 moe_status ffn_with_scratch(const char *fn, moe_ctx *ctx, int layer, const float *x, const uint16_t *ids,
                             const float *w, int M, float *y, int flags, void *stream, float *hbuf);
 int ctx_device(const moe_ctx *ctx);
+// moe_ffn_noalloc's set-up on `device` (current): the device address of its static scratch,
+// looked up once per device and kept.
+hipError_t noalloc_prepare(int device);
 int ctx_inter(const moe_ctx *ctx);
 // Sets the calling thread's moe_last_error message and returns st.
 moe_status set_error(moe_status st, const char *msg);

@@ -9,7 +9,9 @@
 // library runs on keeps its own copy until the process ends.  On
 // the host the array's name is only a stand-in for the symbol: host code never passes it to a
 // kernel or a copy, but the device address hipGetSymbolAddress returns for it, looked up once
-// per device (with that device current) on the first call there and kept in scratch_dev[].
+// per device (with that device current) by moe_create on that device -- so no call of this
+// entry point, the first one under graph capture included, makes the lookup -- and kept in
+// scratch_dev[] (a first call on a device whose lookup failed at moe_create retries it).
 // Every call on a GPU shares that GPU's array; nothing in it needs to start at zero (the
 // launches of a call write every h value and plan word they read), and calls that overlap on one
 // GPU -- on two streams at once -- race.
@@ -51,6 +53,13 @@ hipError_t scratch_for(int device, float **out) {
 }
 
 } // namespace
+
+namespace moe {
+hipError_t noalloc_prepare(int device) {
+    float *p = nullptr;
+    return scratch_for(device, &p);
+}
+} // namespace moe
 
 extern "C" moe_status moe_ffn_noalloc(moe_ctx *ctx, int layer, const float *x, const uint16_t *ids, const float *w,
                                       int M, float *y, int flags, void *stream) {

@@ -2,13 +2,16 @@
 
 Tolerances (normwise, max|y - ref| / max|ref|): decode (M <= 8: activations as two int8
 planes per 32-element chunk, f32 accumulation) 1e-3; prefill (f16 MFMA operands after exact
-power-of-two scaling, f32 accumulate) 5e-3 -- the bounds BASELINE.json states.  BASELINE's
+power-of-two scaling, f32 accumulate) 5e-3 -- the bounds BASELINE.json states.  Beside it the
+elementwise error max |y - ref| / max(|ref|, 1e-3 rms(ref)) is asserted (gpu_util.EW_DECODE,
+EW_PREFILL): both paths' errors are near-uniform in absolute size over the outputs, so it is
+largest on the few outputs near zero, where the 1e-3 rms floor bounds it.  BASELINE's
 configs name the renormalised top-8 (MOE_W_RENORM); both conventions are run.
 """
 import numpy as np
 import pytest
 
-from gpu_util import E, H, I, Layer, log, normwise_err
+from gpu_util import E, H, I, Layer, check_errs, log, normwise_err
 
 pytestmark = pytest.mark.gpu
 
@@ -36,8 +39,12 @@ def run_case(gpu, orc, ctx, layer, M, seed, kind=0, param=0.0, hot=0.0, flags=0,
         xs, ids_h, w_h, y0_h, y_h = xs[subset], ids_h[subset], w_h[subset], y0_h[subset], y_h[subset]
     ref = orc.moe_ffn(layer.host(), xs, ids_h, w_h, c, flags, y=y0_h if flags & 1 else None)
     if flags & 1:  # compare the FFN part, not the residual
-        return normwise_err(y_h - y0_h, ref - y0_h), y
-    return normwise_err(y_h, ref), y
+        got_p, ref_p = y_h - y0_h, ref - y0_h
+    else:
+        got_p, ref_p = y_h, ref
+    # the elementwise bound of the path is asserted here; the normwise one by the caller
+    err = check_errs(got_p, ref_p, M <= 8, assert_normwise=False)
+    return err, y
 
 
 # ---------------------------------------------------------------- small shape, brute force
@@ -207,13 +214,42 @@ def test_duplicate_and_bad_ids_same_at_decode_and_prefill(gpu, orc, full):
     assert f1 == f9 == (gpu.DEVFLAG_BAD_ID | gpu.DEVFLAG_DUP_ID)
     ref = orc.moe_ffn(layer.host(), x[:1].cpu().numpy(), ids_bad[:1].cpu().numpy(), w[:1].cpu().numpy(),
                       1.0 / 9)
-    assert normwise_err(y1.cpu().numpy(), ref) <= TOL_DECODE
-    assert normwise_err(y9[:1].cpu().numpy(), ref) <= TOL_PREFILL
+    check_errs(y1.cpu().numpy(), ref, True)
+    check_errs(y9[:1].cpu().numpy(), ref, False)
     # the oracle drops exactly those slots: the same as zeroing their weights
     w_zero = w[:1].cpu().numpy().copy()
     w_zero[0, 5] = w_zero[0, 7] = 0.0
     ref0 = orc.moe_ffn(layer.host(), x[:1].cpu().numpy(), ids[:1].cpu().numpy(), w_zero, 1.0 / 9)
     assert normwise_err(ref, ref0) <= 1e-12
+
+
+def test_prefill_dropped_slots_skip_nonfinite_row0(gpu, orc, full):
+    """Prefill (M = 16): token 0 routes to expert 0 in slot 0, so its partial output is
+    expert-sorted row 0, and its activations are +inf (that row is non-finite).  Token 1 names
+    one expert twice and an id above n_experts: its dropped slots must add nothing -- not 0
+    times row 0, which would be NaN -- so every token but token 0 still matches the oracle."""
+    import torch
+    ctx, layer = full
+    M = 16
+    x = gpu.gen_normal(M * H, 3601).view(M, H)
+    ids, w = ctx.router_topk(gpu.gen_logits(M, E, 3602))
+    torch.cuda.synchronize()
+    ids_h = ids.cpu().numpy().astype(np.int64)
+    for t in range(M):          # expert 0 only where put below
+        ids_h[t, :8][ids_h[t, :8] == 0] = 255 - t
+    ids_h[0, 0] = 0
+    ids_h[1, 4] = ids_h[1, 1]   # duplicate inside token 1
+    ids_h[1, 6] = E + 5         # out of range
+    ids_bad = torch.from_numpy(ids_h.astype(np.uint16)).cuda()
+    x[0] = float("inf")
+    y = ctx.ffn(0, x, ids_bad, w).clone()
+    torch.cuda.synchronize()
+    assert ctx.device_flags() == (gpu.DEVFLAG_BAD_ID | gpu.DEVFLAG_DUP_ID)
+    y_h = y.cpu().numpy()
+    assert np.isfinite(y_h[1:]).all()
+    ref = orc.moe_ffn(layer.host(), x[1:].cpu().numpy(), ids_h[1:].astype(np.uint16), w[1:].cpu().numpy(),
+                      1.0 / 9)
+    check_errs(y_h[1:], ref, False)
 
 
 @pytest.mark.parametrize("route", [False, True])
@@ -235,7 +271,7 @@ def test_duplicate_and_bad_ids_decode_batch(gpu, orc, full, route):
         assert torch.equal(ids, ids2) and torch.equal(w.view(torch.int32), w2.view(torch.int32))
         assert ctx.device_flags() == 0
         ref = orc.moe_ffn(layer.host(), x.cpu().numpy(), ids.cpu().numpy(), w.cpu().numpy(), 1.0 / 9)
-        assert normwise_err(y.cpu().numpy(), ref) <= TOL_DECODE
+        check_errs(y.cpu().numpy(), ref, True)
         return
     ids_bad = ids.clone()
     ids_bad[0, 5] = ids_bad[0, 2]       # duplicate inside token 0
@@ -245,7 +281,7 @@ def test_duplicate_and_bad_ids_decode_batch(gpu, orc, full, route):
     y = ctx.ffn(0, x, ids_bad, w).clone()
     assert ctx.device_flags() == (gpu.DEVFLAG_BAD_ID | gpu.DEVFLAG_DUP_ID)
     ref = orc.moe_ffn(layer.host(), x.cpu().numpy(), ids_bad.cpu().numpy(), w.cpu().numpy(), 1.0 / 9)
-    assert normwise_err(y.cpu().numpy(), ref) <= TOL_DECODE
+    check_errs(y.cpu().numpy(), ref, True)
     # ... so its slot 8 (the shared id again) is the repeat that is dropped
     w_zero = w.cpu().numpy().copy()
     w_zero[0, 5] = w_zero[0, 7] = w_zero[2, 8] = 0.0
@@ -279,17 +315,17 @@ def test_decode_batch_tokens_without_valid_slots(gpu, orc, full, acc):
     ref = orc.moe_ffn(layer.host(), x.cpu().numpy(), ids_bad.cpu().numpy(), w.cpu().numpy(), 1.0 / 9,
                       1 if acc else 0, y=y0_h if acc else None)
     if acc:
-        assert normwise_err(y_h - y0_h, ref - y0_h) <= TOL_DECODE
+        check_errs(y_h - y0_h, ref - y0_h, True)
         assert np.array_equal(y_h[3], y0_h[3])
     else:
-        assert normwise_err(y_h, ref) <= TOL_DECODE
+        check_errs(y_h, ref, True)
         assert not np.any(y_h[3])
     # the oracle keeps token 5's slot 0 alone
     w5 = np.zeros((1, 9), dtype=np.float32)
     w5[0, 0] = w[5, 0].item()
     ref5 = orc.moe_ffn(layer.host(), x[5:6].cpu().numpy(), ids_bad[5:6].cpu().numpy(), w5, 1.0 / 9)
     part5 = (y_h[5] - y0_h[5]) if acc else y_h[5]
-    assert normwise_err(part5[None], ref5) <= TOL_DECODE
+    check_errs(part5[None], ref5, True)
 
 
 def test_prefill_zero_block_small_activations(gpu, orc):
@@ -320,9 +356,8 @@ def test_prefill_zero_block_small_activations(gpu, orc):
         torch.cuda.synchronize()
         assert torch.isfinite(y).all()
         ref = orc.moe_ffn(layer.host(), x.cpu().numpy(), ids.cpu().numpy(), w.cpu().numpy(), 1.0 / 9)
-        err = normwise_err(y.cpu().numpy(), ref)
-        log(f"zero W3 block, small x: normwise err {err:.3e}")
-        assert err <= TOL_PREFILL
+        log("zero W3 block, small x")
+        check_errs(y.cpu().numpy(), ref, False)
     finally:
         ctx.close()
 
