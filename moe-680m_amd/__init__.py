@@ -36,10 +36,13 @@ STATUS_NAMES = {0: "MOE_OK", 1: "MOE_EINVAL", 2: "MOE_ENOMEM", 3: "MOE_EHIP",
 W_REF, W_RENORM = 0, 1
 FFN_ACCUMULATE, FFN_RMSNORM = 1, 2
 DEVFLAG_BAD_ID, DEVFLAG_DUP_ID, DEVFLAG_TIMEOUT = 1, 2, 4
+# Router gate matrix element types (GGML type ids, include/moe_ffn.h MOE_WG_*).
+WG_F32, WG_F16, WG_IQ4_XS = 0, 1, 23
 
 # Every symbol include/moe_ffn.h declares (checked by the CPU test suite).
 EXPORTS = (
-    "moe_create", "moe_destroy", "moe_bind_layer", "moe_router_topk", "moe_router_gemv_topk", "moe_bucket_fill",
+    "moe_create", "moe_destroy", "moe_bind_layer", "moe_router_topk", "moe_router_gemv_topk",
+    "moe_router_gemv_topk_typed", "moe_bucket_fill",
     "moe_ffn", "moe_ffn_route", "moe_ffn_noalloc", "moe_decode_stack", "moe_dequant_iq4xs", "moe_device_flags",
     "moe_device_flags_async", "moe_stack_spin_limit", "moe_last_error",
     "moe_timing_enable", "moe_timing_read",
@@ -87,6 +90,7 @@ def lib():
         "moe_bind_layer": [vp, i, ctypes.POINTER(_LayerWeights)],
         "moe_router_topk": [vp, vp, i, vp, vp, vp],
         "moe_router_gemv_topk": [vp, vp, vp, i, i, vp, vp, vp, vp],
+        "moe_router_gemv_topk_typed": [vp, vp, i, vp, i, i, vp, vp, vp, vp],
         "moe_bucket_fill": [vp, vp, vp, i, vp, vp, vp, vp],
         "moe_ffn": [vp, i, vp, vp, vp, i, vp, i, vp],
         "moe_ffn_route": [vp, i, vp, vp, i, vp, vp, vp, i, vp],
@@ -207,13 +211,23 @@ class Context:
 
     def router_gemv_topk(self, wg, x, rmsnorm=False, logits=None, ids=None, w=None, want_logits=True,
                          want_ids=True, stream=None):
-        """Router gate GEMV + top-8: wg = IQ4_XS bytes of [n_experts][hidden] (device uint8),
-        x [M][hidden] f32.  Returns (logits or None, ids or None, w or None)."""
+        """Router gate GEMV + top-8 (moe_router_gemv_topk_typed): wg = the [n_experts][hidden]
+        gate matrix on the device, as IQ4_XS bytes (uint8), float32 or float16 -- the element
+        type follows its dtype; x [M][hidden] f32.  Returns (logits or None, ids or None,
+        w or None)."""
         M = x.shape[0]
         if x.shape[-1] != self.hidden:
             raise ValueError("x last dimension must be hidden")
-        if wg.numel() != matrix_bytes(self.hidden, self.n_experts):
-            raise ValueError("wg must hold n_experts x hidden IQ4_XS weights")
+        if wg.dtype == torch.uint8:
+            wtype, want = WG_IQ4_XS, matrix_bytes(self.hidden, self.n_experts)
+        elif wg.dtype == torch.float32:
+            wtype, want = WG_F32, self.n_experts * self.hidden
+        elif wg.dtype == torch.float16:
+            wtype, want = WG_F16, self.n_experts * self.hidden
+        else:
+            raise ValueError(f"gate matrix dtype {wg.dtype}: uint8 (IQ4_XS), float32 or float16")
+        if wg.numel() != want or not wg.is_contiguous():
+            raise ValueError("wg must hold the n_experts x hidden gate matrix, contiguous")
         dev = x.device
         if want_logits and logits is None:
             logits = torch.empty((M, self.n_experts), dtype=torch.float32, device=dev)
@@ -221,8 +235,9 @@ class Context:
             ids = torch.empty((M, SLOTS), dtype=torch.uint16, device=dev)
         if want_ids and w is None:
             w = torch.empty((M, SLOTS), dtype=torch.float32, device=dev)
-        _check(lib().moe_router_gemv_topk(self._h, _ptr(wg), _ptr(x), M, FFN_RMSNORM if rmsnorm else 0,
-                                          _ptr(logits), _ptr(ids), _ptr(w), _stream(stream)))
+        _check(lib().moe_router_gemv_topk_typed(self._h, _ptr(wg), wtype, _ptr(x), M,
+                                                FFN_RMSNORM if rmsnorm else 0, _ptr(logits), _ptr(ids),
+                                                _ptr(w), _stream(stream)))
         return logits, ids, w
 
     def bucket_fill(self, ids, w, stream=None):

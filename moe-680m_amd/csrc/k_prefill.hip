@@ -49,7 +49,6 @@ constexpr int PF_KC = 128;             // K per LDS stage
 constexpr int PF_WAVES = 8;
 constexpr int PF_ND = 32 * PF_WAVES;   // down output rows per workgroup (2 N-tiles per wave)
 
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 // Position, in the stored order, of natural K index k inside a 32-block (and its inverse).

@@ -60,86 +60,182 @@ hipError_t launch_router_topk(const float *logits, int M, int E, int renorm, uin
 }
 
 // ---------------------------------------------------------------- router gate GEMV
-// logits[t][e] = sum_k xin[t][k] * Wg[e][k], xin = x or RMSNorm(x); Wg IQ4_XS [E][H] in the
-// caller's (GGML) layout, rows = experts.  Replaces shaders/router.comp:21-61 (dispatched at
-// src/inference.rs:598-605), whose 64x8 f32 tiles re-dequantized every weight per tile.
-// One wave per (expert row, group of TM tokens: 1, 2 or 4 by M), four waves per workgroup: lane l owns
-// sub-block l of the row (32 weights; H = 2048 is one sub-block per lane), decodes it once
-// into biased codebook bytes and one f32 scale, then for each token takes one f32 dot of 32
-// against x (loaded for all the group's tokens before any is used) and a wave sum.  All f32:
-// the weights are exact, so the logits differ from an f64 sum by f32 rounding only.
+// logits[t][e] = sum_k xin[t][k] * Wg[e][k], xin = x or RMSNorm(x); Wg [E][H], rows = experts,
+// in the caller's buffer as GGML IQ4_XS (136-byte super-blocks), f32 or f16 (the types a GGUF
+// file's ffn_gate_inp comes in: llama.cpp's quantizer keeps that tensor F32 or F16).
+// Replaces shaders/router.comp:21-61 (dispatched at src/inference.rs:598-605), whose 64x8 f32
+// tiles re-dequantized every weight per tile.  One wave per (expert row, group of TM tokens:
+// 1, 2 or 4 by M), four waves per workgroup: lane l owns the 32 weights 32l..32l+31 of the
+// row (H = 2048 is one sub-block per lane) and reads them once -- IQ4_XS: decoded into
+// biased codebook bytes and one f32 scale; f32: eight 16-byte loads; f16: four, converted
+// exactly -- then for each token takes one f32 dot of 32 against x (loaded for all the
+// group's tokens before any is used) and a wave sum.  All f32: the weights are exact, so the
+// logits differ from an f64 sum by f32 rounding only.
+//
+// With FUSE (M <= 8 and ids requested) the same launch also routes: the last workgroup of a
+// token group to finish -- counted on ctr[group] after every wave's agent-scope release of
+// its logits -- takes an agent-scope acquire, routes the group's tokens (one wave each, as
+// k_router_topk, so the ids and weights equal moe_router_topk's of these logits bit for bit)
+// and resets the counter for the next launch.  No workgroup waits on another.
 constexpr int RG_WAVES = 4; // experts per workgroup
 
-template <int H, int RG_TM>
-__global__ __launch_bounds__(64 * RG_WAVES) void k_router_gemv(const uint8_t *__restrict__ wg,
-                                                               const float *__restrict__ x, int M, int E,
-                                                               int rmsnorm, float *__restrict__ logits) {
-    constexpr int NSB = H / 32, SBR = H / QK;
-    static_assert(H % QK == 0 && NSB <= 64, "one sub-block per lane");
-    const int lane = threadIdx.x & 63;
-    const int e = blockIdx.x * RG_WAVES + (int)(threadIdx.x >> 6);
-    const int t0 = blockIdx.y * RG_TM;
-    if (e >= E) return; // whole wave
-    const bool on = lane < NSB;
-    const int sl = on ? lane : 0; // idle lanes (H < 2048) read sub-block 0 and add nothing
-    const uint8_t *blk = wg + ((size_t)e * SBR + sl / 8) * SB_BYTES;
-    const u32x2 hdr = ldg<u32x2>(blk);
-    const int j = sl % 8;
-    uint32_t q[4];
-    {
+struct RouterGemvArgs {
+    const void *wg;
+    const float *x;
+    int M, E, rmsnorm, renorm;
+    float *logits;
+    uint16_t *ids; // FUSE only
+    float *w;
+    uint32_t *ctr; // FUSE only: one zero counter per token group (left zero)
+};
+
+// The lane's 32 weights of row e as f32 (dense types), or its codebook bytes and scale (IQ4_XS).
+template <int H, int WT>
+__device__ __forceinline__ void router_row_weights(const void *wg, int e, int sl, bool on, uint32_t (&kv)[8],
+                                                   float &dl, float (&wf)[32]) {
+    if constexpr (WT == MOE_WG_IQ4_XS) {
+        constexpr int SBR = H / QK;
+        const uint8_t *blk = (const uint8_t *)wg + ((size_t)e * SBR + sl / 8) * SB_BYTES;
+        const u32x2 hdr = ldg<u32x2>(blk);
+        const int j = sl % 8;
         const u32x2 q01 = ldg<u32x2>(blk + 8 + 16 * j), q23 = ldg<u32x2>(blk + 16 + 16 * j);
-        q[0] = q01.x; q[1] = q01.y; q[2] = q23.x; q[3] = q23.y;
-    }
-    float xv[RG_TM][32];
+        const uint32_t q[4] = {q01.x, q01.y, q23.x, q23.y};
 #pragma unroll
-    for (int i = 0; i < RG_TM; ++i) {
-        const int t = t0 + i < M ? t0 + i : M - 1; // rows past M repeat the last; not stored
-        load32(x + (size_t)t * H + 32 * sl, xv[i]);
-    }
-    uint32_t kv[8];
+        for (int d = 0; d < 4; ++d) kv_biased8(q[d], kv[2 * d], kv[2 * d + 1]);
+        dl = on ? sub_scale(hdr, j) : 0.0f;
+    } else if constexpr (WT == MOE_WG_F32) {
+        load32((const float *)wg + (size_t)e * H + 32 * sl, wf);
+        if (!on)
 #pragma unroll
-    for (int d = 0; d < 4; ++d) kv_biased8(q[d], kv[2 * d], kv[2 * d + 1]);
-    const float dl = on ? sub_scale(hdr, j) : 0.0f;
+            for (int k = 0; k < 32; ++k) wf[k] = 0.0f;
+    } else {
+        const _Float16 *src = (const _Float16 *)wg + (size_t)e * H + 32 * sl;
 #pragma unroll
-    for (int i = 0; i < RG_TM; ++i) {
-        float xs = 0.f, ss = 0.f;
+        for (int i = 0; i < 4; ++i) {
+            const u32x4 v = ldg<u32x4>(src + 8 * i);
 #pragma unroll
-        for (int k = 0; k < 32; ++k) {
-            xs += xv[i][k];
-            ss = __builtin_fmaf(xv[i][k], xv[i][k], ss);
+            for (int d = 0; d < 4; ++d) {
+                const f16x2 h2 = __builtin_bit_cast(f16x2, (uint32_t)v[d]);
+                wf[8 * i + 2 * d] = on ? (float)h2[0] : 0.0f;
+                wf[8 * i + 2 * d + 1] = on ? (float)h2[1] : 0.0f;
+            }
         }
-        const float dot = wave_sum(dl * subblock_dot(kv, xv[i], xs));
-        float inv = 1.0f;
-        if (rmsnorm) inv = 1.0f / sqrtf(wave_sum(on ? ss : 0.0f) * (1.0f / (float)H) + 1e-6f);
-        if (lane == 0 && t0 + i < M) logits[(size_t)(t0 + i) * E + e] = dot * inv;
     }
 }
 
-template <int H, int TM>
-static void launch_router_gemv_t(const void *wg, const float *x, int M, int E, int rmsnorm, float *logits,
-                                 hipStream_t st) {
-    const dim3 grid((unsigned)((E + RG_WAVES - 1) / RG_WAVES), (unsigned)((M + TM - 1) / TM));
-    hipLaunchKernelGGL((k_router_gemv<H, TM>), grid, dim3(64 * RG_WAVES), 0, st, (const uint8_t *)wg, x, M, E, rmsnorm,
-                       logits);
+template <int H, int RG_TM, int WT, bool FUSE>
+__global__ __launch_bounds__(64 * RG_WAVES) void k_router_gemv(RouterGemvArgs a) {
+    constexpr int NSB = H / 32;
+    static_assert(H % QK == 0 && NSB <= 64, "one sub-block per lane");
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int e = blockIdx.x * RG_WAVES + wv;
+    const int t0 = blockIdx.y * RG_TM;
+    const int M = a.M, E = a.E;
+    if (e < E) { // whole wave
+        const bool on = lane < NSB;
+        const int sl = on ? lane : 0; // idle lanes (H < 2048) read sub-block 0 and add nothing
+        uint32_t kv[8];
+        float dl = 0.0f, wf[32];
+        router_row_weights<H, WT>(a.wg, e, sl, on, kv, dl, wf);
+        float xv[RG_TM][32];
+#pragma unroll
+        for (int i = 0; i < RG_TM; ++i) {
+            const int t = t0 + i < M ? t0 + i : M - 1; // rows past M repeat the last; not stored
+            load32(a.x + (size_t)t * H + 32 * sl, xv[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < RG_TM; ++i) {
+            float xs = 0.f, ss = 0.f;
+#pragma unroll
+            for (int k = 0; k < 32; ++k) {
+                xs += xv[i][k];
+                ss = __builtin_fmaf(xv[i][k], xv[i][k], ss);
+            }
+            float part;
+            if constexpr (WT == MOE_WG_IQ4_XS) {
+                part = dl * subblock_dot(kv, xv[i], xs);
+            } else {
+                part = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 32; ++k) part = __builtin_fmaf(wf[k], xv[i][k], part);
+            }
+            const float dot = wave_sum(part);
+            float inv = 1.0f;
+            if (a.rmsnorm) inv = 1.0f / sqrtf(wave_sum(on ? ss : 0.0f) * (1.0f / (float)H) + 1e-6f);
+            if (lane == 0 && t0 + i < M) a.logits[(size_t)(t0 + i) * E + e] = dot * inv;
+        }
+    }
+    if constexpr (FUSE) {
+        __shared__ int s_last;
+        // every wave's logits written back to memory before this workgroup is counted
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const uint32_t done = __hip_atomic_fetch_add((MOE_GLOBAL uint32_t *)(a.ctr + blockIdx.y), 1u,
+                                                         __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = done == gridDim.x - 1u;
+        }
+        __syncthreads();
+        if (!s_last) return;
+        // the last workgroup of the group: every other one's logits are visible after this
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        const int t = t0 + wv;
+        if (wv < RG_TM && t < M) {
+            int id;
+            float wt;
+            route_wave<4>(a.logits + (size_t)t * E, E, a.renorm, lane, id, wt);
+            if (lane < SLOTS) {
+                a.ids[(size_t)t * SLOTS + lane] = (uint16_t)id;
+                a.w[(size_t)t * SLOTS + lane] = wt;
+            }
+        }
+        if (threadIdx.x == 0)
+            __hip_atomic_store((MOE_GLOBAL uint32_t *)(a.ctr + blockIdx.y), 0u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+template <int H, int TM, int WT>
+static void launch_router_gemv_t(const RouterGemvArgs &a, bool fuse, hipStream_t st) {
+    const dim3 grid((unsigned)((a.E + RG_WAVES - 1) / RG_WAVES), (unsigned)((a.M + TM - 1) / TM));
+    if (fuse) hipLaunchKernelGGL((k_router_gemv<H, TM, WT, true>), grid, dim3(64 * RG_WAVES), 0, st, a);
+    else hipLaunchKernelGGL((k_router_gemv<H, TM, WT, false>), grid, dim3(64 * RG_WAVES), 0, st, a);
+}
+
+template <int H, int WT>
+static void launch_router_gemv_w(const RouterGemvArgs &a, bool fuse, hipStream_t st) {
+    // a wave's tokens past M repeat the last one: at small M fewer tokens per wave
+    if (a.M == 1) launch_router_gemv_t<H, 1, WT>(a, fuse, st);
+    else if (a.M == 2) launch_router_gemv_t<H, 2, WT>(a, fuse, st);
+    else launch_router_gemv_t<H, 4, WT>(a, fuse, st);
 }
 
 template <int H>
-static void launch_router_gemv_h(const void *wg, const float *x, int M, int E, int rmsnorm, float *logits,
-                                 hipStream_t st) {
-    // a wave's tokens past M repeat the last one: at small M fewer tokens per wave
-    if (M == 1) launch_router_gemv_t<H, 1>(wg, x, M, E, rmsnorm, logits, st);
-    else if (M == 2) launch_router_gemv_t<H, 2>(wg, x, M, E, rmsnorm, logits, st);
-    else launch_router_gemv_t<H, 4>(wg, x, M, E, rmsnorm, logits, st);
+static void launch_router_gemv_h(int wtype, const RouterGemvArgs &a, bool fuse, hipStream_t st) {
+    if (wtype == MOE_WG_IQ4_XS) launch_router_gemv_w<H, MOE_WG_IQ4_XS>(a, fuse, st);
+    else if (wtype == MOE_WG_F32) launch_router_gemv_w<H, MOE_WG_F32>(a, fuse, st);
+    else launch_router_gemv_w<H, MOE_WG_F16>(a, fuse, st);
 }
 
-hipError_t launch_router_gemv(int H, const void *wg, const float *x, int M, int E, int rmsnorm, float *logits,
-                              hipStream_t st, KernelTimer *T) {
+hipError_t launch_router_gemv(int H, int wtype, const void *wg, const float *x, int M, int E, int rmsnorm,
+                              float *logits, int renorm, uint16_t *ids, float *w, uint32_t *ctr, hipStream_t st,
+                              KernelTimer *T) {
     if (M <= 0) return hipSuccess;
     if (H != 2048 && H != 512) return hipErrorInvalidValue;
-    TimedLaunch tl(T, MOE_K_ROUTER_GEMV, st);
-    if (H == 2048) launch_router_gemv_h<2048>(wg, x, M, E, rmsnorm, logits, st);
-    else launch_router_gemv_h<512>(wg, x, M, E, rmsnorm, logits, st);
-    return hipGetLastError();
+    if (wtype != MOE_WG_IQ4_XS && wtype != MOE_WG_F32 && wtype != MOE_WG_F16) return hipErrorInvalidValue;
+    if (E < TOPK || E > 256) return hipErrorInvalidValue;
+    RouterGemvArgs a{wg, x, M, E, rmsnorm, renorm, logits, ids, w, ctr};
+    // one launch for the GEMV and the top-8 when M <= 8 (at most 8 token groups, one counter
+    // each); larger M: the GEMV, then k_router_topk's throughput form
+    const bool fuse = ids && M <= RG_FUSE_MAX_M;
+    {
+        TimedLaunch tl(T, MOE_K_ROUTER_GEMV, st);
+        if (H == 2048) launch_router_gemv_h<2048>(wtype, a, fuse, st);
+        else launch_router_gemv_h<512>(wtype, a, fuse, st);
+    }
+    hipError_t he = hipGetLastError();
+    if (he == hipSuccess && ids && !fuse) he = launch_router_topk(logits, M, E, renorm, ids, w, st, T);
+    return he;
 }
 
 // ---------------------------------------------------------------- bucket fill

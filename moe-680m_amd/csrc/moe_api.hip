@@ -25,7 +25,7 @@ struct moe_ctx {
     uint8_t *spk = nullptr;         // [n_layers][E+1][W1|W3|W2] split layout: the one resident copy
     void *arena = nullptr; // one device allocation, carved below
     size_t arena_bytes = 0;
-    uint32_t *flags = nullptr;
+    uint32_t *flags = nullptr;   // 64 words: [0] sticky flags, [1] stack abort word, FLAG_RG_CTR..
     float *hbuf = nullptr;       // decode path h scratch [72][I]
     _Float16 *xh = nullptr;      // [m_max][H]
     float *xinv = nullptr;       // [m_max]
@@ -283,10 +283,13 @@ moe_status moe_router_topk(moe_ctx *ctx, const float *logits, int M, uint16_t *i
     return ok();
 }
 
-moe_status moe_router_gemv_topk(moe_ctx *ctx, const void *wg, const float *x, int M, int flags, float *logits,
-                                uint16_t *ids, float *w, void *stream) {
+moe_status moe_router_gemv_topk_typed(moe_ctx *ctx, const void *wg, int wg_type, const float *x, int M, int flags,
+                                      float *logits, uint16_t *ids, float *w, void *stream) {
     static const char *fn = "moe_router_gemv_topk";
     if (!ctx) return fail(MOE_EINVAL, "%s: null context", fn);
+    if (wg_type != MOE_WG_IQ4_XS && wg_type != MOE_WG_F32 && wg_type != MOE_WG_F16)
+        return fail(MOE_EUNSUPPORTED, "%s: gate matrix type %d (IQ4_XS %d, F32 %d and F16 %d are read)", fn, wg_type,
+                    MOE_WG_IQ4_XS, MOE_WG_F32, MOE_WG_F16);
     if (M < 0 || M > 65535) return fail(MOE_EINVAL, "%s: M=%d outside 0..65535", fn, M);
     if (flags & ~MOE_FFN_RMSNORM) return fail(MOE_EINVAL, "%s: flags 0x%x (only MOE_FFN_RMSNORM)", fn, flags);
     if (!ids != !w) return fail(MOE_EINVAL, "%s: ids and w must both be given or both be NULL", fn);
@@ -298,13 +301,17 @@ moe_status moe_router_gemv_topk(moe_ctx *ctx, const void *wg, const float *x, in
     if (!aligned16(wg) || !aligned16(x) || ((uintptr_t)logits & 3u) || ((uintptr_t)w & 3u) || ((uintptr_t)ids & 1u))
         return fail(MOE_EINVAL, "%s: misaligned pointer (wg and x need 16 bytes)", fn);
     const hipStream_t st = as_stream(stream);
-    KernelTimer *T = timer_for(ctx, st);
     float *lg = logits ? logits : ctx->logits;
-    const int E = ctx->cfg.n_experts;
-    hipError_t he = launch_router_gemv(ctx->cfg.hidden, wg, x, M, E, (flags & MOE_FFN_RMSNORM) ? 1 : 0, lg, st, T);
-    if (he == hipSuccess && ids) he = launch_router_topk(lg, M, E, ctx->cfg.wmode == MOE_W_RENORM, ids, w, st, T);
+    hipError_t he = launch_router_gemv(ctx->cfg.hidden, wg_type, wg, x, M, ctx->cfg.n_experts,
+                                       (flags & MOE_FFN_RMSNORM) ? 1 : 0, lg, ctx->cfg.wmode == MOE_W_RENORM, ids, w,
+                                       ctx->flags + FLAG_RG_CTR, st, timer_for(ctx, st));
     if (he != hipSuccess) return hip_fail(he, "moe_router_gemv_topk: launch");
     return ok();
+}
+
+moe_status moe_router_gemv_topk(moe_ctx *ctx, const void *wg, const float *x, int M, int flags, float *logits,
+                                uint16_t *ids, float *w, void *stream) {
+    return moe_router_gemv_topk_typed(ctx, wg, MOE_WG_IQ4_XS, x, M, flags, logits, ids, w, stream);
 }
 
 moe_status moe_bucket_fill(moe_ctx *ctx, const uint16_t *ids, const float *w, int M, uint32_t *ranges,

@@ -218,11 +218,8 @@ void orc_rmsnorm(const float *x, int H, double *out) {
 /* Router gate GEMV, restating shaders/router.comp:21-61 (logits = x . Wg, dispatched at
  * src/inference.rs:598-605) with Wg rows = experts (the [out][in] convention of the expert
  * matrices): logits[t][e] = sum_k xin[t][k] * Wg[e][k], xin = x or RMSNorm(x).  f64 sums of
- * exact f32 weights; the output is the f64 value rounded to f32. */
-void orc_router_gemv(const uint8_t *wg, int H, int E, const float *x, int M, int flags, float *logits) {
-    size_t nw = (size_t)E * H;
-    float *W = (float *)malloc(nw * 4);
-    orc_dequant_iq4xs(wg, nw / ORC_QK, W);
+ * the f32 weights W [E][H]; the output is the f64 value rounded to f32. */
+void orc_router_gemv_f32(const float *W, int H, int E, const float *x, int M, int flags, float *logits) {
 #pragma omp parallel
     {
         double *xin = (double *)malloc((size_t)H * sizeof(double));
@@ -236,6 +233,14 @@ void orc_router_gemv(const uint8_t *wg, int H, int E, const float *x, int M, int
         }
         free(xin);
     }
+}
+
+/* The same on an IQ4_XS gate matrix (wg: E*H/256 super-blocks), decoded exactly first. */
+void orc_router_gemv(const uint8_t *wg, int H, int E, const float *x, int M, int flags, float *logits) {
+    size_t nw = (size_t)E * H;
+    float *W = (float *)malloc(nw * 4);
+    orc_dequant_iq4xs(wg, nw / ORC_QK, W);
+    orc_router_gemv_f32(W, H, E, x, M, flags, logits);
     free(W);
 }
 

@@ -90,6 +90,7 @@ void orc_moe_ffn_f32(const orc_layer *L, int H, int I, int E, const float *x, co
 /* Router gate GEMV: logits[t][e] = sum_k xin[t][k] * Wg[e][k] (f64 sum, rounded to f32),
  * xin = flags & ORC_FFN_RMSNORM ? RMSNorm(x_t) : x_t.  wg: IQ4_XS [E][H], rows = experts. */
 void orc_router_gemv(const uint8_t *wg, int H, int E, const float *x, int M, int flags, float *logits);
+void orc_router_gemv_f32(const float *W, int H, int E, const float *x, int M, int flags, float *logits);
 
 /* Single expert on one row, f64 out (for fine-grained tests). */
 void orc_expert_forward(const uint8_t *w1, const uint8_t *w3, const uint8_t *w2, int H, int I,

@@ -39,6 +39,7 @@ def lib():
         L.orc_moe_ffn.argtypes = [vp, i, i, i, vp, vp, vp, i, d, i, vp]
         L.orc_expert_forward.argtypes = [vp, vp, vp, i, i, vp, vp]
         L.orc_router_gemv.argtypes = [vp, i, i, vp, i, i, vp]
+        L.orc_router_gemv_f32.argtypes = [vp, i, i, vp, i, i, vp]
         L.orc_moe_ffn_f32.argtypes = [vp, i, i, i, vp, vp, vp, i, ctypes.c_float, i, vp]
         L.orc_mix64.argtypes = [u64]
         L.orc_mix64.restype = u64
@@ -91,13 +92,20 @@ def router_topk(logits, mode=W_REF):
 
 
 def router_gemv(wg, x, E, flags=0):
-    """logits [M][E] f32 = (x or RMSNorm(x)) . Wg^T; wg: IQ4_XS bytes of [E][H]."""
-    wg = np.ascontiguousarray(wg, dtype=np.uint8)
+    """logits [M][E] f32 = (x or RMSNorm(x)) . Wg^T.  wg: IQ4_XS bytes of [E][H] (uint8), or
+    the matrix [E][H] as float32, or as float16 (widened exactly to float32)."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     M, H = x.shape
-    assert wg.size == E * H // QK * SB_BYTES
     out = np.empty((M, E), dtype=np.float32)
-    lib().orc_router_gemv(_p(wg), H, E, _p(x), M, flags, _p(out))
+    wg = np.asarray(wg)
+    if wg.dtype == np.uint8:
+        wg = np.ascontiguousarray(wg)
+        assert wg.size == E * H // QK * SB_BYTES
+        lib().orc_router_gemv(_p(wg), H, E, _p(x), M, flags, _p(out))
+    else:
+        assert wg.dtype in (np.float32, np.float16) and wg.size == E * H
+        W = np.ascontiguousarray(wg.reshape(E, H), dtype=np.float32)
+        lib().orc_router_gemv_f32(_p(W), H, E, _p(x), M, flags, _p(out))
     return out
 
 

@@ -7,7 +7,7 @@ import numpy as np
 T_U8, T_I8, T_U16, T_I16, T_U32, T_I32, T_F32, T_BOOL, T_STRING, T_ARRAY, T_U64, T_I64, T_F64 = range(13)
 _FMT = {T_U8: "<B", T_I8: "<b", T_U16: "<H", T_I16: "<h", T_U32: "<I", T_I32: "<i", T_F32: "<f",
         T_BOOL: "<?", T_U64: "<Q", T_I64: "<q", T_F64: "<d"}
-IQ4_XS, F16 = 23, 1
+F32, F16, Q8_0, IQ4_XS = 0, 1, 8, 23
 
 
 def _string(s):
@@ -53,8 +53,9 @@ def write_gguf(path, metadata, tensors, alignment=32, version=3, misalign=None):
             f.write(np.asarray(data, dtype=np.uint8).tobytes())
 
 
-def layer_tensors(L, packed, hidden, inter, n_experts, router=None, merged=True):
-    """GGUF tensors of one layer from bytes packed as [n_experts+1][w1|w3|w2] (shared last)."""
+def layer_tensors(L, packed, hidden, inter, n_experts, router=None, merged=True, router_type=IQ4_XS):
+    """GGUF tensors of one layer from bytes packed as [n_experts+1][w1|w3|w2] (shared last).
+    router: IQ4_XS bytes, or (router_type F32 / F16) the [n_experts][hidden] matrix."""
     mb = hidden * inter // 256 * 136
     v = np.asarray(packed, dtype=np.uint8).reshape(n_experts + 1, 3, mb)
     gate, down = [hidden, inter], [inter, hidden]
@@ -64,12 +65,14 @@ def layer_tensors(L, packed, hidden, inter, n_experts, router=None, merged=True)
             out.append((f"blk.{L}.ffn_{stem}_exps.weight", dims + [n_experts], IQ4_XS, v[:n_experts, j].reshape(-1)))
             out.append((f"blk.{L}.ffn_{stem}_shexp.weight", dims, IQ4_XS, v[n_experts, j]))
         if router is not None:
-            out.append((f"blk.{L}.ffn_gate_inp.weight", [hidden, n_experts], IQ4_XS, router))
+            rb = np.ascontiguousarray(router).view(np.uint8).reshape(-1)
+            out.append((f"blk.{L}.ffn_gate_inp.weight", [hidden, n_experts], router_type, rb))
     else:
         for j, (w, dims) in enumerate((("w1", gate), ("w3", gate), ("w2", down))):
             for e in range(n_experts):
                 out.append((f"blk.{L}.experts.{e}.{w}.weight", dims, IQ4_XS, v[e, j]))
             out.append((f"blk.{L}.shared_expert.{w}.weight", dims, IQ4_XS, v[n_experts, j]))
         if router is not None:
-            out.append((f"blk.{L}.ffn_gate.weight", [hidden, n_experts], IQ4_XS, router))
+            rb = np.ascontiguousarray(router).view(np.uint8).reshape(-1)
+            out.append((f"blk.{L}.ffn_gate.weight", [hidden, n_experts], router_type, rb))
     return out

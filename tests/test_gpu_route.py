@@ -94,13 +94,20 @@ def test_bucket_fill_flags_invalid_ids(gpu, ctx):
 
 # ---------------------------------------------------------------- router gate GEMV
 
-def _router_gemv_case(gpu, orc, c, E_, H_, M, seed, rmsnorm):
+def _router_gemv_case(gpu, orc, c, E_, H_, M, seed, rmsnorm, dense=None):
+    """dense: None for an IQ4_XS gate matrix, or np.float32 / np.float16 for an unquantized one."""
     import torch
-    wg = gpu.gen_iq4xs(E_ * H_ // 256, seed)
+    if dense is None:
+        wg = gpu.gen_iq4xs(E_ * H_ // 256, seed)
+        wg_h = None
+    else:
+        wg_h = (np.random.default_rng(seed).standard_normal((E_, H_)) * 0.05).astype(dense)
+        wg = torch.from_numpy(wg_h).cuda()
     x = gpu.gen_normal(M * H_, seed ^ 0x58, 0, 0.0, 1.0).view(M, H_)
     lg, ids, w = c.router_gemv_topk(wg, x, rmsnorm=rmsnorm)
     torch.cuda.synchronize()
-    ref = orc.router_gemv(wg.cpu().numpy(), x.cpu().numpy(), E_, flags=2 if rmsnorm else 0)
+    ref = orc.router_gemv(wg.cpu().numpy() if wg_h is None else wg_h, x.cpu().numpy(), E_,
+                          flags=2 if rmsnorm else 0)
     got = lg.cpu().numpy()
     # f32 sums of exact weights: within 1e-5 of each row's logit scale
     scale = np.maximum(np.abs(ref).max(axis=1, keepdims=True), 1.0)
@@ -134,6 +141,15 @@ def test_router_gemv_matches_oracle(gpu, orc, ctx, ctx_renorm, M, rmsnorm):
     _router_gemv_case(gpu, orc, ctx if M % 2 else ctx_renorm, E, 2048, M, 0x52470000 + M, rmsnorm)
 
 
+@pytest.mark.parametrize("M", [1, 2, 8, 9, 64])
+@pytest.mark.parametrize("dense", [np.float32, np.float16])
+def test_router_gemv_dense_matches_oracle(gpu, orc, ctx, ctx_renorm, M, dense):
+    """Unquantized gate matrices (a GGUF ffn_gate_inp as llama.cpp leaves it): M <= 8 routes in
+    the GEMV's own launch, M > 8 in a second one."""
+    log(f"router gemv dense {np.dtype(dense).name} E={E} H=2048 M={M}")
+    _router_gemv_case(gpu, orc, ctx if M % 2 else ctx_renorm, E, 2048, M, 0x52480000 + M, True, dense=dense)
+
+
 @pytest.mark.parametrize("M", [1, 7])
 def test_router_gemv_small_shape(gpu, orc, M):
     log(f"router gemv E=16 H=512 M={M}")
@@ -164,3 +180,36 @@ def test_router_gemv_outputs_and_errors(gpu, orc, ctx):
     assert L.moe_router_gemv_topk(ctx._h, wg.data_ptr(), x.data_ptr(), 3, 0, None, None, None, None) == gpu.MOE_EINVAL
     assert L.moe_router_gemv_topk(ctx._h, wg.data_ptr() + 4, x.data_ptr(), 3, 0, lg.data_ptr(), None, None,
                                   None) == gpu.MOE_EINVAL
+
+
+def test_router_gemv_fused_graph_replays(gpu, ctx):
+    """The one-launch GEMV + top-8 (M <= 8) counts finished workgroups on device counters that
+    its last workgroup resets: replays of a captured call, with eager calls of other M in
+    between, each give the eager result bit for bit."""
+    import torch
+    log("router gemv fused: graph capture, 4 replays")
+    wg = gpu.gen_iq4xs(E * 2048 // 256, 0x5249)
+    x = gpu.gen_normal(3 * 2048, 0x524A).view(3, 2048)
+    x5 = gpu.gen_normal(5 * 2048, 0x524B).view(5, 2048)
+    lg0, ids0, w0 = (t.clone() for t in ctx.router_gemv_topk(wg, x))
+    torch.cuda.synchronize()
+    lg = torch.empty_like(lg0)
+    ids = torch.empty_like(ids0)
+    w = torch.empty_like(w0)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            ctx.router_gemv_topk(wg, x, logits=lg, ids=ids, w=w, stream=s)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        lg.fill_(float("nan"))
+        ids.zero_()
+        w.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(lg.view(torch.int32), lg0.view(torch.int32)), rep
+        assert torch.equal(ids, ids0) and torch.equal(w.view(torch.int32), w0.view(torch.int32)), rep
+        ctx.router_gemv_topk(wg, x5)        # an eager call of another M in between
+        torch.cuda.synchronize()

@@ -333,6 +333,33 @@ def test_router_gemv_closed_forms(orc):
     assert np.allclose(got_c[0], ref_c, rtol=1e-6, atol=1e-6 * np.abs(ref_c).max())
 
 
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_router_gemv_dense_weights(orc, dtype):
+    """F32 and F16 gate matrices (llama.cpp keeps ffn_gate_inp unquantized): against numpy's
+    f64 product of the matrix as given (rows = experts; f16 widened exactly), under RMSNorm
+    too; a unit vector e_k picks column k exactly; a transposed [H][E] matrix differs."""
+    E, H = 16, 512
+    rng = np.random.default_rng(31)
+    W = (rng.standard_normal((E, H)) * 0.05).astype(dtype)
+    x = rng.standard_normal((5, H)).astype(np.float32)
+    Wd = W.astype(np.float64)
+    got = orc.router_gemv(W, x, E)
+    ref = x.astype(np.float64) @ Wd.T
+    assert np.allclose(got, ref, rtol=2e-7, atol=1e-7 * np.abs(ref).max())
+    xn = x / np.sqrt((x.astype(np.float64) ** 2).mean(axis=1, keepdims=True) + 1e-6)
+    got_n = orc.router_gemv(W, x, E, flags=2)
+    assert np.allclose(got_n, xn @ Wd.T, rtol=2e-7, atol=1e-7 * np.abs(ref).max())
+    e_k = np.zeros((3, H), dtype=np.float32)
+    for i, k in enumerate((0, 77, H - 1)):
+        e_k[i, k] = 1.0
+    got_k = orc.router_gemv(W, e_k, E)
+    for i, k in enumerate((0, 77, H - 1)):
+        assert np.array_equal(got_k[i], W[:, k].astype(np.float32))
+    # the [H][E] transpose of the same numbers is a different matrix (only square shapes hide it)
+    got_t = orc.router_gemv(np.ascontiguousarray(W.T.reshape(E, H)), x, E)
+    assert np.abs(got_t - got).max() > 1e-2
+
+
 # ---------------------------------------------------------------- generator
 
 def test_generator_math(orc):
