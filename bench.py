@@ -43,7 +43,9 @@ F16_PEAK_TFLOPS = 2500.0  # dense f16 MFMA peak (the bf16 figure is the same)
 # HBM bytes per decode-stack launch measured by rocprofv3 (FETCH_SIZE and WRITE_SIZE runs,
 # calibrated on a plain copy); the summary and its commands are in this file:
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_stack_config2.md")
-LEGS = ("decode", "config0", "prefill", "config3", "config4")
+LEGS = ("decode", "decode_routed", "config0", "prefill", "config3", "config4")
+# config 2 routed from the activations: the 40 gate matrices are read too (IQ4_XS [256][2048])
+DECODE_ROUTED_BYTES_PER_TOKEN = DECODE_BYTES_PER_TOKEN + LAYERS * (E * H // 256 * 136)
 DTYPE = ("int8x2+f32: activations as two int8 planes (v_dot4_i32_i8 against the int8 IQ4_XS codebook, "
          "f32 scales and accumulation) in gate/up; f32 FMA in down and combine")
 
@@ -184,6 +186,43 @@ def leg_decode(torch, pkg, ctx, K, W, eager):
     return {"us": us, "gbs": gbs, "us_one_graph": us_one, "kern": kern}
 
 
+def leg_decode_routed(torch, pkg, ctx, routers, K, W, eager):
+    """Config 2 as a forward pass: every layer routed from its own RMSNorm'd input by its
+    IQ4_XS gate matrix inside the one stack launch (moe_bind_router + MOE_STACK_ROUTE_GEMV)."""
+    dev = torch.device("cuda:0")
+    for l in range(LAYERS):
+        ctx.bind_router(l, routers[l])
+    nsteps = W + K
+    x = pkg.gen_normal(H, pkg.seed_for(2, 0, pkg.TAG_X) + 1)
+    ids = torch.empty((LAYERS, 9), dtype=torch.uint16, device=dev)
+    wts = torch.empty((LAYERS, 9), dtype=torch.float32, device=dev)
+
+    def token(s):
+        ctx.decode_stack(0, x, y=x, ids=ids, w=wts, rmsnorm=True, n_layers=LAYERS)
+
+    token(0)
+    torch.cuda.synchronize()
+    assert ctx.device_flags() == 0, "decode stack raised a device flag"
+    if eager:
+        for s in range(nsteps):
+            token(s)
+        torch.cuda.synchronize()
+        return None
+    us, us_ev = timed_graphs(torch, token, nsteps, W, 8)
+    gbs = DECODE_ROUTED_BYTES_PER_TOKEN / (us * 1e-6) / 1e9
+    assert torch.isfinite(x).all() and ctx.device_flags() == 0
+    kern = kernel_times(ctx, lambda: [token(s) for s in range(W, min(nsteps, W + 8))], 64)
+    log(f"decode routed from activations: {us:.1f} us/token ({us_ev:.1f} by events), {gbs:.1f} GB/s = "
+        f"{100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak; kernels {kern}")
+    for l in range(LAYERS):
+        ctx.bind_router(l, None)
+    return {"workload": "config 2 as a forward pass: each of the 40 layers routed inside the stack launch "
+                        "from its own RMSNorm'd input by an IQ4_XS [256][2048] gate matrix "
+                        "(moe_bind_router, MOE_STACK_ROUTE_GEMV); graphs of 8 tokens",
+            "us_per_token": round(us, 2), "bytes_per_token": DECODE_ROUTED_BYTES_PER_TOKEN,
+            "gbs": round(gbs, 1), "hbm_peak_frac": round(gbs / HBM_PEAK_GBS, 4), "kernels": kern}
+
+
 def leg_config0(torch, pkg, ctx, routers, eager):
     """Config 0: one layer, M = 1 -- moe_ffn_route (routing inside the decode launch); and the
     activation-routed variant: moe_router_gemv_topk for the logits only, then moe_ffn_route.
@@ -319,7 +358,10 @@ def leg_config3(torch, pkg, ctx, eager):
     if eager:
         return None
     return {"workload": "config 3: one layer, M in {2, 4, 8}, independent N(0,1) x and logits per token; "
-                        "moe_ffn_route per step, graph replays", **c3}
+                        "moe_ffn_route per step, graph replays",
+            "dtype": "int8x2+f32: activations and, in the down product, h as two int8 planes per 32 "
+                     "elements (v_dot4_i32_i8 against the int8 IQ4_XS codebook), f32 scales and accumulation",
+            **c3}
 
 
 def leg_config4(torch, pkg, layer0, eager):
@@ -415,6 +457,7 @@ def main():
     if args.only:
         eager = True
         {"decode": lambda: leg_decode(torch, pkg, ctx, K, W, eager),
+         "decode_routed": lambda: leg_decode_routed(torch, pkg, ctx, routers, K, W, eager),
          "config0": lambda: leg_config0(torch, pkg, ctx, routers, eager),
          "prefill": lambda: leg_prefill(torch, pkg, ctx, args.prefill_steps, eager),
          "config3": lambda: leg_config3(torch, pkg, ctx, eager),
@@ -429,6 +472,7 @@ def main():
     stack_gbs = DECODE_BYTES_PER_TOKEN / (stack_us * 1e-6) / 1e9
     extra = {}
     if not args.no_extra_configs:
+        extra["decode_routed"] = leg_decode_routed(torch, pkg, ctx, routers, K, W, False)
         extra["config0"] = leg_config0(torch, pkg, ctx, routers, False)
     prefill = leg_prefill(torch, pkg, ctx, args.prefill_steps, False)
     if not args.no_extra_configs:

@@ -49,10 +49,12 @@ typedef enum { MOE_W_REF = 0, MOE_W_RENORM = 1 } moe_wmode;
 
 enum { MOE_TOPK = 8, MOE_SLOTS = 9, MOE_DECODE_MAX_M = 8, MOE_MAX_EXPERTS = 256 };
 
-/* moe_ffn flags */
+/* moe_ffn flags (and moe_decode_stack's) */
 enum {
-    MOE_FFN_ACCUMULATE = 1, /* y += out (fused residual); otherwise y = out */
-    MOE_FFN_RMSNORM = 2     /* FFN input is x / sqrt(mean(x^2) + 1e-6) (unit gain) */
+    MOE_FFN_ACCUMULATE = 1,  /* y += out (fused residual); otherwise y = out */
+    MOE_FFN_RMSNORM = 2,     /* FFN input is x / sqrt(mean(x^2) + 1e-6) (unit gain) */
+    MOE_STACK_ROUTE_GEMV = 4 /* moe_decode_stack only: route every layer from its own input
+                                with the router bound by moe_bind_router (no logits) */
 };
 
 /* Device-side input flags (sticky per context, read by moe_device_flags). */
@@ -96,6 +98,14 @@ moe_status moe_destroy(moe_ctx *ctx);
  * copy.
  * Replaces LayerWeights::from_registry (src/memory.rs:227-291). */
 moe_status moe_bind_layer(moe_ctx *ctx, int layer, const moe_layer_weights *lw);
+
+/* Bind layer `layer`'s router gate matrix for moe_decode_stack's MOE_STACK_ROUTE_GEMV form:
+ * wg [n_experts][hidden] of element type wg_type (MOE_WG_IQ4_XS, MOE_WG_F32, MOE_WG_F16 --
+ * declared below), rows = experts, 16-byte aligned device memory.  The library keeps the
+ * pointer, not a copy: the matrix must stay valid while bound.  wg = NULL unbinds.
+ * Replaces the ffn_gate entry of LayerWeights::from_registry (src/memory.rs:236-262), which
+ * the Router dispatch reads (src/inference.rs:598-605). */
+moe_status moe_bind_router(moe_ctx *ctx, int layer, const void *wg, int wg_type);
 
 /* Softmax + top-8 per token: logits f32 [M][n_experts] -> ids u16 [M][9], w f32 [M][9].
  * Ties go to the lower index; NaN logits never win and count as -inf in the softmax.
@@ -177,11 +187,16 @@ moe_status moe_ffn_noalloc(moe_ctx *ctx, int layer, const float *x, const uint16
 /* One token (M = 1) through n_layers consecutive MoE layers in one persistent launch (the
  * routing of every layer runs inside it; nothing else is launched):
  *   for l in layer0 .. layer0+n_layers-1:
+ *       xin = RMSNorm(x) if asked, else x
  *       (ids_l, w_l) = top8(softmax(logits[l - layer0]))      (as moe_router_topk)
- *       x = x + c * sum_{s<9} w_l[s] * FFN_{ids_l[s]}(xin),  xin = RMSNorm(x) if asked
+ *          or, with MOE_STACK_ROUTE_GEMV, top8(softmax(Wg_l xin)), Wg_l the router bound
+ *          to layer l (as moe_router_gemv_topk_typed, with xin read as the two int8 planes
+ *          per 32 elements the expert products read; logits within 1 ulp of f32 sums)
+ *       x = x + c * sum_{s<9} w_l[s] * FFN_{ids_l[s]}(xin)
  *   y = x  (y may be the same buffer as x)
- * logits f32 [n_layers][n_experts]; ids u16 / w f32 [n_layers][9] receive the routing
- * (both may be NULL).  flags: MOE_FFN_RMSNORM (the residual is always added).
+ * logits f32 [n_layers][n_experts] (NULL with MOE_STACK_ROUTE_GEMV); ids u16 / w f32
+ * [n_layers][9] receive the routing (both may be NULL).  flags: MOE_FFN_RMSNORM,
+ * MOE_STACK_ROUTE_GEMV (the residual is always added).
  * Needs n_experts <= 256 and every workgroup of the launch resident at once (one per CU;
  * checked at moe_create), hidden/8 workgroups spread evenly over the device's 8 XCDs.
  * Every wait inside the launch is bounded: one that expires sets MOE_DEVFLAG_TIMEOUT, every
@@ -192,7 +207,8 @@ moe_status moe_ffn_noalloc(moe_ctx *ctx, int layer, const float *x, const uint16
  * fail the same way (never with a silently wrong y).
  * Replaces, for the MoE path of one decode token, the per-layer sequence
  * record_and_submit_layer's RouterTopk dispatch -> do_route -> record_and_submit_moe of
- * InferenceEngine::forward_single (src/inference.rs:296-301, 608-616, 622-766). */
+ * InferenceEngine::forward_single (src/inference.rs:296-301, 608-616, 622-766) -- with
+ * MOE_STACK_ROUTE_GEMV also its Router dispatch (src/inference.rs:598-605). */
 moe_status moe_decode_stack(moe_ctx *ctx, int layer0, int n_layers, const float *x,
                             const float *logits, float *y, uint16_t *ids, float *w, int flags,
                             void *stream);

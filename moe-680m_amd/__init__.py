@@ -34,14 +34,14 @@ MOE_OK, MOE_EINVAL, MOE_ENOMEM, MOE_EHIP, MOE_EUNSUPPORTED, MOE_EDEVICE = range(
 STATUS_NAMES = {0: "MOE_OK", 1: "MOE_EINVAL", 2: "MOE_ENOMEM", 3: "MOE_EHIP",
                 4: "MOE_EUNSUPPORTED", 5: "MOE_EDEVICE"}
 W_REF, W_RENORM = 0, 1
-FFN_ACCUMULATE, FFN_RMSNORM = 1, 2
+FFN_ACCUMULATE, FFN_RMSNORM, STACK_ROUTE_GEMV = 1, 2, 4
 DEVFLAG_BAD_ID, DEVFLAG_DUP_ID, DEVFLAG_TIMEOUT = 1, 2, 4
 # Router gate matrix element types (GGML type ids, include/moe_ffn.h MOE_WG_*).
 WG_F32, WG_F16, WG_IQ4_XS = 0, 1, 23
 
 # Every symbol include/moe_ffn.h declares (checked by the CPU test suite).
 EXPORTS = (
-    "moe_create", "moe_destroy", "moe_bind_layer", "moe_router_topk", "moe_router_gemv_topk",
+    "moe_create", "moe_destroy", "moe_bind_layer", "moe_bind_router", "moe_router_topk", "moe_router_gemv_topk",
     "moe_router_gemv_topk_typed", "moe_bucket_fill",
     "moe_ffn", "moe_ffn_route", "moe_ffn_noalloc", "moe_decode_stack", "moe_dequant_iq4xs", "moe_device_flags",
     "moe_device_flags_async", "moe_stack_spin_limit", "moe_last_error",
@@ -91,6 +91,7 @@ def lib():
         "moe_router_topk": [vp, vp, i, vp, vp, vp],
         "moe_router_gemv_topk": [vp, vp, vp, i, i, vp, vp, vp, vp],
         "moe_router_gemv_topk_typed": [vp, vp, i, vp, i, i, vp, vp, vp, vp],
+        "moe_bind_router": [vp, i, vp, i],
         "moe_bucket_fill": [vp, vp, vp, i, vp, vp, vp, vp],
         "moe_ffn": [vp, i, vp, vp, vp, i, vp, i, vp],
         "moe_ffn_route": [vp, i, vp, vp, i, vp, vp, vp, i, vp],
@@ -283,16 +284,40 @@ class Context:
                                    flags, _stream(stream)))
         return y, ids, w
 
-    def decode_stack(self, layer0, x, logits, y=None, ids=None, w=None, rmsnorm=True, stream=None):
-        """One token through len(logits) consecutive layers starting at layer0:
-        routing from logits[l], x <- x + MoE_l(RMSNorm(x)).  Returns y (= x if y is x)."""
-        n = logits.shape[0]
+    def decode_stack(self, layer0, x, logits=None, y=None, ids=None, w=None, rmsnorm=True, n_layers=None,
+                     stream=None):
+        """One token through consecutive layers starting at layer0, x <- x + MoE_l(RMSNorm(x)):
+        routing from logits[l] (len(logits) layers), or -- logits None -- from each layer's
+        input through the routers bound with bind_router (n_layers layers).  Returns y (= x
+        if y is x)."""
+        flags = FFN_RMSNORM if rmsnorm else 0
+        if logits is None:
+            if n_layers is None:
+                raise ValueError("n_layers is required when routing from the activations")
+            n = n_layers
+            flags |= STACK_ROUTE_GEMV
+        else:
+            n = logits.shape[0]
         if y is None:
             y = torch.empty_like(x)
-        flags = FFN_RMSNORM if rmsnorm else 0
         _check(lib().moe_decode_stack(self._h, layer0, n, _ptr(x), _ptr(logits), _ptr(y), _ptr(ids),
                                       _ptr(w), flags, _stream(stream)))
         return y
+
+    def bind_router(self, layer, wg):
+        """Bind layer's router gate matrix [n_experts][hidden] (a device tensor: uint8 IQ4_XS
+        bytes, float32 or float16) for decode_stack without logits; None unbinds.  The
+        library keeps the pointer: keep the tensor alive while it is bound."""
+        if wg is None:
+            _check(lib().moe_bind_router(self._h, layer, None, 0))
+            return
+        wtype = {torch.uint8: WG_IQ4_XS, torch.float32: WG_F32, torch.float16: WG_F16}.get(wg.dtype)
+        if wtype is None:
+            raise ValueError(f"gate matrix dtype {wg.dtype}: uint8 (IQ4_XS), float32 or float16")
+        want = matrix_bytes(self.hidden, self.n_experts) if wtype == WG_IQ4_XS else self.n_experts * self.hidden
+        if wg.numel() != want or not wg.is_contiguous():
+            raise ValueError("wg must hold the n_experts x hidden gate matrix, contiguous")
+        _check(lib().moe_bind_router(self._h, layer, _ptr(wg), wtype))
 
     def device_flags(self, stream=None):
         v = ctypes.c_uint32()

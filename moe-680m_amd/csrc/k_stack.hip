@@ -219,12 +219,21 @@ __device__ __forceinline__ void store_quad(uint32_t *xq, int q, u32x4 v) {
 // 16-byte quads of one layer block of an exchange set (stack_layer_words / 4).
 template <int H, int I>
 __host__ __device__ constexpr uint64_t stack_layer_quads() {
-    return (uint64_t)STK_NX * (3 * I + H + H / 2 + H / 32 + H / 64) / 4;
+    return (uint64_t)STK_NX * (3 * I + H + H / 2 + H / 32 + H / 64 + STK_LG_WORDS) / 4;
 }
-static_assert(stack_layer_quads<2048, 512>() * 4 == (uint64_t)STK_NX * (3 * 512 + 2048 + 1024 + 64 + 32),
+static_assert(stack_layer_quads<2048, 512>() * 4 ==
+                  (uint64_t)STK_NX * (3 * 512 + 2048 + 1024 + 64 + 32 + STK_LG_WORDS),
               "whole quads per layer block");
 
-template <int H, int I>
+// AR (StackArgs::logits null): every layer is routed from its own input.  Per layer, after
+// x_l is in LDS (B1), every compute wave takes one router row's dot with it -- row
+// (j * NCW + w) * RPS1 + rr1 of the layer's gate matrix (IQ4_XS, f32 or f16, requested
+// while the previous layer's x was exchanged), against the same int8 planes phase A reads --
+// and publishes the logit inside its XCD; the router wave gathers all E, routes the layer and
+// fills its ring slot; one more LDS barrier (BR) hands the routing to the compute waves, which
+// only then request that layer's expert weights.  Every XCD computes the same logits from the
+// same planes, so all eight agree on the routing.  Logits are LSB-tagged (<= 1 ulp).
+template <int H, int I, bool AR>
 __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     constexpr int NX = STK_NX;
     constexpr int NCW = STK_CWAVES;          // compute waves, two per SIMD
@@ -282,6 +291,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     __shared__ int s_j;
     __shared__ uint32_t s_ep;
     __shared__ RouteLds s_route[2]; // layers 0 and 1, routed by four waves each
+    __shared__ __attribute__((aligned(16))) float s_lg[STK_LG_WORDS]; // AR: a layer's logits
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     // HW_REG_XCC_ID (readfirstlane: the compiler then knows the value is wave-uniform)
@@ -317,12 +327,18 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     // raise the timeout and leave, and the others' bounded waits end the launch with y
     // untouched.
     if (wv < NCW) {
-        const int grp = wv >> 2, r = grp < n ? grp : 0;
-        const LayerPtrs L = load_layer(a.layers + a.layer0 + r);
-        int id;
-        float wt;
-        route_wg4(a.logits + (size_t)r * a.E, a.E, a.renorm, lane, wv & 3, s_route[grp], id, wt);
-        if ((wv & 3) == 0 && grp < n) ring_write(grp, id, wt, L);
+        if constexpr (AR) {
+            // nothing to route yet: the two barriers of route_wg4 only
+            lds_barrier();
+            lds_barrier();
+        } else {
+            const int grp = wv >> 2, r = grp < n ? grp : 0;
+            const LayerPtrs L = load_layer(a.layers + a.layer0 + r);
+            int id;
+            float wt;
+            route_wg4(a.logits + (size_t)r * a.E, a.E, a.renorm, lane, wv & 3, s_route[grp], id, wt);
+            if ((wv & 3) == 0 && grp < n) ring_write(grp, id, wt, L);
+        }
     } else {
         // the ticket and the epoch are requested first and waited for only after the routing
         // waves' two barriers
@@ -375,49 +391,98 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     auto hbuf = [&](int li) { return xset + (size_t)li * LW + (size_t)k * HXG; };
     auto pbuf = [&](int li) { return xset + (size_t)li * LW + (size_t)NX * HXG; };
     auto xbuf = [&](int li) { return xset + (size_t)li * LW + (size_t)NX * (HXG + H) + (size_t)k * (4 * XQ); }; // x_{li+1}
+    auto lbuf = [&](int li) { // AR: layer li's logits
+        return xset + (size_t)li * LW + (size_t)NX * (HXG + H + 4 * XQ) + (size_t)k * STK_LG_WORDS;
+    };
+    const int E4 = (a.E + 3) & ~3; // AR: logit words published (rows E..E4-1 as dummies)
 
     if (wv == NCW) {
-        // ---------------- router wave: routes layer r + 3 into ring slot r % 3 while the
-        // pollers end layer r (after B3; that slot was last read in phase B of r and is next
-        // read at B2 of r + 2), layer 2 right after B0; clears the other exchange set.
-        float raw[4];
-        LayerPtrs L;
-        auto fetch = [&](int r) __attribute__((always_inline)) {
-            load_logits<4>(a.logits + (size_t)r * a.E, a.E, lane, raw);
-            L = load_layer(a.layers + a.layer0 + r);
-        };
-        auto route = [&](int r) __attribute__((always_inline)) {
-            int id;
-            float wt;
-            route_values<4>(raw, a.E, a.renorm, lane, id, wt);
-            ring_write(r, id, wt, L);
-            if (r + 1 < n) fetch(r + 1);
-        };
-        if (blockIdx.x == 0 && lane == 0)
-            __hip_atomic_store((MOE_GLOBAL uint32_t *)ctl(STK_CTL_DIRTY + (int)(ep & 1u)), (uint32_t)n,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (n > 2) fetch(2);
-        // window 0 follows B0, window li + 1 follows B3 of layer li; window w routes layer w + 2
-        for (int wdw = 0; wdw <= n; ++wdw) {
-            if (wdw > 0) {
-                lds_barrier();             // B1 of layer wdw - 1
-                lds_barrier();             // B2
-                // every workgroup of the XCD published its h of layer 0 (the wait before B2
-                // succeeded), so all took their tickets: reset the XCD's counter for the next
-                // launch
-                if (wdw == 1 && j == 0 && lane == 0 && !*abort_lds)
-                    __hip_atomic_store((MOE_GLOBAL uint32_t *)ctl(k), 0u, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                lds_barrier();             // B3
+        if constexpr (AR) {
+            // ---------------- router wave (AR): routes layer li from the logits that every
+            // workgroup of this XCD published after B1 of li, into ring slot li % 3 before BR;
+            // clears the other exchange set in n + 1 pieces, as below
+            if (blockIdx.x == 0 && lane == 0)
+                __hip_atomic_store((MOE_GLOBAL uint32_t *)ctl(STK_CTL_DIRTY + (int)(ep & 1u)), (uint32_t)n,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            clear_other(0, n + 1);
+            const int nq = E4 >> 2;
+            for (int li = 0; li < n; ++li) {
+                const LayerPtrs L = load_layer(a.layers + a.layer0 + li);
+                lds_barrier(); // B1: x_li in LDS, its logits being published
+                {
+                    const LocalQuads ld{reinterpret_cast<const uint64_t *>(lbuf(li))};
+                    int q[1] = {lane};
+                    u32x4 v[1] = {lane < nq ? ld(lane) : u32x4{1u, 1u, 1u, 1u}};
+                    // a wait that gives up leaves the abort flag set: stale logits then still
+                    // route to valid expert ids, and nothing computed from them is published
+                    (void)poll_until_tagged<1>(v, q, ld, a.flags, atag, a.spin_max, abort_lds);
+                    if (lane < nq) *reinterpret_cast<f32x4 *>(s_lg + 4 * lane) = __builtin_bit_cast(f32x4, v[0]);
+                    // lanes read what other lanes of this wave wrote: LDS keeps a wave's
+                    // accesses in order, the compiler must too
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    float raw[4];
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) raw[jj] = s_lg[min(lane + 64 * jj, a.E - 1)];
+                    int id;
+                    float wt;
+                    __builtin_amdgcn_s_setprio(3);
+                    route_values<4>(raw, a.E, a.renorm, lane, id, wt);
+                    __builtin_amdgcn_s_setprio(0);
+                    ring_write(li, id, wt, L);
+                }
+                lds_barrier(); // BR: routing of li in LDS
+                lds_barrier(); // B2
+                // every workgroup of the XCD published its h of layer 0, so all took their
+                // tickets: reset the XCD's counter for the next launch
+                if (li == 0 && j == 0 && lane == 0 && !*abort_lds)
+                    __hip_atomic_store((MOE_GLOBAL uint32_t *)ctl(k), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                lds_barrier(); // B3
+                clear_other(li + 1, n + 1);
             }
-            // at the priority of the compute waves' phases: at 0 the routing took issue slots
-            // behind the compute waves' lookups and reached B1 late (measured +0.5 us per layer)
-            __builtin_amdgcn_s_setprio(3);
-            if (wdw + 2 < n) route(wdw + 2);
-            __builtin_amdgcn_s_setprio(0);
-            clear_other(wdw, n + 1);
+            return;
+        } else {
+            // ---------------- router wave: routes layer r + 3 into ring slot r % 3 while the
+            // pollers end layer r (after B3; that slot was last read in phase B of r and is next
+            // read at B2 of r + 2), layer 2 right after B0; clears the other exchange set.
+            float raw[4];
+            LayerPtrs L;
+            auto fetch = [&](int r) __attribute__((always_inline)) {
+                load_logits<4>(a.logits + (size_t)r * a.E, a.E, lane, raw);
+                L = load_layer(a.layers + a.layer0 + r);
+            };
+            auto route = [&](int r) __attribute__((always_inline)) {
+                int id;
+                float wt;
+                route_values<4>(raw, a.E, a.renorm, lane, id, wt);
+                ring_write(r, id, wt, L);
+                if (r + 1 < n) fetch(r + 1);
+            };
+            if (blockIdx.x == 0 && lane == 0)
+                __hip_atomic_store((MOE_GLOBAL uint32_t *)ctl(STK_CTL_DIRTY + (int)(ep & 1u)), (uint32_t)n,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (n > 2) fetch(2);
+            // window 0 follows B0, window li + 1 follows B3 of layer li; window w routes layer w + 2
+            for (int wdw = 0; wdw <= n; ++wdw) {
+                if (wdw > 0) {
+                    lds_barrier();             // B1 of layer wdw - 1
+                    lds_barrier();             // B2
+                    // every workgroup of the XCD published its h of layer 0 (the wait before B2
+                    // succeeded), so all took their tickets: reset the XCD's counter for the next
+                    // launch
+                    if (wdw == 1 && j == 0 && lane == 0 && !*abort_lds)
+                        __hip_atomic_store((MOE_GLOBAL uint32_t *)ctl(k), 0u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                    lds_barrier();             // B3
+                }
+                // at the priority of the compute waves' phases: at 0 the routing took issue slots
+                // behind the compute waves' lookups and reached B1 late (measured +0.5 us per layer)
+                __builtin_amdgcn_s_setprio(3);
+                if (wdw + 2 < n) route(wdw + 2);
+                __builtin_amdgcn_s_setprio(0);
+                clear_other(wdw, n + 1);
+            }
+            return;
         }
-        return;
     }
 
     if (wv > NCW) {
@@ -453,6 +518,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         float xres = first ? a.x[ROWS * j + lane] : 0.f;
         for (int li = 0; li < n; ++li) {
             lds_barrier(); // B1: x_li in LDS
+            if constexpr (AR) lds_barrier(); // BR: the layer's routing in LDS
             // the h exchange: ahead of the compute waves' phase-B lookups (priority 0), level
             // with phase A (priority 1; the older compute waves win the ties)
             __builtin_amdgcn_s_setprio(1);
@@ -796,15 +862,123 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         asm volatile("" : "+v"(sbk[0]), "+v"(sbk[1]), "+v"(bs), "+v"(sbs));
     };
 
-    prefetch_a(0);
-    decode_a();
+    // AR: this wave's router row of the next layer to route -- row rG, the lane's sub-block
+    // g1 (rows past E read row E-1; their logit is a dummy) -- and its element type.  IQ4_XS
+    // and f16 weights are requested into registers while the previous layer's x is exchanged;
+    // an f32 lane's 128 bytes (one cache line) are only touched then, by one dword load, and
+    // read whole by router_dot (from the L2): 32 more registers live across the exchange would
+    // spill.
+    const int rG = (j * NCW + w) * RPS1 + rr1, rGc = min(rG, a.E - 1);
+    u32x4 rq[8];        // IQ4_XS: rq[0] = the 16 qs bytes; f16: rq[0..3]; f32: rq[0..7]
+    u32x2 rgh;          // IQ4_XS header
+    uint32_t rg_type = MOE_WG_IQ4_XS;
+    const uint8_t *rg_row = nullptr; // f32: this lane's 128 bytes
+    auto rg_prefetch = [&](int li) __attribute__((always_inline)) {
+        const uint64_t *t = reinterpret_cast<const uint64_t *>(a.routers + a.layer0 + li);
+        const uint8_t *wg = (const uint8_t *)ldg<uint64_t>(t);
+        rg_type = (uint32_t)ldg<uint64_t>(t + 1);
+        if (rg_type == MOE_WG_IQ4_XS) {
+            const uint8_t *blk = wg + ((size_t)rGc * SBR1 + (g1 >> 3)) * SB_BYTES;
+            rgh = ldg<u32x2>(blk);
+            const u32x2 q01 = ldg<u32x2>(blk + 8 + 16 * (g1 & 7)), q23 = ldg<u32x2>(blk + 16 + 16 * (g1 & 7));
+            rq[0] = u32x4{q01.x, q01.y, q23.x, q23.y};
+        } else if (rg_type == MOE_WG_F16) {
+            const uint8_t *p = wg + ((size_t)rGc * H + 32 * g1) * 2;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) rq[i] = ldg<u32x4>(p + 16 * i);
+        } else {
+            rg_row = wg + ((size_t)rGc * H + 32 * g1) * 4;
+            rq[0].x = ldg<uint32_t>(rg_row); // the line into the L2; the value is not used
+            asm volatile("" : "+v"(rq[0].x));
+        }
+    };
+    // AR: the logit of row rG against x_li (xin = RMSNorm(x) when asked, as phase A), published
+    // in this XCD's logit block of layer li
+    auto router_dot = [&](int li) __attribute__((always_inline)) {
+        uint32_t xh[8], xl[8];
+        {
+            const u32x4 *c = reinterpret_cast<const u32x4 *>(xq + XQS * g1);
+            const u32x4 h0 = c[0], h1 = c[1], l0 = c[2], l1 = c[3];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                xh[e] = h0[e];
+                xh[4 + e] = h1[e];
+                xl[e] = l0[e];
+                xl[4 + e] = l1[e];
+            }
+        }
+        const float sx = xsc[g1];
+        const int ab = *abort_lds;
+        float inv = 1.0f;
+        if (a.rmsnorm) {
+            float ss = 0.f;
+#pragma unroll
+            for (int i = 0; i < NSS; ++i) ss += ssq[i];
+            inv = __builtin_amdgcn_rsqf(ss * (1.0f / (float)H) + 1e-6f);
+        }
+        float part;
+        if (rg_type == MOE_WG_F32)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) rq[i] = ldg<u32x4>(rg_row + 16 * i);
+        if (rg_type == MOE_WG_IQ4_XS) {
+            uint32_t kv[8];
+#pragma unroll
+            for (int d = 0; d < 4; ++d) kv_signed8(rq[0][d], kv[2 * d], kv[2 * d + 1]);
+            part = (sub_scale(rgh, g1 & 7) * sx) * subblock_idot(kv, xh, xl);
+        } else {
+            // element 4i + b of the chunk: weight word i, byte / half b; planes dword i, byte
+            // b, read biased (xh + 128, by v_cvt_f32_ubyte) with the bias removed once:
+            // sum w (xh + xl/256) = sum w (xh + 128) + sum w (xl + 128) / 256 - 128.5 sum w
+            float ah = 0.f, al = 0.f, sw = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t bh = xh[i] ^ 0x80808080u, bl = xl[i] ^ 0x80808080u;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const int e = 4 * i + b;
+                    float wv;
+                    if (rg_type == MOE_WG_F16) {
+                        const f16x2 h2 = __builtin_bit_cast(f16x2, (uint32_t)rq[e >> 3][(e >> 1) & 3]);
+                        wv = (float)h2[e & 1];
+                    } else {
+                        wv = __builtin_bit_cast(float, (uint32_t)rq[e >> 2][e & 3]);
+                    }
+                    ah = __builtin_fmaf(wv, ubyte(bh, b), ah);
+                    al = __builtin_fmaf(wv, ubyte(bl, b), al);
+                    sw += wv;
+                }
+            }
+            part = sx * (__builtin_fmaf(al, 1.0f / 256.0f, ah) - 128.5f * sw);
+        }
+        const float tot = inv * row_total<LPR1>(part);
+        if (g1 == LPR1_LAST && rG < E4 && !ab) tag_store_local(lbuf(li) + rG, rG < a.E ? tot : 0.0f);
+    };
+
+    if constexpr (AR) {
+        rg_prefetch(0);
+    } else {
+        prefetch_a(0);
+        decode_a();
+    }
 
     for (int li = 0; li < n; ++li) {
         lds_barrier(); // B1: x_l in LDS
-        // phase A ahead of the other compute wave's decode on this SIMD
-        __builtin_amdgcn_s_setprio(1);
-        prefetch_b(li);
-        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (AR) {
+            // route this layer from x_l: this wave's logit, then (after BR) the routed
+            // experts' weights, requested only now
+            router_dot(li);
+            lds_barrier(); // BR: routing of li in LDS
+            prefetch_a(li);
+            __builtin_amdgcn_s_setprio(1);
+            prefetch_b(li);
+            __builtin_amdgcn_sched_barrier(0);
+            decode_a();
+        } else {
+            // phase A ahead of the other compute wave's decode on this SIMD
+            __builtin_amdgcn_s_setprio(1);
+            prefetch_b(li);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         // phase A: h = silu(W1 xin) * (W3 xin) for this wave's slot-k row pairs, and this
         // wave's K share of the workgroup's shared rows (partial g, u: combined by the
         // pollers of every workgroup of the XCD)
@@ -858,7 +1032,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         __builtin_amdgcn_s_setprio(0);
         decode_b();
         lds_barrier(); // B2: h_l in LDS; routing of layer li+2 in LDS
-        prefetch_a(min(li + 1, n - 1));
+        if constexpr (!AR) prefetch_a(min(li + 1, n - 1));
         // nothing of phase B above the burst: its first use of this layer's W2 registers
         // then waits for those loads only, not for everything (stores included) in flight
         __builtin_amdgcn_sched_barrier(0);
@@ -897,31 +1071,40 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         }
         lds_barrier(); // B3: contributions in LDS
         // the pollers now gather the partials and exchange x: decode layer li+1's phase-A
-        // weights (requested at B2) meanwhile
-        decode_a();
+        // weights (requested at B2) meanwhile -- or, AR, request layer li+1's router rows
+        if constexpr (AR) rg_prefetch(min(li + 1, n - 1));
+        else decode_a();
     }
 }
 
 size_t stack_layer_words(int H, int I) {
-    return (size_t)STK_NX * (3 * (size_t)I + (size_t)H + (size_t)(H / 2 + H / 32 + H / 64));
+    return (size_t)STK_NX * (3 * (size_t)I + (size_t)H + (size_t)(H / 2 + H / 32 + H / 64) + STK_LG_WORDS);
 }
 
 template <int H, int I>
 static hipError_t launch_stack_t(const StackArgs &a, hipStream_t st, KernelTimer *T) {
     TimedLaunch tl(T, MOE_K_DECODE_STACK, st);
-    hipLaunchKernelGGL((k_decode_stack<H, I>), dim3(H / 8), dim3(64 * STK_WAVES), 0, st, a);
+    if (a.logits)
+        hipLaunchKernelGGL((k_decode_stack<H, I, false>), dim3(H / 8), dim3(64 * STK_WAVES), 0, st, a);
+    else
+        hipLaunchKernelGGL((k_decode_stack<H, I, true>), dim3(H / 8), dim3(64 * STK_WAVES), 0, st, a);
     return hipGetLastError();
 }
 
 int stack_blocks(int H) { return H / 8; }
 
-hipError_t stack_occupancy(int H, int I, int *blocks_per_cu) {
-    if (H == 2048 && I == 512)
-        return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, k_decode_stack<2048, 512>,
+template <int H, int I>
+static hipError_t stack_occupancy_t(bool ar, int *blocks_per_cu) {
+    if (ar)
+        return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, k_decode_stack<H, I, true>,
                                                             64 * STK_WAVES, 0);
-    if (H == 512 && I == 256)
-        return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, k_decode_stack<512, 256>,
-                                                            64 * STK_WAVES, 0);
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, k_decode_stack<H, I, false>, 64 * STK_WAVES,
+                                                        0);
+}
+
+hipError_t stack_occupancy(int H, int I, bool ar, int *blocks_per_cu) {
+    if (H == 2048 && I == 512) return stack_occupancy_t<2048, 512>(ar, blocks_per_cu);
+    if (H == 512 && I == 256) return stack_occupancy_t<512, 256>(ar, blocks_per_cu);
     return hipErrorInvalidValue;
 }
 

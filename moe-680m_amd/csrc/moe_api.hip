@@ -41,9 +41,12 @@ struct moe_ctx {
     uint32_t *chunk = nullptr;   // [ceil(m_max/64)][E+1]
     Tile *tiles = nullptr;       // [tile_max(m_max)]
     LayerPtrs *dlayers = nullptr; // device layer table of the split copies (decode stack)
+    StackRouter *drouters = nullptr;   // device table of the bound router matrices
+    std::vector<StackRouter> hrouters; // ... and its host copy
     uint32_t *xtag = nullptr;    // decode stack: control words, then its two exchange sets
     size_t xtag_words = 0;
     int stack_ok = 0;            // all stack workgroups fit on the device at once
+    int stack_ok_ar = 0;         // ... and those of its activation-routed form
     int ncu = 0;                 // compute units of the device
     uint32_t spin_max = STK_SPIN_DEFAULT; // decode stack: poll rounds before a wait expires
     KernelTimer timer;
@@ -128,6 +131,7 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
     c->cfg = *cfg;
     c->slayers.resize(cfg->n_layers);
     c->bound.assign(cfg->n_layers, 0);
+    c->hrouters.assign(cfg->n_layers, StackRouter{nullptr, 0u, 0u});
 
     const size_t mm = (size_t)cfg->m_max, E1 = (size_t)E + 1;
     const size_t nchunk = (mm + 63) / 64;
@@ -152,6 +156,7 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
         {(void **)&c->chunk, nchunk * E1 * 4},
         {(void **)&c->tiles, tmax * sizeof(Tile)},
         {(void **)&c->dlayers, (size_t)cfg->n_layers * sizeof(LayerPtrs)},
+        {(void **)&c->drouters, (size_t)cfg->n_layers * sizeof(StackRouter)},
         {(void **)&c->xtag, (STK_CTL_WORDS + 2 * (size_t)cfg->n_layers * stack_layer_words(H, I)) * 4},
     };
     size_t total = 0;
@@ -183,6 +188,7 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
     c->xtag_words = STK_CTL_WORDS + 2 * (size_t)cfg->n_layers * stack_layer_words(H, I);
     he = hipMemset(c->flags, 0, 256);
     if (he == hipSuccess) he = hipMemset(c->dlayers, 0, (size_t)cfg->n_layers * sizeof(LayerPtrs));
+    if (he == hipSuccess) he = hipMemset(c->drouters, 0, (size_t)cfg->n_layers * sizeof(StackRouter));
     // the decode stack's control words and both exchange sets start zeroed
     if (he == hipSuccess) he = hipMemset(c->xtag, 0, c->xtag_words * 4);
     if (he == hipSuccess) he = hipDeviceSynchronize();
@@ -197,8 +203,11 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
     if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || ncu < 1)
         ncu = 1;
     c->ncu = ncu;
-    if (stack_occupancy(H, I, &per_cu) == hipSuccess)
+    if (stack_occupancy(H, I, false, &per_cu) == hipSuccess)
         c->stack_ok = (per_cu >= 1 && (long)per_cu * ncu >= stack_blocks(H) && E <= 256) ? 1 : 0;
+    per_cu = 0;
+    if (stack_occupancy(H, I, true, &per_cu) == hipSuccess)
+        c->stack_ok_ar = (per_cu >= 1 && (long)per_cu * ncu >= stack_blocks(H) && E <= 256) ? 1 : 0;
     // moe_ffn_noalloc's static scratch: its device address looked up now, with the device
     // current, so that entry point never makes the lookup itself (a failure here is not
     // fatal: that entry point retries and reports it)
@@ -266,6 +275,26 @@ moe_status moe_bind_layer(moe_ctx *ctx, int layer, const moe_layer_weights *lw) 
         ctx->slayers[layer] = S;
     }
     ctx->bound[layer] = 1;
+    return ok();
+}
+
+moe_status moe_bind_router(moe_ctx *ctx, int layer, const void *wg, int wg_type) {
+    if (!ctx) return fail(MOE_EINVAL, "moe_bind_router: null context");
+    if (layer < 0 || layer >= ctx->cfg.n_layers)
+        return fail(MOE_EINVAL, "moe_bind_router: layer %d outside 0..%d", layer, ctx->cfg.n_layers - 1);
+    StackRouter R{nullptr, 0u, 0u};
+    if (wg) {
+        if (wg_type != MOE_WG_IQ4_XS && wg_type != MOE_WG_F32 && wg_type != MOE_WG_F16)
+            return fail(MOE_EUNSUPPORTED, "moe_bind_router: gate matrix type %d (IQ4_XS %d, F32 %d and F16 %d)",
+                        wg_type, MOE_WG_IQ4_XS, MOE_WG_F32, MOE_WG_F16);
+        if (!aligned16(wg)) return fail(MOE_EINVAL, "moe_bind_router: gate matrix %p not 16-byte aligned", wg);
+        R.wg = (const uint8_t *)wg;
+        R.type = (uint32_t)wg_type;
+    }
+    hipError_t he = hipSetDevice(ctx->device);
+    if (he == hipSuccess) he = hipMemcpy(ctx->drouters + layer, &R, sizeof R, hipMemcpyHostToDevice);
+    if (he != hipSuccess) return hip_fail(he, "moe_bind_router: copying the router table");
+    ctx->hrouters[layer] = R;
     return ok();
 }
 
@@ -458,14 +487,26 @@ moe_status moe_ffn_route(moe_ctx *ctx, int layer, const float *x, const float *l
 moe_status moe_decode_stack(moe_ctx *ctx, int layer0, int n_layers, const float *x, const float *logits,
                             float *y, uint16_t *ids, float *w, int flags, void *stream) {
     if (!ctx) return fail(MOE_EINVAL, "moe_decode_stack: null context");
-    if (!x || !logits || !y) return fail(MOE_EINVAL, "moe_decode_stack: null argument");
+    const bool ar = (flags & MOE_STACK_ROUTE_GEMV) != 0;
+    if (!x || !y) return fail(MOE_EINVAL, "moe_decode_stack: null argument");
+    if (ar && logits) return fail(MOE_EINVAL, "moe_decode_stack: MOE_STACK_ROUTE_GEMV takes no logits");
+    if (!ar && !logits) return fail(MOE_EINVAL, "moe_decode_stack: null logits (without MOE_STACK_ROUTE_GEMV)");
     if ((ids == nullptr) != (w == nullptr)) return fail(MOE_EINVAL, "moe_decode_stack: ids and w go together");
     if (n_layers < 1 || layer0 < 0 || layer0 + n_layers > ctx->cfg.n_layers)
         return fail(MOE_EINVAL, "moe_decode_stack: layers %d..%d outside 0..%d", layer0, layer0 + n_layers - 1,
                     ctx->cfg.n_layers - 1);
     for (int l = layer0; l < layer0 + n_layers; ++l)
         if (!ctx->bound[l]) return fail(MOE_EINVAL, "moe_decode_stack: layer %d has no bound weights", l);
-    if (flags & ~MOE_FFN_RMSNORM) return fail(MOE_EINVAL, "moe_decode_stack: unknown flags 0x%x", flags);
+    if (flags & ~(MOE_FFN_RMSNORM | MOE_STACK_ROUTE_GEMV))
+        return fail(MOE_EINVAL, "moe_decode_stack: unknown flags 0x%x", flags);
+    if (ar) {
+        for (int l = layer0; l < layer0 + n_layers; ++l)
+            if (!ctx->hrouters[l].wg)
+                return fail(MOE_EINVAL, "moe_decode_stack: layer %d has no bound router (moe_bind_router)", l);
+        if (!ctx->stack_ok_ar)
+            return fail(MOE_EUNSUPPORTED, "moe_decode_stack: the activation-routed form needs %d co-resident "
+                        "workgroups", stack_blocks(ctx->cfg.hidden));
+    }
     if (!aligned16(x) || !aligned16(y) || ((uintptr_t)logits & 3u) || ((uintptr_t)ids & 1u) || ((uintptr_t)w & 3u))
         return fail(MOE_EINVAL, "moe_decode_stack: misaligned pointer (x, y need 16 bytes)");
     if (!ctx->stack_ok)
@@ -474,6 +515,7 @@ moe_status moe_decode_stack(moe_ctx *ctx, int layer0, int n_layers, const float 
     const int H = ctx->cfg.hidden, I = ctx->cfg.inter;
     StackArgs a{};
     a.layers = ctx->dlayers;
+    a.routers = ctx->drouters;
     a.layer0 = layer0;
     a.n_layers = n_layers;
     a.x = x;

@@ -108,11 +108,20 @@ struct PrefillArgs {
 constexpr int STK_CWAVES = 8;             // decode stack: 8 compute waves (two per SIMD),
 constexpr int STK_WAVES = STK_CWAVES + 3; // 1 router wave, 2 poller waves
 
+// A layer's router gate matrix as bound by moe_bind_router: [E][H] of element type `type`
+// (MOE_WG_*) in the caller's memory; wg null when none is bound.
+struct StackRouter {
+    const uint8_t *wg;
+    uint32_t type, pad;
+};
+static_assert(sizeof(StackRouter) == 16, "router table entry");
+
 struct StackArgs {
     const LayerPtrs *layers; // device table indexed by absolute layer
+    const StackRouter *routers; // device table indexed by absolute layer (activation routing)
     int layer0, n_layers;
     const float *x;          // [H] input activation
-    const float *logits;     // [n_layers][E]
+    const float *logits;     // [n_layers][E], or null: every layer routed from its input (routers)
     float *y;                // [H] output activation (may alias x)
     uint16_t *ids_out;       // [n_layers][9] or null
     float *w_out;            // [n_layers][9] or null
@@ -199,11 +208,14 @@ hipError_t launch_stack(int H, int I, const StackArgs &a, hipStream_t st, Kernel
 // MOE_DEVFLAG_TIMEOUT, the decode stack's state -- `stack_words` words from `stack` on, its
 // control words and both exchange sets -- is zeroed as well (recovery after an expired wait).
 hipError_t launch_flags_take(uint32_t *flags, uint32_t *dst, uint32_t *stack, size_t stack_words, hipStream_t st);
-hipError_t stack_occupancy(int H, int I, int *blocks_per_cu);
+// ar: the activation-routed form of the kernel (StackArgs::logits null).
+hipError_t stack_occupancy(int H, int I, bool ar, int *blocks_per_cu);
 int stack_blocks(int H);
 // Words of one layer block of a decode-stack exchange set: per XCD the h words (3I), the
-// partial of every output row (H), and x' as int8 pair words + chunk scales + per-workgroup
-// sums of squares (H/2 + H/32 + H/64).
+// partial of every output row (H), x' as int8 pair words + chunk scales + per-workgroup
+// sums of squares (H/2 + H/32 + H/64), and the layer's router logits (STK_LG_WORDS, used by
+// the activation-routed form only).
+constexpr int STK_LG_WORDS = 256;
 size_t stack_layer_words(int H, int I);
 
 // Tiles: the PF_BM-slot tiles of every expert, then each expert's remainder (above

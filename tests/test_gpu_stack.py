@@ -301,3 +301,206 @@ def test_rebind_refreshes_copies(gpu, small):
     finally:
         ctx.bind_packed(0, layers[0])  # the module's other tests use the original layer 0
         fresh.close()
+
+
+# ---------------------------------------------------------------- activation-routed stack
+
+def plane_logit_bound(orc, W, xin):
+    """Largest error the stack's int8-plane activations can put on a logit: element k of a
+    32-element chunk c is off by at most max_c |xin| / (127 * 512), so logit e is off by at most
+    sum_c max_c|xin| / 65024 * sum_{k in c} |W_ek|."""
+    Wd = (orc.dequant(W).astype(np.float64) if W.dtype == np.uint8 else W.astype(np.float64))
+    nexp = xin.shape[-1] and (Wd.size // xin.shape[-1])
+    Wd = np.abs(Wd.reshape(nexp, -1))
+    cmax = np.abs(xin.astype(np.float64)).reshape(-1, 32).max(axis=1) / 65024.0
+    return float((Wd.reshape(nexp, -1, 32).sum(axis=2) * cmax[None, :]).sum(axis=1).max())
+
+
+def oracle_chain_routed(orc, layers_dev, routers, hidden, inter, nexp, x0, gpu_ids, gpu_w, rmsnorm=True,
+                        mode=0):
+    """The oracle chain routed from each layer's own input: logits = orc.router_gemv(Wg_l, xin)
+    (xin = RMSNorm(x) when asked), top-8 by orc.router_topk, then the FFN.  With lb the
+    layer's int8-plane logit error bound (plane_logit_bound, plus f32 rounding): where the
+    oracle's 8th and 9th logits are more than 2 lb apart, the GPU's ids must equal the
+    oracle's and its weights agree to 2.5 lb relative (a logit error d moves a softmax weight by
+    at most 2 max|d| relative, to first order); a closer pair is a near-tie that may break
+    either way, and the GPU's routing is followed.  Returns (y, layers checked)."""
+    x = np.array(x0, dtype=np.float32).reshape(1, hidden)
+    eb = 3 * (hidden * inter // 256 * 136)
+    host = np.zeros((nexp + 1) * eb, dtype=np.uint8)
+    checked = 0
+    for l, dev in enumerate(layers_dev):
+        lg = orc.router_gemv(routers[l], x, nexp, flags=orc.RMSNORM if rmsnorm else 0)
+        xin = x / np.sqrt((x.astype(np.float64) ** 2).mean() + 1e-6) if rmsnorm else x
+        lb = plane_logit_bound(orc, routers[l], xin) + 1e-6 * np.abs(lg).max()
+        rid, rw = orc.router_topk(lg, mode)
+        top9 = -np.sort(-lg[0])[:9]
+        if top9[7] - top9[8] > 2 * lb:
+            assert np.array_equal(gpu_ids[l], rid[0]), (l, gpu_ids[l], rid[0])
+            assert np.allclose(gpu_w[l], rw[0], rtol=2.5 * lb + 1e-5, atol=0), (l, lb)
+            ids, w = rid, rw
+            checked += 1
+        else:
+            # a near-tie: every expert the GPU chose is within 2 lb of the oracle's 8th logit,
+            # and it chose 8 distinct routed experts and the shared one
+            g = gpu_ids[l][:8].astype(np.int64)
+            assert len(set(g.tolist())) == 8 and gpu_ids[l][8] == nexp, l
+            assert np.all(lg[0][g] >= top9[7] - 2 * lb), (l, lg[0][g], top9[7], lb)
+            ids, w = gpu_ids[l:l + 1], gpu_w[l:l + 1]
+        for e in ids[0]:
+            host[int(e) * eb:(int(e) + 1) * eb] = dev[int(e) * eb:(int(e) + 1) * eb].cpu().numpy()
+        L = orc.PackedLayer(host, hidden, inter, nexp)
+        flags = orc.ACCUMULATE | (orc.RMSNORM if rmsnorm else 0)
+        x = orc.moe_ffn(L, x, ids, w, 1.0 / 9 if mode == 0 else 1.0, flags, y=x)
+    return x.reshape(-1), checked
+
+
+def make_routers(gpu, hidden, nexp, n, seed, kinds=("iq4", "f32", "f16")):
+    """n router gate matrices [nexp][hidden], cycling through the element types: (device
+    tensors, host arrays for the oracle)."""
+    import torch
+    rng = np.random.default_rng(seed)
+    dev, host = [], []
+    for l in range(n):
+        kind = kinds[l % len(kinds)]
+        if kind == "iq4":
+            t = gpu.gen_iq4xs(nexp * hidden // 256, seed + 17 * l)
+            torch.cuda.synchronize()
+            h = t.cpu().numpy()
+        else:
+            h = (rng.standard_normal((nexp, hidden)) * 0.05).astype(np.float32 if kind == "f32" else np.float16)
+            t = torch.from_numpy(h).cuda()
+        dev.append(t)
+        host.append(h)
+    return dev, host
+
+
+@pytest.mark.parametrize("layer0,n,rmsnorm", [(0, 1, True), (0, 6, True), (2, 3, True), (0, 2, False)])
+def test_small_stack_routed_from_activations(gpu, orc, small, layer0, n, rmsnorm):
+    """MOE_STACK_ROUTE_GEMV: every layer routed from its own input through its bound router
+    (IQ4_XS, f32 and f16 matrices in turn), against the oracle chain with orc.router_gemv."""
+    import torch
+    ctx, layers, (hidden, inter, nexp) = small
+    rdev, rhost = make_routers(gpu, hidden, nexp, 6, 7100)
+    try:
+        for l in range(6):
+            ctx.bind_router(l, rdev[l])
+        log(f"stack routed from activations, small H={hidden} layers {layer0}..{layer0 + n - 1} "
+            f"rmsnorm={rmsnorm}")
+        x = gpu.gen_normal(hidden, 7200 + n)
+        ids = torch.empty((n, 9), dtype=torch.uint16, device="cuda")
+        w = torch.empty((n, 9), dtype=torch.float32, device="cuda")
+        y = ctx.decode_stack(layer0, x, ids=ids, w=w, rmsnorm=rmsnorm, n_layers=n)
+        torch.cuda.synchronize()
+        assert ctx.device_flags() == 0
+        ref, checked = oracle_chain_routed(orc, layers[layer0:layer0 + n], rhost[layer0:layer0 + n], hidden, inter,
+                                           nexp, x.cpu().numpy(), ids.cpu().numpy(), w.cpu().numpy(),
+                                           rmsnorm=rmsnorm)
+        log(f"  routing checked on {checked} of {n} layers")
+        assert checked >= (n + 1) // 2
+        check_errs(y.cpu().numpy(), ref, True, tol=TOL, ew_tol=EW_STACK)
+    finally:
+        for l in range(6):
+            ctx.bind_router(l, None)
+
+
+@pytest.fixture(scope="module")
+def full_routers(gpu, full):
+    ctx, _ = full
+    rdev, rhost = make_routers(gpu, H, E, 40, 7300)
+    for l in range(40):
+        ctx.bind_router(l, rdev[l])
+    yield rdev, rhost
+    for l in range(40):
+        ctx.bind_router(l, None)
+
+
+def test_config2_forty_layers_routed_from_activations(gpu, orc, full, full_routers):
+    """Config 2 as a forward pass: 40 layers, each routed from its own RMSNorm'd input by its
+    router (IQ4_XS, f32, f16 in turn), against the oracle chain."""
+    import torch
+    ctx, layers = full
+    rdev, rhost = full_routers
+    log("config 2 routed from activations: 40-layer stack, M=1")
+    x = gpu.gen_normal(H, gpu.seed_for(2, 0, gpu.TAG_X) + 7)
+    ids = torch.empty((40, 9), dtype=torch.uint16, device="cuda")
+    w = torch.empty((40, 9), dtype=torch.float32, device="cuda")
+    y = ctx.decode_stack(0, x, ids=ids, w=w, n_layers=40)
+    torch.cuda.synchronize()
+    assert ctx.device_flags() == 0
+    ref, checked = oracle_chain_routed(orc, layers, rhost, H, I, E, x.cpu().numpy(), ids.cpu().numpy(),
+                                       w.cpu().numpy())
+    log(f"  routing checked on {checked} of 40 layers")
+    assert checked >= 30
+    check_errs(y.cpu().numpy(), ref, True, tol=TOL, ew_tol=EW_STACK)
+
+
+def test_routed_stack_matches_per_layer_path(gpu, full, full_routers):
+    """The activation-routed stack against the per-layer calls it replaces:
+    moe_router_gemv_topk_typed (RMSNorm) then moe_ffn (RMSNorm, ACCUMULATE), layer by layer.
+    The stack reads x as int8 planes where the per-layer path reads f32: ids equal on these
+    layers, outputs within the stack-vs-per-layer bound."""
+    import torch
+    ctx, _ = full
+    rdev, _ = full_routers
+    n = 6
+    x = gpu.gen_normal(H, 7401)
+    ids = torch.empty((n, 9), dtype=torch.uint16, device="cuda")
+    w = torch.empty((n, 9), dtype=torch.float32, device="cuda")
+    y = ctx.decode_stack(8, x, ids=ids, w=w, n_layers=n)
+    xr = x.clone().view(1, H)
+    pids = []
+    for l in range(n):
+        _, i_l, w_l = ctx.router_gemv_topk(rdev[8 + l], xr, rmsnorm=True, want_logits=False)
+        pids.append(i_l.clone())
+        ctx.ffn(8 + l, xr, i_l, w_l, y=xr, accumulate=True, rmsnorm=True)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, torch.cat(pids))
+    err = normwise_err(y.cpu().numpy(), xr.view(-1).cpu().numpy())
+    log(f"  routed stack vs per-layer normwise diff {err:.3e}")
+    assert err <= 2e-4
+
+
+def test_routed_stack_graph_replays_and_timeout(gpu, full, full_routers):
+    """Graph replays of the activation-routed stack equal the eager result bit for bit; a
+    host-forced timeout leaves an in-place x untouched, and the context then runs normally."""
+    import torch
+    ctx, _ = full
+    x = gpu.gen_normal(H, 7501)
+    eager = ctx.decode_stack(0, x, n_layers=8).clone()
+    torch.cuda.synchronize()
+    y = torch.empty_like(x)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ctx.decode_stack(0, x, y=y, n_layers=8)
+    for _ in range(3):
+        y.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int32), eager.view(torch.int32))
+        assert ctx.device_flags() == 0
+    xi = x.clone()
+    ctx.stack_spin_limit(0)
+    try:
+        log("routed stack with spin limit 0 (forced timeout), in place")
+        ctx.decode_stack(0, xi, y=xi, n_layers=8)
+        torch.cuda.synchronize()
+        assert ctx.device_flags() & gpu.DEVFLAG_TIMEOUT
+        assert torch.equal(xi.view(torch.int32), x.view(torch.int32))
+    finally:
+        ctx.stack_spin_limit(65536)
+    again = ctx.decode_stack(0, x, n_layers=8)
+    torch.cuda.synchronize()
+    assert ctx.device_flags() == 0
+    assert torch.equal(again.view(torch.int32), eager.view(torch.int32))
+
+
+def test_routed_stack_errors(gpu, full):
+    import torch
+    ctx, _ = full
+    x = torch.zeros(H, device="cuda")
+    ctx.bind_router(39, None)
+    with pytest.raises(gpu.MoeError, match="no bound router"):
+        ctx.decode_stack(38, x, n_layers=2)
+    with pytest.raises(gpu.MoeError):
+        ctx.bind_router(0, torch.zeros(E * H + 1, dtype=torch.float32, device="cuda")[1:])  # misaligned
