@@ -281,7 +281,7 @@ def leg_config0(torch, pkg, ctx, routers, eager):
 
 
 def leg_prefill(torch, pkg, ctx, PK, eager):
-    """Config 1: M = 512, Zipf(1.1)-biased logits, router + moe_ffn per step."""
+    """Config 1: M = 512, Zipf(1.1)-biased logits, moe_ffn_route (router + FFN) per step."""
     dev = torch.device("cuda:0")
     pw, pn = 3, 3 + PK
     xp = pkg.gen_normal(PREFILL_M * H, pkg.seed_for(1, 0, pkg.TAG_X)).view(PREFILL_M, H)
@@ -291,8 +291,8 @@ def leg_prefill(torch, pkg, ctx, PK, eager):
     pwt = torch.empty((pn, PREFILL_M, 9), dtype=torch.float32, device=dev)
 
     def prefill(s):
-        ctx.router_topk(plog[s], pids[s], pwt[s])
-        ctx.ffn(s % LAYERS, xp, pids[s], pwt[s], y=yp)
+        # moe_ffn_route: the routing runs inside the first prefill launch
+        ctx.ffn_route(s % LAYERS, xp, plog[s], y=yp, ids=pids[s], w=pwt[s])
 
     prefill(0)
     torch.cuda.synchronize()
@@ -313,7 +313,8 @@ def leg_prefill(torch, pkg, ctx, PK, eager):
     pgu_us = pkern["prefill_gate_up"]["avg_us"]
     pgu_tflops = (PREFILL_FLOPS * 2 / 3) / (pgu_us * 1e-6) / 1e12  # gate/up: 2/3 of the FLOPs
     return {"workload": "config 1: M=512, Zipf(1.1) router bias, one layer per step "
-                        "(cycling the 40 resident layers)",
+                        "(cycling the 40 resident layers); moe_ffn_route per step (routing inside the "
+                        "bucket-fill launch)",
             "dtype": "f16 MFMA (operands scaled by exact powers of two), f32 accumulate",
             "ms_per_step": round(p_ms, 5), "tok_per_s": round(PREFILL_M / (us * 1e-6), 1),
             "tflops": round(tflops, 2), "mfma_frac": round(tflops / F16_PEAK_TFLOPS, 4),
@@ -378,8 +379,7 @@ def leg_config4(torch, pkg, layer0, eager):
     w4 = torch.empty((n4, M4, 9), dtype=torch.float32, device=dev)
 
     def step4(s):
-        ctx4.router_topk(l4[s], i4[s], w4[s])
-        ctx4.ffn(0, x4, i4[s], w4[s], y=y4)
+        ctx4.ffn_route(0, x4, l4[s], y=y4, ids=i4[s], w=w4[s])
 
     step4(0)
     torch.cuda.synchronize()
@@ -397,7 +397,7 @@ def leg_config4(torch, pkg, layer0, eager):
     log(f"config 4, M={M4}: {us4:.1f} us/step, {M4 / (us4 * 1e-6):.0f} tok/s, {tf4:.1f} TFLOP/s = "
         f"{100 * tf4 / F16_PEAK_TFLOPS:.2f}% of the f16 MFMA peak; kernels {kern4}")
     return {"workload": "config 4: one layer, M=4096, N(0,1) logits with 5% of tokens forced onto one hot "
-                        "expert; router + moe_ffn per step",
+                        "expert; moe_ffn_route per step (routing inside the first launch)",
             "us_per_step": round(us4, 1), "tok_per_s": round(M4 / (us4 * 1e-6), 1),
             "tflops": round(tf4, 2), "mfma_frac": round(tf4 / F16_PEAK_TFLOPS, 4), "kernels": kern4}
 

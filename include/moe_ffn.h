@@ -117,8 +117,8 @@ moe_status moe_router_topk(moe_ctx *ctx, const float *logits, int M, uint16_t *i
 
 /* Router gate GEMV fused with the top-8: logits[t][e] = sum_k xin[t][k] * Wg[e][k], xin = x_t
  * or, with flags = MOE_FFN_RMSNORM, RMSNorm(x_t) (eps 1e-6, no gain); then ids/w exactly as
- * moe_router_topk computes them from those logits (for M <= MOE_DECODE_MAX_M in the GEMV's
- * own launch).  wg: IQ4_XS [n_experts][hidden] in the GGML layout (rows = experts, 16-byte
+ * moe_router_topk computes them from those logits (a second launch).  wg: IQ4_XS
+ * [n_experts][hidden] in the GGML layout (rows = experts, 16-byte
  * aligned device memory, read in place -- no binding; other element types:
  * moe_router_gemv_topk_typed);
  * x f32 [M][hidden]; logits f32 [M][n_experts] or NULL (then M <= m_max and the context's
@@ -136,8 +136,7 @@ enum { MOE_WG_F32 = 0, MOE_WG_F16 = 1, MOE_WG_IQ4_XS = 23 };
 /* moe_router_gemv_topk with the gate matrix's element type given: wg [n_experts][hidden] as
  * IQ4_XS super-blocks (MOE_WG_IQ4_XS), f32 (MOE_WG_F32) or f16 (MOE_WG_F16), row-major, rows
  * = experts, 16-byte aligned device memory, read in place.  f32 arithmetic (f16 weights
- * converted exactly).  For M <= MOE_DECODE_MAX_M with ids/w requested the GEMV and the top-8
- * are one launch; otherwise the top-8 is a second launch.  Replaces the Router GEMV dispatch
+ * converted exactly).  With ids/w the top-8 is a second launch.  Replaces the Router GEMV dispatch
  * (shaders/router.comp:21-61 at src/inference.rs:598-605) on the weight the loader found
  * (src/memory.rs:236-262 binds blk.L.ffn_gate) and, with ids/w, the RouterTopk dispatch and
  * do_route (src/inference.rs:608-659). */

@@ -72,21 +72,18 @@ hipError_t launch_router_topk(const float *logits, int M, int E, int renorm, uin
 // group's tokens before any is used) and a wave sum.  All f32: the weights are exact, so the
 // logits differ from an f64 sum by f32 rounding only.
 //
-// With FUSE (M <= 8 and ids requested) the same launch also routes: the last workgroup of a
-// token group to finish -- counted on ctr[group] after every wave's agent-scope release of
-// its logits -- takes an agent-scope acquire, routes the group's tokens (one wave each, as
-// k_router_topk, so the ids and weights equal moe_router_topk's of these logits bit for bit)
-// and resets the counter for the next launch.  No workgroup waits on another.
+// The top-8 follows as a k_router_topk launch.  Measured on MI355X, one launch for both at
+// M <= 8 -- the last workgroup of a token group routing it after the others' logits were
+// handed over through a device counter -- was slower than two launches in a graph: 8.8 us
+// at M = 1 with an agent-scope release / acquire pair (each writes back / invalidates the XCD's
+// whole L2), 6.2 us with write-through stores and system-scope loads instead, against 5.6 us.
 constexpr int RG_WAVES = 4; // experts per workgroup
 
 struct RouterGemvArgs {
     const void *wg;
     const float *x;
-    int M, E, rmsnorm, renorm;
+    int M, E, rmsnorm;
     float *logits;
-    uint16_t *ids; // FUSE only
-    float *w;
-    uint32_t *ctr; // FUSE only: one zero counter per token group (left zero)
 };
 
 // The lane's 32 weights of row e as f32 (dense types), or its codebook bytes and scale (IQ4_XS).
@@ -123,7 +120,7 @@ __device__ __forceinline__ void router_row_weights(const void *wg, int e, int sl
     }
 }
 
-template <int H, int RG_TM, int WT, bool FUSE>
+template <int H, int RG_TM, int WT>
 __global__ __launch_bounds__(64 * RG_WAVES) void k_router_gemv(RouterGemvArgs a) {
     constexpr int NSB = H / 32;
     static_assert(H % QK == 0 && NSB <= 64, "one sub-block per lane");
@@ -165,76 +162,43 @@ __global__ __launch_bounds__(64 * RG_WAVES) void k_router_gemv(RouterGemvArgs a)
             if (lane == 0 && t0 + i < M) a.logits[(size_t)(t0 + i) * E + e] = dot * inv;
         }
     }
-    if constexpr (FUSE) {
-        __shared__ int s_last;
-        // every wave's logits written back to memory before this workgroup is counted
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            const uint32_t done = __hip_atomic_fetch_add((MOE_GLOBAL uint32_t *)(a.ctr + blockIdx.y), 1u,
-                                                         __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-            s_last = done == gridDim.x - 1u;
-        }
-        __syncthreads();
-        if (!s_last) return;
-        // the last workgroup of the group: every other one's logits are visible after this
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        const int t = t0 + wv;
-        if (wv < RG_TM && t < M) {
-            int id;
-            float wt;
-            route_wave<4>(a.logits + (size_t)t * E, E, a.renorm, lane, id, wt);
-            if (lane < SLOTS) {
-                a.ids[(size_t)t * SLOTS + lane] = (uint16_t)id;
-                a.w[(size_t)t * SLOTS + lane] = wt;
-            }
-        }
-        if (threadIdx.x == 0)
-            __hip_atomic_store((MOE_GLOBAL uint32_t *)(a.ctr + blockIdx.y), 0u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    }
 }
 
 template <int H, int TM, int WT>
-static void launch_router_gemv_t(const RouterGemvArgs &a, bool fuse, hipStream_t st) {
+static void launch_router_gemv_t(const RouterGemvArgs &a, hipStream_t st) {
     const dim3 grid((unsigned)((a.E + RG_WAVES - 1) / RG_WAVES), (unsigned)((a.M + TM - 1) / TM));
-    if (fuse) hipLaunchKernelGGL((k_router_gemv<H, TM, WT, true>), grid, dim3(64 * RG_WAVES), 0, st, a);
-    else hipLaunchKernelGGL((k_router_gemv<H, TM, WT, false>), grid, dim3(64 * RG_WAVES), 0, st, a);
+    hipLaunchKernelGGL((k_router_gemv<H, TM, WT>), grid, dim3(64 * RG_WAVES), 0, st, a);
 }
 
 template <int H, int WT>
-static void launch_router_gemv_w(const RouterGemvArgs &a, bool fuse, hipStream_t st) {
+static void launch_router_gemv_w(const RouterGemvArgs &a, hipStream_t st) {
     // a wave's tokens past M repeat the last one: at small M fewer tokens per wave
-    if (a.M == 1) launch_router_gemv_t<H, 1, WT>(a, fuse, st);
-    else if (a.M == 2) launch_router_gemv_t<H, 2, WT>(a, fuse, st);
-    else launch_router_gemv_t<H, 4, WT>(a, fuse, st);
+    if (a.M == 1) launch_router_gemv_t<H, 1, WT>(a, st);
+    else if (a.M == 2) launch_router_gemv_t<H, 2, WT>(a, st);
+    else launch_router_gemv_t<H, 4, WT>(a, st);
 }
 
 template <int H>
-static void launch_router_gemv_h(int wtype, const RouterGemvArgs &a, bool fuse, hipStream_t st) {
-    if (wtype == MOE_WG_IQ4_XS) launch_router_gemv_w<H, MOE_WG_IQ4_XS>(a, fuse, st);
-    else if (wtype == MOE_WG_F32) launch_router_gemv_w<H, MOE_WG_F32>(a, fuse, st);
-    else launch_router_gemv_w<H, MOE_WG_F16>(a, fuse, st);
+static void launch_router_gemv_h(int wtype, const RouterGemvArgs &a, hipStream_t st) {
+    if (wtype == MOE_WG_IQ4_XS) launch_router_gemv_w<H, MOE_WG_IQ4_XS>(a, st);
+    else if (wtype == MOE_WG_F32) launch_router_gemv_w<H, MOE_WG_F32>(a, st);
+    else launch_router_gemv_w<H, MOE_WG_F16>(a, st);
 }
 
 hipError_t launch_router_gemv(int H, int wtype, const void *wg, const float *x, int M, int E, int rmsnorm,
-                              float *logits, int renorm, uint16_t *ids, float *w, uint32_t *ctr, hipStream_t st,
-                              KernelTimer *T) {
+                              float *logits, int renorm, uint16_t *ids, float *w, hipStream_t st, KernelTimer *T) {
     if (M <= 0) return hipSuccess;
     if (H != 2048 && H != 512) return hipErrorInvalidValue;
     if (wtype != MOE_WG_IQ4_XS && wtype != MOE_WG_F32 && wtype != MOE_WG_F16) return hipErrorInvalidValue;
     if (E < TOPK || E > 256) return hipErrorInvalidValue;
-    RouterGemvArgs a{wg, x, M, E, rmsnorm, renorm, logits, ids, w, ctr};
-    // one launch for the GEMV and the top-8 when M <= 8 (at most 8 token groups, one counter
-    // each); larger M: the GEMV, then k_router_topk's throughput form
-    const bool fuse = ids && M <= RG_FUSE_MAX_M;
+    RouterGemvArgs a{wg, x, M, E, rmsnorm, logits};
     {
         TimedLaunch tl(T, MOE_K_ROUTER_GEMV, st);
-        if (H == 2048) launch_router_gemv_h<2048>(wtype, a, fuse, st);
-        else launch_router_gemv_h<512>(wtype, a, fuse, st);
+        if (H == 2048) launch_router_gemv_h<2048>(wtype, a, st);
+        else launch_router_gemv_h<512>(wtype, a, st);
     }
     hipError_t he = hipGetLastError();
-    if (he == hipSuccess && ids && !fuse) he = launch_router_topk(logits, M, E, renorm, ids, w, st, T);
+    if (he == hipSuccess && ids) he = launch_router_topk(logits, M, E, renorm, ids, w, st, T);
     return he;
 }
 

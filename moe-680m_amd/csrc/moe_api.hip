@@ -25,7 +25,7 @@ struct moe_ctx {
     uint8_t *spk = nullptr;         // [n_layers][E+1][W1|W3|W2] split layout: the one resident copy
     void *arena = nullptr; // one device allocation, carved below
     size_t arena_bytes = 0;
-    uint32_t *flags = nullptr;   // 64 words: [0] sticky flags, [1] stack abort word, FLAG_RG_CTR..
+    uint32_t *flags = nullptr;   // [0] sticky device flags, [1] the decode stack's abort word
     float *hbuf = nullptr;       // decode path h scratch [72][I]
     _Float16 *xh = nullptr;      // [m_max][H]
     float *xinv = nullptr;       // [m_max]
@@ -333,7 +333,7 @@ moe_status moe_router_gemv_topk_typed(moe_ctx *ctx, const void *wg, int wg_type,
     float *lg = logits ? logits : ctx->logits;
     hipError_t he = launch_router_gemv(ctx->cfg.hidden, wg_type, wg, x, M, ctx->cfg.n_experts,
                                        (flags & MOE_FFN_RMSNORM) ? 1 : 0, lg, ctx->cfg.wmode == MOE_W_RENORM, ids, w,
-                                       ctx->flags + FLAG_RG_CTR, st, timer_for(ctx, st));
+                                       st, timer_for(ctx, st));
     if (he != hipSuccess) return hip_fail(he, "moe_router_gemv_topk: launch");
     return ok();
 }

@@ -188,17 +188,10 @@ hipError_t launch_gen_logits(float *dst, int M, int E, uint64_t seed, int kind, 
 hipError_t launch_router_topk(const float *logits, int M, int E, int renorm, uint16_t *ids,
                               float *w, hipStream_t st, KernelTimer *T);
 hipError_t launch_bucket_fill(const BucketArgs &a, hipStream_t st, KernelTimer *T);
-// Router gate GEMV on Wg of type wtype (MOE_WG_*), then -- with ids -- the top-8: in the same
-// launch for M <= RG_FUSE_MAX_M (ctr: RG_FUSE_MAX_M zero words, left zero), else in a
-// k_router_topk launch after it.
-constexpr int RG_FUSE_MAX_M = MOE_DECODE_MAX_M;
-// Words of the context's 64-word flags block: [0] sticky device flags, [1] the decode stack's
-// abort word, [FLAG_RG_CTR, FLAG_RG_CTR + RG_FUSE_MAX_M) the fused router's group counters.
-constexpr int FLAG_RG_CTR = 16;
-static_assert(FLAG_RG_CTR + RG_FUSE_MAX_M <= 64, "flags block");
+// Router gate GEMV on Wg of type wtype (MOE_WG_*), then -- with ids -- the top-8 (a
+// k_router_topk launch).
 hipError_t launch_router_gemv(int H, int wtype, const void *wg, const float *x, int M, int E, int rmsnorm,
-                              float *logits, int renorm, uint16_t *ids, float *w, uint32_t *ctr, hipStream_t st,
-                              KernelTimer *T);
+                              float *logits, int renorm, uint16_t *ids, float *w, hipStream_t st, KernelTimer *T);
 hipError_t launch_decode(int H, int I, const DecodeArgs &a, hipStream_t st, KernelTimer *T);
 // prep, one gate/up and one down launch over both tile lists, combine -- all on st.
 // Bucket fill and prep (one launch), gate/up, down, combine.

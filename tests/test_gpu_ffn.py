@@ -176,10 +176,11 @@ def test_renorm_flags(gpu, orc, full_renorm):
             assert err <= (TOL_DECODE if M <= 8 else TOL_PREFILL)
 
 
-@pytest.mark.parametrize("M", [1, 2, 5, 8, 9, 40])
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 9, 40, 512, 1000, 1025, 4096])
 def test_ffn_route_equals_router_then_ffn(gpu, full, M):
-    """moe_ffn_route (routing inside the FFN's first launch for M <= 8) gives the router's
-    ids and weights and the FFN's output bit for bit."""
+    """moe_ffn_route (routing inside the decode launches for M <= 8, a router launch before the
+    prefill launches beyond) gives the router's ids and weights and the FFN's output bit for
+    bit, on both bucket-fill paths (one workgroup up to M = 1024, many beyond)."""
     import torch
     ctx, _ = full
     log(f"ffn_route M={M}")
@@ -192,6 +193,41 @@ def test_ffn_route_equals_router_then_ffn(gpu, full, M):
     assert torch.equal(ids, ids2)
     assert torch.equal(w.view(torch.int32), w2.view(torch.int32))
     assert torch.equal(y.view(torch.int32), y_ref.view(torch.int32))
+    assert ctx.device_flags() == 0
+
+
+@pytest.mark.parametrize("M", [512, 1025])
+def test_ffn_route_prefill_graph_replays(gpu, full, M):
+    """Graph replays of the routed prefill (router launch, bucket fill, GEMMs, combine), with
+    eager calls of another M in between, equal the eager result bit for bit."""
+    import torch
+    ctx, _ = full
+    log(f"ffn_route prefill M={M}: graph capture, 3 replays")
+    x = gpu.gen_normal(M * H, 3700 + M).view(M, H)
+    logits = gpu.gen_logits(M, E, 3800 + M, 1, 1.1)
+    y0, i0, w0 = (t.clone() for t in ctx.ffn_route(0, x, logits))
+    x2 = gpu.gen_normal(64 * H, 3900).view(64, H)
+    l2 = gpu.gen_logits(64, E, 3901)
+    torch.cuda.synchronize()
+    y = torch.empty_like(y0)
+    ids = torch.empty_like(i0)
+    w = torch.empty_like(w0)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            ctx.ffn_route(0, x, logits, y=y, ids=ids, w=w, stream=s)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        y.fill_(float("nan"))
+        ids.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ids, i0) and torch.equal(w.view(torch.int32), w0.view(torch.int32)), rep
+        assert torch.equal(y.view(torch.int32), y0.view(torch.int32)), rep
+        ctx.ffn_route(0, x2, l2)
+        torch.cuda.synchronize()
     assert ctx.device_flags() == 0
 
 

@@ -144,8 +144,8 @@ def test_router_gemv_matches_oracle(gpu, orc, ctx, ctx_renorm, M, rmsnorm):
 @pytest.mark.parametrize("M", [1, 2, 8, 9, 64])
 @pytest.mark.parametrize("dense", [np.float32, np.float16])
 def test_router_gemv_dense_matches_oracle(gpu, orc, ctx, ctx_renorm, M, dense):
-    """Unquantized gate matrices (a GGUF ffn_gate_inp as llama.cpp leaves it): M <= 8 routes in
-    the GEMV's own launch, M > 8 in a second one."""
+    """Unquantized gate matrices (a GGUF ffn_gate_inp as llama.cpp leaves it), f32 and f16, at
+    M from 1 to 64 (1, 2 and 4 tokens per wave)."""
     log(f"router gemv dense {np.dtype(dense).name} E={E} H=2048 M={M}")
     _router_gemv_case(gpu, orc, ctx if M % 2 else ctx_renorm, E, 2048, M, 0x52480000 + M, True, dense=dense)
 
@@ -182,12 +182,11 @@ def test_router_gemv_outputs_and_errors(gpu, orc, ctx):
                                   None) == gpu.MOE_EINVAL
 
 
-def test_router_gemv_fused_graph_replays(gpu, ctx):
-    """The one-launch GEMV + top-8 (M <= 8) counts finished workgroups on device counters that
-    its last workgroup resets: replays of a captured call, with eager calls of other M in
-    between, each give the eager result bit for bit."""
+def test_router_gemv_graph_replays(gpu, ctx):
+    """Replays of a captured moe_router_gemv_topk (GEMV + top-8), with eager calls of another
+    M in between, each give the eager result bit for bit."""
     import torch
-    log("router gemv fused: graph capture, 4 replays")
+    log("router gemv + top-8: graph capture, 4 replays")
     wg = gpu.gen_iq4xs(E * 2048 // 256, 0x5249)
     x = gpu.gen_normal(3 * 2048, 0x524A).view(3, 2048)
     x5 = gpu.gen_normal(5 * 2048, 0x524B).view(5, 2048)
