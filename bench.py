@@ -148,6 +148,71 @@ def profiled_traffic():
     return None
 
 
+# ---------------------------------------------------------------- decode stack timeline
+
+# Events of one (workgroup, layer) record, in moe_stack_trace's order (k_stack.hip).
+EV = {"start": 0, "x": 1, "routed": 2, "a": 3, "hpoll": 4, "h": 5, "b": 6, "pub": 7, "gather": 8,
+      "xpub": 9, "xpoll": 10}
+TRACE_EV = 16
+# (name, from event, to event) of a layer's phases, all on one workgroup
+PHASES = (("route (activation routing)", "x", "routed"), ("phase A", "x", "a"),
+          ("phase A (after routing)", "routed", "a"), ("h exchange to B2", "a", "h"),
+          ("phase B", "h", "b"), ("B3 + partial publish", "b", "pub"),
+          ("cross-XCD partial gather", "pub", "gather"), ("reduce + x publish", "gather", "xpub"))
+
+
+def stack_timeline(torch, pkg, ctx, routers, n_tok, routed):
+    """Per-phase timeline of moe_decode_stack from the trace build (MOE680M_TRACE=1): n_tok
+    tokens through the 40 layers (seeded logits, or routed from the activations); returns the
+    per-phase medians over workgroups, averaged over layers 1..38 and the tokens."""
+    import numpy as np
+    nb = H // 8
+    buf = torch.zeros(nb * LAYERS * TRACE_EV, dtype=torch.int64, device="cuda")
+    x = pkg.gen_normal(H, pkg.seed_for(2, 0, pkg.TAG_X))
+    logits = pkg.gen_logits(n_tok * LAYERS, E, pkg.seed_for(2, 0, pkg.TAG_L)).view(n_tok, LAYERS, E)
+    if routed:
+        for l in range(LAYERS):
+            ctx.bind_router(l, routers[l])
+    ctx.decode_stack(0, x, None if routed else logits[0], y=x, n_layers=LAYERS)  # warm
+    torch.cuda.synchronize()
+    ctx.stack_trace(buf)
+    rows = []
+    for t in range(n_tok):
+        buf.zero_()
+        ctx.decode_stack(0, x, None if routed else logits[t], y=x, n_layers=LAYERS)
+        torch.cuda.synchronize()
+        rows.append(buf.view(nb, LAYERS, TRACE_EV).cpu().numpy().astype(np.float64) * 10.0)  # 100 MHz -> ns
+    ctx.stack_trace(None)
+    assert ctx.device_flags() == 0
+    if routed:
+        for l in range(LAYERS):
+            ctx.bind_router(l, None)
+    ph = {name: [] for name, _, _ in PHASES}
+    layer_ns, kernel_ns = [], []
+    for tr in rows:
+        t0 = tr[:, 0, EV["start"]].min()
+        kernel_ns.append(tr[:, LAYERS - 1, EV["xpub"]].max() - t0)
+        xs = tr[:, :, EV["x"]].max(axis=0)   # x of layer l in LDS on the last workgroup
+        layer_ns += list(np.diff(xs)[1:-1])
+        for name, a, b in PHASES:
+            if name.startswith("route") or name.endswith("(after routing)"):
+                if not routed:
+                    continue
+            elif name == "phase A" and routed:
+                continue
+            d = tr[:, 1:LAYERS - 1, EV[b]] - tr[:, 1:LAYERS - 1, EV[a]]
+            ph[name].append(float(np.median(d)))
+    out = {name: round(float(np.mean(v)) / 1e3, 3) for name, v in ph.items() if v}
+    return {"tokens": n_tok, "routed_from_activations": routed,
+            "kernel_us": round(float(np.mean(kernel_ns)) / 1e3, 2),
+            "layer_us_median": round(float(np.median(layer_ns)) / 1e3, 3),
+            "layer_us_mean": round(float(np.mean(layer_ns)) / 1e3, 3),
+            "phase_us_median_over_workgroups": out,
+            "what": "s_memrealtime stamps (100 MHz) by lane 0 of the named wave of every workgroup; a layer = "
+                    "the time between the last workgroup's x of consecutive layers; phases are medians over "
+                    "the 256 workgroups, averaged over layers 1..38"}
+
+
 # ---------------------------------------------------------------- legs
 
 def leg_decode(torch, pkg, ctx, K, W, eager):
@@ -415,6 +480,9 @@ def main():
     ap.add_argument("--only", choices=LEGS,
                     help="run this leg alone with eager launches (no graphs, no JSON line): "
                          "the program profiled by rocprofv3")
+    ap.add_argument("--stack-timeline", type=int, default=0, metavar="TOKENS",
+                    help="print the decode stack's per-phase timeline over this many tokens (seeded and "
+                         "activation-routed) from the trace build libmoe680m_trace.so, and nothing else")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="run a plain device copy of this size first (scales PMC byte counters)")
     args = ap.parse_args()
@@ -424,6 +492,8 @@ def main():
             "(the sharding design is in DESIGN.md); run with --gpus 1")
         sys.exit(2)
 
+    if args.stack_timeline:
+        os.environ["MOE680M_TRACE"] = "1"   # the package then loads libmoe680m_trace.so
     import torch
     pkg = load_pkg()
     torch.cuda.set_device(0)
@@ -453,6 +523,14 @@ def main():
     torch.cuda.synchronize()
     log(f"generated {LAYERS} layers x {E + 1} experts ({LAYERS * (E + 1) * EXPERT_BYTES / 1e9:.2f} GB) "
         f"in {time.perf_counter() - t0:.2f} s")
+
+    if args.stack_timeline:
+        for routed in (False, True):
+            tl = stack_timeline(torch, pkg, ctx, routers, args.stack_timeline, routed)
+            log(f"stack timeline: {tl}")
+            print(json.dumps(tl), flush=True)
+        ctx.close()
+        return
 
     if args.only:
         eager = True

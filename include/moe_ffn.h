@@ -232,6 +232,14 @@ moe_status moe_device_flags_async(moe_ctx *ctx, uint32_t *dst, void *stream);
  * which every workgroup still exits normally.  No reference counterpart. */
 moe_status moe_stack_spin_limit(moe_ctx *ctx, uint32_t polls);
 
+/* Per-phase timeline of moe_decode_stack (profiling hook; no reference counterpart).  In a
+ * library built with MOE_STACK_TRACE (libmoe680m_trace.so) every later moe_decode_stack
+ * launch of this context stores, per workgroup, layer and event, the 100 MHz device clock
+ * into buf (device memory, `words` u64: hidden/8 workgroups x n_layers x 16 events; the event
+ * numbering is k_stack.hip's StackTraceEvent).  buf = NULL stops it.  Other builds return
+ * MOE_EUNSUPPORTED. */
+moe_status moe_stack_trace(moe_ctx *ctx, uint64_t *buf, size_t words);
+
 /* Last error message of the calling thread ("" when none). */
 const char *moe_last_error(void);
 

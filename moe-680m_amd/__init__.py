@@ -22,7 +22,10 @@ import os
 import torch  # must precede the library load: it brings the process's HIP runtime
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libmoe680m.so")
+# MOE680M_TRACE=1 loads the same library built with the decode stack's per-phase timeline
+# (moe_stack_trace); results are identical, launches slightly slower.
+LIB_PATH = os.path.join(_HERE, "libmoe680m_trace.so" if os.environ.get("MOE680M_TRACE") == "1"
+                        else "libmoe680m.so")
 
 QK = 256
 SB_BYTES = 136
@@ -44,7 +47,7 @@ EXPORTS = (
     "moe_create", "moe_destroy", "moe_bind_layer", "moe_bind_router", "moe_router_topk", "moe_router_gemv_topk",
     "moe_router_gemv_topk_typed", "moe_bucket_fill",
     "moe_ffn", "moe_ffn_route", "moe_ffn_noalloc", "moe_decode_stack", "moe_dequant_iq4xs", "moe_device_flags",
-    "moe_device_flags_async", "moe_stack_spin_limit", "moe_last_error",
+    "moe_device_flags_async", "moe_stack_spin_limit", "moe_stack_trace", "moe_last_error",
     "moe_timing_enable", "moe_timing_read",
     "moe_gen_iq4xs", "moe_gen_normal", "moe_gen_logits",
 )
@@ -101,6 +104,7 @@ def lib():
         "moe_device_flags": [vp, vp, ctypes.POINTER(ctypes.c_uint32)],
         "moe_device_flags_async": [vp, vp, vp],
         "moe_stack_spin_limit": [vp, ctypes.c_uint32],
+        "moe_stack_trace": [vp, vp, sz],
         "moe_gen_iq4xs": [vp, sz, u64, u64, vp],
         "moe_gen_normal": [vp, sz, u64, u64, ctypes.c_float, ctypes.c_float, vp],
         "moe_gen_logits": [vp, i, i, u64, i, ctypes.c_double, ctypes.c_double, vp],
@@ -332,6 +336,11 @@ class Context:
 
     def stack_spin_limit(self, polls):
         _check(lib().moe_stack_spin_limit(self._h, polls))
+
+    def stack_trace(self, buf):
+        """Record decode_stack's per-phase timeline into buf (a device int64 tensor of
+        hidden/8 x n_layers x 16 words), or stop with None (MOE680M_TRACE=1 builds only)."""
+        _check(lib().moe_stack_trace(self._h, _ptr(buf), 0 if buf is None else buf.numel()))
 
     def timing_enable(self, capacity=4096):
         _check(lib().moe_timing_enable(self._h, capacity))

@@ -64,6 +64,38 @@
 
 namespace moe {
 
+// Per-phase timeline (a build with -DMOE_STACK_TRACE, libmoe680m_trace.so; moe_stack_trace):
+// lane 0 of the named wave stores the 100 MHz device clock (s_memrealtime, one clock for every
+// CU) at each event of each layer into trace[(workgroup * n_layers + layer) * STK_TRACE_EV +
+// event].  Other builds compile the marks away.
+enum StackTraceEvent {
+    STK_EV_START = 0,   // router wave: past B0 (layer 0 only)
+    STK_EV_X = 1,       // first poller: past B1 (x_l in LDS)
+    STK_EV_ROUTED = 2,  // compute wave 0: past BR (activation routing only)
+    STK_EV_A = 3,       // compute wave 0: phase A stored
+    STK_EV_HPOLL = 4,   // second poller: its h wait satisfied
+    STK_EV_H = 5,       // compute wave 0: past B2 (h_l in LDS)
+    STK_EV_B = 6,       // compute wave 0: phase B done
+    STK_EV_PUB = 7,     // first poller: partial published (past B3)
+    STK_EV_GATHER = 8,  // first poller: the eight partials gathered
+    STK_EV_XPUB = 9,    // first poller: x_{l+1} published (or y stored, last layer)
+    STK_EV_XPOLL = 10,  // second poller: its x_{l+1} wait satisfied
+    STK_TRACE_EV_USED = 11
+};
+static_assert(STK_TRACE_EV_USED <= STK_TRACE_EV, "trace record");
+#ifdef MOE_STACK_TRACE
+#define STK_MARK(ev, li)                                                                                          \
+    do {                                                                                                          \
+        if (a.trace && lane == 0)                                                                                 \
+            a.trace[((size_t)blockIdx.x * a.n_layers + (size_t)(li)) * STK_TRACE_EV + (ev)] =                    \
+                __builtin_amdgcn_s_memrealtime();                                                                 \
+    } while (0)
+#else
+#define STK_MARK(ev, li) \
+    do {                 \
+    } while (0)
+#endif
+
 constexpr int STK_NX = 8;   // XCDs
 constexpr uint32_t STK_DONE_ABORT = 1u << 16; // a done-count contribution that vetoes the y store
 
@@ -71,6 +103,7 @@ constexpr uint32_t STK_DONE_ABORT = 1u << 16; // a done-count contribution that 
 __device__ __forceinline__ void tag_store_local(uint32_t *p, float v) {
     *(MOE_GLOBAL uint32_t *)p = __builtin_bit_cast(uint32_t, v) | 1u;
 }
+
 
 // LDS index of word k with 4 pad words after every 32 (conflict-free 128-bit reads of a
 // lane's 32-float chunk).
@@ -404,6 +437,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             if (blockIdx.x == 0 && lane == 0)
                 __hip_atomic_store((MOE_GLOBAL uint32_t *)ctl(STK_CTL_DIRTY + (int)(ep & 1u)), (uint32_t)n,
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            STK_MARK(STK_EV_START, 0);
             clear_other(0, n + 1);
             const int nq = E4 >> 2;
             for (int li = 0; li < n; ++li) {
@@ -461,6 +495,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 __hip_atomic_store((MOE_GLOBAL uint32_t *)ctl(STK_CTL_DIRTY + (int)(ep & 1u)), (uint32_t)n,
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (n > 2) fetch(2);
+            STK_MARK(STK_EV_START, 0);
             // window 0 follows B0, window li + 1 follows B3 of layer li; window w routes layer w + 2
             for (int wdw = 0; wdw <= n; ++wdw) {
                 if (wdw > 0) {
@@ -518,6 +553,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         float xres = first ? a.x[ROWS * j + lane] : 0.f;
         for (int li = 0; li < n; ++li) {
             lds_barrier(); // B1: x_li in LDS
+            if (first) STK_MARK(STK_EV_X, li);
             if constexpr (AR) lds_barrier(); // BR: the layer's routing in LDS
             // the h exchange: ahead of the compute waves' phase-B lookups (priority 0), level
             // with phase A (priority 1; the older compute waves win the ties)
@@ -536,6 +572,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                     v[m] = ok ? ld(q[m]) : u32x4{1u, 1u, 1u, 1u};
                 }
                 got = poll_until_tagged<4>(v, q, ld, a.flags, atag, a.spin_max, abort_lds) && got;
+                if (!first) STK_MARK(STK_EV_HPOLL, li);
                 if (first) {
                     if (lane < I / NX) {
                         float g = 0.f, u = 0.f;
@@ -577,12 +614,14 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 const float pv = part[0][lane] + part[1][lane];
                 const int ab = *abort_lds;
                 if (got && !ab) tag_store(pb + (size_t)k * H + ROWS * j + lane, pv);
+                STK_MARK(STK_EV_PUB, li);
                 // ... gather all eight (lane: quad lane&15 of XCDs lane>>4 and (lane>>4)+4) ...
                 const RemoteQuads ld{reinterpret_cast<const u32x4 *>(pb + ROWS * j)};
                 const int m = lane >> 4, qq = lane & 15;
                 int q[2] = {m * (H / 4) + qq, (m + 4) * (H / 4) + qq};
                 u32x4 v[2] = {ld(q[0]), ld(q[1])};
                 got = poll_until_tagged<2>(v, q, ld, a.flags, atag, a.spin_max, abort_lds) && got;
+                STK_MARK(STK_EV_GATHER, li);
                 *reinterpret_cast<f32x4 *>(&ps[m][4 * qq]) = __builtin_bit_cast(f32x4, v[0]);
                 *reinterpret_cast<f32x4 *>(&ps[m + 4][4 * qq]) = __builtin_bit_cast(f32x4, v[1]);
                 // lanes read what other lanes of this wave wrote: LDS keeps a wave's
@@ -616,6 +655,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                         if ((lane & 31) == 0) tag_store_local(xb + H / 2 + (row >> 5), am * (1.0f / 127.0f));
                         if (lane == 0) tag_store_local(xb + H / 2 + H / 32 + j, ss);
                     }
+                    STK_MARK(STK_EV_XPUB, li);
                 } else if (k == 0) {
                     // y is written by all of XCD 0's reducers or by none.  Nothing computed
                     // from a wait that gave up is ever published (a wave publishes only after
@@ -636,6 +676,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                         *(MOE_GLOBAL float *)(a.y + row) = x1;
                     else if (c != 0u && lane == 0)
                         set_flag(a.flags, MOE_DEVFLAG_TIMEOUT); // a count past NJ: not every reducer was sound
+                    STK_MARK(STK_EV_XPUB, li);
                     // The last of XCD 0's reducers to leave resets the two counts and advances
                     // the epoch, which switches the next launch to the exchange set this launch
                     // cleared.  By then every workgroup of the launch has started (each of them
@@ -669,6 +710,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 // pair words are tagged by being nonzero; the scales and sums of squares
                 // are LSB-tagged f32 words, which are nonzero too
                 got = poll_until_tagged<XP>(v, q, ld, a.flags, atag, a.spin_max, abort_lds, NonzeroTag{}) && got;
+                if (!first) STK_MARK(STK_EV_XPOLL, li);
 #pragma unroll
                 for (int m = 0; m < XP; ++m) {
                     if (q[m] < XD) {
@@ -968,6 +1010,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             // experts' weights, requested only now
             router_dot(li);
             lds_barrier(); // BR: routing of li in LDS
+            if (w == 0) STK_MARK(STK_EV_ROUTED, li);
             prefetch_a(li);
             __builtin_amdgcn_s_setprio(1);
             prefetch_b(li);
@@ -1030,8 +1073,10 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 tag_store_local(hb + I + ((j * SRP + pA) * NCW + w) * 2 + mA, sp);
         }
         __builtin_amdgcn_s_setprio(0);
+        if (w == 0) STK_MARK(STK_EV_A, li);
         decode_b();
         lds_barrier(); // B2: h_l in LDS; routing of layer li+2 in LDS
+        if (w == 0) STK_MARK(STK_EV_H, li);
         if constexpr (!AR) prefetch_a(min(li + 1, n - 1));
         // nothing of phase B above the burst: its first use of this layer's W2 registers
         // then waits for those loads only, not for everything (stores included) in flight
@@ -1069,6 +1114,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             ds = adjacent_sum<LPRB>(ds);
             if (lane % LPRB == 0 && lane < NSB) part[1][8 * w + rB] = wsh * ds;
         }
+        if (w == 0) STK_MARK(STK_EV_B, li);
         lds_barrier(); // B3: contributions in LDS
         // the pollers now gather the partials and exchange x: decode layer li+1's phase-A
         // weights (requested at B2) meanwhile -- or, AR, request layer li+1's router rows

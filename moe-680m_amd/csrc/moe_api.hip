@@ -49,6 +49,8 @@ struct moe_ctx {
     int stack_ok_ar = 0;         // ... and those of its activation-routed form
     int ncu = 0;                 // compute units of the device
     uint32_t spin_max = STK_SPIN_DEFAULT; // decode stack: poll rounds before a wait expires
+    uint64_t *trace = nullptr;   // decode stack timeline buffer (MOE_STACK_TRACE builds)
+    size_t trace_words = 0;
     KernelTimer timer;
 };
 
@@ -533,6 +535,13 @@ moe_status moe_decode_stack(moe_ctx *ctx, int layer0, int n_layers, const float 
     a.rmsnorm = (flags & MOE_FFN_RMSNORM) ? 1 : 0;
     a.renorm = ctx->cfg.wmode == MOE_W_RENORM;
     a.c = ctx->cfg.wmode == MOE_W_REF ? 1.0f / 9.0f : 1.0f;
+    a.trace = nullptr;
+    if (ctx->trace) {
+        if ((size_t)stack_blocks(H) * n_layers * STK_TRACE_EV > ctx->trace_words)
+            return fail(MOE_EINVAL, "moe_decode_stack: %d layers do not fit the trace buffer (%zu words)", n_layers,
+                        ctx->trace_words);
+        a.trace = ctx->trace;
+    }
     hipStream_t st = as_stream(stream);
     hipError_t he = launch_stack(H, I, a, st, timer_for(ctx, st));
     if (he != hipSuccess) return hip_fail(he, "moe_decode_stack: launch");
@@ -628,6 +637,21 @@ moe_status moe_device_flags_async(moe_ctx *ctx, uint32_t *dst, void *stream) {
     hipError_t he = launch_flags_take(ctx->flags, dst, ctx->xtag, ctx->xtag_words, as_stream(stream));
     if (he != hipSuccess) return hip_fail(he, "moe_device_flags_async: launch");
     return ok();
+}
+
+moe_status moe_stack_trace(moe_ctx *ctx, uint64_t *buf, size_t words) {
+    if (!ctx) return fail(MOE_EINVAL, "moe_stack_trace: null context");
+#ifdef MOE_STACK_TRACE
+    if (buf && ((uintptr_t)buf & 7u)) return fail(MOE_EINVAL, "moe_stack_trace: buffer not 8-byte aligned");
+    ctx->trace = buf;
+    ctx->trace_words = buf ? words : 0;
+    return ok();
+#else
+    (void)buf;
+    (void)words;
+    return fail(MOE_EUNSUPPORTED, "moe_stack_trace: this library was built without MOE_STACK_TRACE "
+                                  "(libmoe680m_trace.so has it)");
+#endif
 }
 
 moe_status moe_stack_spin_limit(moe_ctx *ctx, uint32_t polls) {

@@ -136,7 +136,9 @@ struct StackArgs {
     uint32_t spin_max;       // poll rounds before a bounded wait expires
     int E, rmsnorm, renorm;
     float c;
+    uint64_t *trace;         // -DMOE_STACK_TRACE builds: [NB][n_layers][STK_TRACE_EV] clocks, or null
 };
+constexpr int STK_TRACE_EV = 16; // words per (workgroup, layer) of a stack trace
 
 constexpr uint32_t STK_SPIN_DEFAULT = 1u << 16;
 // Control words of the decode stack, each on its own 128-byte line: one workgroup ticket
