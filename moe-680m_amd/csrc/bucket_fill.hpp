@@ -134,30 +134,12 @@ __device__ __forceinline__ BucketScan bucket_scan_lds(uint32_t *p, int E1) {
     return BucketScan{p, p + (E1 + 1), p + 2 * (E1 + 1), p + 3 * (E1 + 1), p + 4 * (E1 + 1)};
 }
 
-// Phases 2a/2b and the lists: exclusive scan of each bucket's chunk counts in place, bucket
-// totals, ranges, and the tile lists.  Every thread of the workgroup; ends with a barrier.
-// 2a loads B counts at a time as independent loads before any is overwritten.
-template <int B>
-__device__ __forceinline__ void bucket_scan_and_lists(const BucketArgs &a, CntLayout CL, int nch, BucketScan S) {
+// Phase 2b and the lists, from the bucket totals in S.tot: scans over buckets (ranges, tile
+// counts) into S, and -- when write -- the ranges and the tile lists to global memory.  Every
+// thread of the workgroup; ends with a barrier.
+__device__ __forceinline__ void bucket_lists(const BucketArgs &a, BucketScan S, bool write) {
     const int E1 = a.E1;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    for (int e = tid; e < E1; e += BF_THREADS) {
-        uint32_t run = 0;
-        for (int c0 = 0; c0 < nch; c0 += B) {
-            uint32_t v[B];
-            // every load unconditional (the index clamped, the value dropped below)
-#pragma unroll
-            for (int j = 0; j < B; ++j) v[j] = CL.at(c0 + j < nch ? c0 + j : nch - 1, e);
-#pragma unroll
-            for (int j = 0; j < B; ++j)
-                if (c0 + j < nch) {
-                    CL.at(c0 + j, e) = run;
-                    run += v[j];
-                }
-        }
-        S.tot[e] = run;
-    }
-    __syncthreads();
     // 2b: scans over buckets (one wave each): ranges; full big tiles; partial big tiles;
     // small tiles.  Big tiles are listed full ones first, so the long work items start first.
     if (wv < 4) {
@@ -179,8 +161,9 @@ __device__ __forceinline__ void bucket_scan_and_lists(const BucketArgs &a, CntLa
     }
     __syncthreads();
 
-    for (int e = tid; e <= E1; e += BF_THREADS) a.ranges[e] = S.rg[e];
-    if (a.tiles) {
+    if (write)
+        for (int e = tid; e <= E1; e += BF_THREADS) a.ranges[e] = S.rg[e];
+    if (write && a.tiles) {
         // one list: full tiles, big remainders, then small remainders, then empty entries up to
         // tile_max (every expert has at most one remainder, so the tiles never exceed it)
         const uint32_t nfull = S.ts[E1], nbig = nfull + S.tp[E1];
@@ -198,6 +181,33 @@ __device__ __forceinline__ void bucket_scan_and_lists(const BucketArgs &a, CntLa
         for (int i = (int)(nbig + S.tsm[E1]) + tid; i < a.tile_max; i += BF_THREADS) a.tiles[i] = Tile{-1, 0, 0, 0};
     }
     __syncthreads();
+}
+
+// Phases 2a/2b and the lists: exclusive scan of each bucket's chunk counts in place, bucket
+// totals, ranges, and the tile lists.  Every thread of the workgroup; ends with a barrier.
+// 2a loads B counts at a time as independent loads before any is overwritten.
+template <int B>
+__device__ __forceinline__ void bucket_scan_and_lists(const BucketArgs &a, CntLayout CL, int nch, BucketScan S) {
+    const int E1 = a.E1;
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E1; e += BF_THREADS) {
+        uint32_t run = 0;
+        for (int c0 = 0; c0 < nch; c0 += B) {
+            uint32_t v[B];
+            // every load unconditional (the index clamped, the value dropped below)
+#pragma unroll
+            for (int j = 0; j < B; ++j) v[j] = CL.at(c0 + j < nch ? c0 + j : nch - 1, e);
+#pragma unroll
+            for (int j = 0; j < B; ++j)
+                if (c0 + j < nch) {
+                    CL.at(c0 + j, e) = run;
+                    run += v[j];
+                }
+        }
+        S.tot[e] = run;
+    }
+    __syncthreads();
+    bucket_lists(a, S, true);
 }
 
 // ---- one workgroup, at most bucket_cw(E1) chunks: every chunk has its own bitmap set (one

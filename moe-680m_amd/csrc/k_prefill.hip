@@ -3,12 +3,13 @@
 // Replaces the reference's bucketed prefill dispatches (src/inference.rs:683-732): per
 // non-empty bucket a tiled w1_w3_fused GEMM into an f16 scratch and a w2_scatter GEMM
 // whose epilogue read-modify-writes the f16 hidden state (shaders/w1_w3_fused.comp,
-// shaders/w2_scatter.comp).  Here, after the bucket fill has produced expert-sorted slots
-// and a list of tiles (up to PF_BM slots of one expert):
+// shaders/w2_scatter.comp).  Here, after the chain's bucket fill (k_pf_count, k_pf_place,
+// below) has produced expert-sorted slots and a list of tiles (up to PF_BM slots of one
+// expert):
 //   prep:    per token, x (RMSNorm fused when asked) times a power of two s_t that puts
 //            max|x| in [2^14, 2^15), stored as f16 with K permuted inside 32-blocks (the
 //            order the weight nibbles arrive in, see below); 1/s_t kept per token -- run in
-//            the same launch as the bucket fill (k_pf_route_prep), which does not need it;
+//            the same launch as the slot placement (k_pf_place), which does not need it;
 //   gate_up: per (tile, 64 gate/up column pairs; 128 when M > 768) a workgroup of 8 waves,
 //            two per CU; the tile's token rows (gathered -- the reference's kernel skipped
 //            this gather) are resident in LDS one 64 KB chunk of K at a time and shared by the
@@ -191,28 +192,124 @@ __device__ __forceinline__ void prep_token(const PrefillArgs &a, int t, int lane
     if (lane == 0) a.xinv[t] = inv_s;
 }
 
-// The chain's first launch: the first workgroups run the bucket fill, the others the prep of
-// one token per wave -- independent work that would otherwise be two launches in a row.
-// ONE: 1024-thread workgroups, workgroup 0 runs the one-workgroup fill (M <= 1024), the
-// others 16 tokens each; else 64-thread workgroups, the first ceil(M/64) count one chunk
-// each (the scan and the scatter follow as their own launches), the others one token each.
-template <int H, bool ONE>
-__global__ __launch_bounds__(ONE ? BF_THREADS : BF_CHUNK_THREADS) void k_pf_route_prep(BucketArgs b, PrefillArgs a) {
-    static_assert(H % (32 * 64) == 0 || H == 512, "prep shape");
-    constexpr int TPW = (ONE ? BF_THREADS : BF_CHUNK_THREADS) / 64; // tokens per prep workgroup
-    const int nfill = ONE ? 1 : (b.M + 63) / 64;
-    if ((int)blockIdx.x < nfill) {
-        if constexpr (ONE) bucket_fill_one_wg(b);
-        else bucket_count_chunk(b, blockIdx.x);
-        return;
+// ---------------------------------------------------------------- the chain's bucket fill
+// Replaces router::build_expert_batches (src/router.rs:55-97) inside the prefill chain, where
+// only the tiles, each slot's sorted position and the sorted tokens and weights are needed --
+// and where a slot's place inside its bucket changes no result (every GEMM row, its scaling
+// and its partial are computed from that row alone, and the combine sums a token's slots in
+// slot order).  So the slots are ranked by an atomic counter per bucket rather than in token
+// order (moe_bucket_fill, the drop-in for build_expert_batches, keeps the token order), and the
+// fill takes two launches of many workgroups whatever M is:
+//   k_pf_count: one wave per token routes it (with logits, as k_router_topk) or reads its ids,
+//       applies the pair rule (an id above n_experts, or one its token named in an earlier slot,
+//       is dropped and flagged) and ranks each kept slot in its bucket: inside the workgroup by
+//       an LDS counter, then by one add per touched bucket to the bucket's global counter;
+//   k_pf_place: every placing workgroup scans the E + 1 counts itself (ranges; workgroup 0 also
+//       writes the tile lists) and places its share of the slots -- sorted token, weight and
+//       position -- with the prep of PF_PREP_TOKENS tokens per workgroup in the others.
+// The counters start at zero and k_pf_combine, the chain's last launch, zeroes them again.
+// The shared expert's bucket has no counter: token t's shared row is row t of it.
+constexpr int PF_COUNT_TOKENS = 16; // tokens per counting workgroup (one wave each; 4 measured slower at M = 4096)
+constexpr uint32_t PF_SLOT_HOLE = 0xFFFFFFFEu; // slot 8 of a token with no kept shared slot
+
+template <bool ROUTE>
+__global__ __launch_bounds__(64 * PF_COUNT_TOKENS) void k_pf_count(PfCountArgs c) {
+    // Routed experts: per-workgroup bucket counts in LDS first, then one global add per bucket
+    // the workgroup touched.  The shared expert's bucket takes no count: every token has one
+    // row in it, at rank t -- its kept shared slot, or (only when its ids name no valid shared
+    // slot) a hole row of weight 0 that no token reads back.  An add per shared slot would
+    // serialise M adds on one counter.
+    __shared__ uint32_t hist[MOE_MAX_EXPERTS + 1], base[MOE_MAX_EXPERTS + 1];
+    const int lane = threadIdx.x & 63, E1 = c.E + 1;
+    for (int e = threadIdx.x; e < E1; e += 64 * PF_COUNT_TOKENS) hist[e] = 0u;
+    __syncthreads();
+    const int t = blockIdx.x * PF_COUNT_TOKENS + (int)(threadIdx.x >> 6);
+    const bool tok = t < c.M; // whole waves
+    int id = 0;
+    if (tok) {
+        if constexpr (ROUTE) {
+            float wt;
+            route_wave<4>(c.logits + (size_t)t * c.E, c.E, c.renorm, lane, id, wt);
+            if (lane < SLOTS) {
+                c.ids[(size_t)t * SLOTS + lane] = (uint16_t)id;
+                c.w[(size_t)t * SLOTS + lane] = wt;
+            }
+        } else {
+            id = lane < SLOTS ? (int)c.ids[(size_t)t * SLOTS + lane] : 0;
+        }
     }
-    const int t = ((int)blockIdx.x - nfill) * TPW + (int)(threadIdx.x >> 6);
-    if (t < a.M) prep_token<H>(a, t, threadIdx.x & 63); // whole waves
+    const bool bad = tok && lane < SLOTS && id > c.E;
+    bool dup = false;
+#pragma unroll
+    for (int s = 0; s < SLOTS - 1; ++s) {
+        const int o = __builtin_amdgcn_readlane(id, s);
+        dup = dup || (tok && s < lane && lane < SLOTS && !bad && o == id);
+    }
+    const bool keep = tok && lane < SLOTS && !bad && !dup;
+    const uint64_t nb = __ballot(bad), nd = __ballot(dup), ns = __ballot(keep && id == c.E);
+    if (lane == 0 && (nb | nd))
+        set_flag(c.flags, (nb ? (uint32_t)MOE_DEVFLAG_BAD_ID : 0u) | (nd ? (uint32_t)MOE_DEVFLAG_DUP_ID : 0u));
+    const bool routed = keep && id != c.E;
+    uint32_t rank = routed ? atomicAdd(&hist[id], 1u) : 0u;
+    __syncthreads();
+    for (int e = threadIdx.x; e < E1; e += 64 * PF_COUNT_TOKENS) {
+        const uint32_t n = hist[e];
+        base[e] = n ? __hip_atomic_fetch_add((MOE_GLOBAL uint32_t *)(c.cnt + e), n, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT)
+                    : 0u;
+    }
+    __syncthreads();
+    if (tok && lane < SLOTS) {
+        uint32_t info = 0xFFFFFFFFu;
+        if (routed) info = ((uint32_t)id << PF_SLOT_RANK_BITS) | (base[id] + rank);
+        else if (keep) info = ((uint32_t)c.E << PF_SLOT_RANK_BITS) | (uint32_t)t; // the shared slot
+        else if (lane == SLOTS - 1 && !ns) info = PF_SLOT_HOLE;
+        c.slot[(size_t)t * SLOTS + lane] = info;
+    }
 }
 
-// The many-workgroup fill's scan and scatter (after k_pf_route_prep's counts).
-__global__ __launch_bounds__(BF_THREADS) void k_pf_bucket_scan(BucketArgs b) { bucket_scan_wg(b); }
-__global__ __launch_bounds__(BF_CHUNK_THREADS) void k_pf_scatter(BucketArgs b) { bucket_scatter_chunk(b, blockIdx.x); }
+// Slots per placing workgroup (one per thread) and tokens per prep workgroup (its first four
+// waves; the others leave at once): both are bound by the CU's address unit -- scattered
+// 2- and 4-byte stores, and per wave 64 cache lines touched by each of a token's 8 loads and 4
+// stores -- so they are spread over many CUs (measured, M = 512: 9.1 us for the launch with
+// 4096 slots and 16 tokens per workgroup).
+constexpr int PF_PLACE_SLOTS = 1024;
+constexpr int PF_PREP_TOKENS = 4;
+
+template <int H>
+__global__ __launch_bounds__(BF_THREADS) void k_pf_place(BucketArgs b, PfCountArgs c, PrefillArgs a) {
+    const int nplace = (SLOTS * b.M + PF_PLACE_SLOTS - 1) / PF_PLACE_SLOTS;
+    const int blk = (int)blockIdx.x, tid = (int)threadIdx.x;
+    if (blk >= nplace) {
+        const int wv = tid >> 6, t = (blk - nplace) * PF_PREP_TOKENS + wv;
+        if (wv < PF_PREP_TOKENS && t < a.M) prep_token<H>(a, t, tid & 63); // whole waves
+        return;
+    }
+    extern __shared__ uint32_t smem[];
+    const int E1 = b.E1;
+    const BucketScan S = bucket_scan_lds(smem, E1);
+    for (int e = tid; e < E1; e += BF_THREADS) S.tot[e] = e == E1 - 1 ? (uint32_t)b.M : ldg<uint32_t>(c.cnt + e);
+    __syncthreads();
+    bucket_lists(b, S, blk == 0);
+    const int n = SLOTS * b.M, i0 = blk * PF_PLACE_SLOTS, i1 = min(i0 + PF_PLACE_SLOTS, n);
+    for (int i = i0 + tid; i < i1; i += BF_THREADS) {
+        const uint32_t info = ldg<uint32_t>(c.slot + i);
+        const float wv = ldg<float>(c.w + i);
+        const int t = i / SLOTS;
+        uint32_t p = 0xFFFFFFFFu;
+        if (info == PF_SLOT_HOLE) {
+            // the token's shared row, unused: a valid token index, weight 0
+            const uint32_t q = S.rg[E1 - 1] + (uint32_t)t;
+            b.sorted_tok[q] = (uint16_t)t;
+            b.sorted_w[q] = 0.0f;
+        } else if (info != 0xFFFFFFFFu) {
+            p = S.rg[info >> PF_SLOT_RANK_BITS] + (info & ((1u << PF_SLOT_RANK_BITS) - 1u));
+            b.sorted_tok[p] = (uint16_t)t;
+            b.sorted_w[p] = wv;
+        }
+        b.pos[i] = p;
+    }
+}
 
 // ---------------------------------------------------------------- shared pipeline pieces
 // A wave-uniform pointer moved to SGPRs (loads then take a scalar base and a lane offset).
@@ -697,6 +794,9 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
 template <int H>
 __global__ __launch_bounds__(256) void k_pf_combine(PrefillArgs a) {
     const int t = blockIdx.x;
+    // the chain's bucket counters, read by k_pf_place (an earlier launch), start over at zero
+    if (t == 0 && a.cnt)
+        for (int e = threadIdx.x; e <= a.E; e += 256) a.cnt[e] = 0u;
     uint32_t ps[SLOTS];
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) ps[s] = a.pos[(size_t)t * SLOTS + s];
@@ -731,20 +831,21 @@ __global__ __launch_bounds__(256) void k_pf_combine(PrefillArgs a) {
 }
 
 template <int H, int I>
-static hipError_t launch_prefill_t(const BucketArgs &b, const PrefillArgs &a, hipStream_t st, KernelTimer *T) {
+static hipError_t launch_prefill_t(const BucketArgs &b, const PfCountArgs &c, const PrefillArgs &a, hipStream_t st,
+                                   KernelTimer *T) {
+    // the chain's own fill: count (routing first with logits), then place + prep
+    {
+        TimedLaunch tl(T, c.logits ? MOE_K_ROUTER_TOPK : MOE_K_BUCKET_FILL, st);
+        const dim3 grid((unsigned)((c.M + PF_COUNT_TOKENS - 1) / PF_COUNT_TOKENS));
+        if (c.logits) hipLaunchKernelGGL(k_pf_count<true>, grid, dim3(64 * PF_COUNT_TOKENS), 0, st, c);
+        else hipLaunchKernelGGL(k_pf_count<false>, grid, dim3(64 * PF_COUNT_TOKENS), 0, st, c);
+    }
     {
         TimedLaunch tl(T, MOE_K_BUCKET_FILL, st);
-        if (bucket_one_wg(b.M, b.E1)) {
-            const dim3 grid((unsigned)(1 + (a.M + BF_THREADS / 64 - 1) / (BF_THREADS / 64)));
-            hipLaunchKernelGGL((k_pf_route_prep<H, true>), grid, dim3(BF_THREADS), bucket_smem_one(b.E1, b.M), st, b, a);
-        } else {
-            const int nch = (b.M + 63) / 64;
-            const size_t smem = bucket_chunk_smem(b.E1);
-            hipLaunchKernelGGL((k_pf_route_prep<H, false>), dim3((unsigned)(nch + a.M)), dim3(BF_CHUNK_THREADS), smem,
-                               st, b, a);
-            hipLaunchKernelGGL(k_pf_bucket_scan, dim3(1), dim3(BF_THREADS), bucket_smem(b.E1, false), st, b);
-            hipLaunchKernelGGL(k_pf_scatter, dim3((unsigned)nch), dim3(BF_CHUNK_THREADS), smem, st, b);
-        }
+        const int nplace = (SLOTS * b.M + PF_PLACE_SLOTS - 1) / PF_PLACE_SLOTS;
+        const int nprep = (a.M + PF_PREP_TOKENS - 1) / PF_PREP_TOKENS;
+        hipLaunchKernelGGL((k_pf_place<H>), dim3((unsigned)(nplace + nprep)), dim3(BF_THREADS),
+                           5 * (size_t)(b.E1 + 1) * 4, st, b, c, a);
     }
     // one launch over the tile list (full and big remainder tiles, then small remainders, then
     // empty entries, which exit at once)
@@ -767,9 +868,10 @@ static hipError_t launch_prefill_t(const BucketArgs &b, const PrefillArgs &a, hi
     return hipGetLastError();
 }
 
-hipError_t launch_prefill(int H, int I, const BucketArgs &b, const PrefillArgs &a, hipStream_t st, KernelTimer *T) {
-    if (H == 2048 && I == 512) return launch_prefill_t<2048, 512>(b, a, st, T);
-    if (H == 512 && I == 256) return launch_prefill_t<512, 256>(b, a, st, T);
+hipError_t launch_prefill(int H, int I, const BucketArgs &b, const PfCountArgs &c, const PrefillArgs &a,
+                          hipStream_t st, KernelTimer *T) {
+    if (H == 2048 && I == 512) return launch_prefill_t<2048, 512>(b, c, a, st, T);
+    if (H == 512 && I == 256) return launch_prefill_t<512, 256>(b, c, a, st, T);
     return hipErrorInvalidValue;
 }
 

@@ -39,6 +39,8 @@ struct moe_ctx {
     float *sw = nullptr;         // [9 m_max]
     uint32_t *pos = nullptr;     // [m_max][9]
     uint32_t *chunk = nullptr;   // [ceil(m_max/64)][E+1]
+    uint32_t *pcnt = nullptr;    // [E+1] the prefill chain's bucket counters (zero between calls)
+    uint32_t *pslot = nullptr;   // [9 m_max] the prefill chain's slot bucket and rank
     Tile *tiles = nullptr;       // [tile_max(m_max)]
     LayerPtrs *dlayers = nullptr; // device layer table of the split copies (decode stack)
     StackRouter *drouters = nullptr;   // device table of the bound router matrices
@@ -156,6 +158,8 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
         {(void **)&c->sw, SLOTS * mm * 4},
         {(void **)&c->pos, mm * SLOTS * 4},
         {(void **)&c->chunk, nchunk * E1 * 4},
+        {(void **)&c->pcnt, E1 * 4},
+        {(void **)&c->pslot, SLOTS * mm * 4},
         {(void **)&c->tiles, tmax * sizeof(Tile)},
         {(void **)&c->dlayers, (size_t)cfg->n_layers * sizeof(LayerPtrs)},
         {(void **)&c->drouters, (size_t)cfg->n_layers * sizeof(StackRouter)},
@@ -191,6 +195,7 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
     he = hipMemset(c->flags, 0, 256);
     if (he == hipSuccess) he = hipMemset(c->dlayers, 0, (size_t)cfg->n_layers * sizeof(LayerPtrs));
     if (he == hipSuccess) he = hipMemset(c->drouters, 0, (size_t)cfg->n_layers * sizeof(StackRouter));
+    if (he == hipSuccess) he = hipMemset(c->pcnt, 0, E1 * 4);
     // the decode stack's control words and both exchange sets start zeroed
     if (he == hipSuccess) he = hipMemset(c->xtag, 0, c->xtag_words * 4);
     if (he == hipSuccess) he = hipDeviceSynchronize();
@@ -417,10 +422,17 @@ static moe_status ffn_call(const char *fn, moe_ctx *ctx, int layer, const float 
         if (he != hipSuccess) return fail(MOE_EHIP, "%s: decode launch: %s", fn, hipGetErrorString(he));
         return ok();
     }
-    if (logits) {
-        he = launch_router_topk(logits, M, E, renorm, ids, w, st, T);
-        if (he != hipSuccess) return fail(MOE_EHIP, "%s: router launch: %s", fn, hipGetErrorString(he));
-    }
+    // with logits the chain's first launch routes the tokens (into ids / w) as it counts them
+    PfCountArgs pc{};
+    pc.logits = logits;
+    pc.ids = ids;
+    pc.w = w;
+    pc.M = M;
+    pc.E = E;
+    pc.renorm = renorm;
+    pc.cnt = ctx->pcnt;
+    pc.slot = ctx->pslot;
+    pc.flags = ctx->flags;
     BucketArgs b{};
     b.ids = ids;
     b.w = w;
@@ -454,7 +466,8 @@ static moe_status ffn_call(const char *fn, moe_ctx *ctx, int layer, const float 
     p.rmsnorm = (flags & MOE_FFN_RMSNORM) ? 1 : 0;
     p.tile_max = b.tile_max;
     p.c = c;
-    he = launch_prefill(H, I, b, p, st, T);
+    p.cnt = ctx->pcnt;
+    he = launch_prefill(H, I, b, pc, p, st, T);
     if (he != hipSuccess) return fail(MOE_EHIP, "%s: prefill launch: %s", fn, hipGetErrorString(he));
     return ok();
 }

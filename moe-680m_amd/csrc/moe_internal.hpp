@@ -82,6 +82,20 @@ struct BucketArgs {
     uint32_t *flags;
 };
 
+// The prefill chain's own bucket fill (k_pf_count, k_pf_place): slots placed by an atomic rank
+// inside their bucket, not in token order -- no row of the GEMMs depends on its position, so
+// the output is the same bit for bit -- in two launches of many workgroups.
+struct PfCountArgs {
+    const float *logits; // [M][E]: routed here into ids / w; null: ids / w given
+    uint16_t *ids;       // [M][9]
+    float *w;            // [M][9]
+    int M, E, renorm;
+    uint32_t *cnt;       // [E + 1] bucket counters: zero on entry (k_pf_combine zeroes them)
+    uint32_t *slot;      // [9M] (bucket << 23) | rank in the bucket, or ~0 for a dropped slot
+    uint32_t *flags;
+};
+constexpr int PF_SLOT_RANK_BITS = 23; // ranks < 9 * 65535 < 2^23
+
 // Prefill reads the split copy of a layer (k_repack_split), as the decode kernels do.
 struct PrefillArgs {
     LayerPtrs L;
@@ -103,6 +117,7 @@ struct PrefillArgs {
     float *y;
     int M, E, accumulate, rmsnorm, tile_max;
     float c;
+    uint32_t *cnt;       // the fill's bucket counters: zeroed by k_pf_combine for the next call
 };
 
 constexpr int STK_CWAVES = 8;             // decode stack: 8 compute waves (two per SIMD),
@@ -197,7 +212,8 @@ hipError_t launch_router_gemv(int H, int wtype, const void *wg, const float *x, 
 hipError_t launch_decode(int H, int I, const DecodeArgs &a, hipStream_t st, KernelTimer *T);
 // prep, one gate/up and one down launch over both tile lists, combine -- all on st.
 // Bucket fill and prep (one launch), gate/up, down, combine.
-hipError_t launch_prefill(int H, int I, const BucketArgs &b, const PrefillArgs &a, hipStream_t st, KernelTimer *T);
+hipError_t launch_prefill(int H, int I, const BucketArgs &b, const PfCountArgs &c, const PrefillArgs &a,
+                          hipStream_t st, KernelTimer *T);
 hipError_t launch_stack(int H, int I, const StackArgs &a, hipStream_t st, KernelTimer *T);
 // *dst = the sticky device flags, which are cleared (stream ordered).  When they hold
 // MOE_DEVFLAG_TIMEOUT, the decode stack's state -- `stack_words` words from `stack` on, its

@@ -263,7 +263,9 @@ def test_prefill_dropped_slots_skip_nonfinite_row0(gpu, orc, full):
     """Prefill (M = 16): token 0 routes to expert 0 in slot 0, so its partial output is
     expert-sorted row 0, and its activations are +inf (that row is non-finite).  Token 1 names
     one expert twice and an id above n_experts: its dropped slots must add nothing -- not 0
-    times row 0, which would be NaN -- so every token but token 0 still matches the oracle."""
+    times row 0, which would be NaN -- so every token but token 0 still matches the oracle.
+    Token 2 names no valid id (its output is 0), token 3 the shared expert in a routed slot
+    (its slot 8 is the repeat that is dropped)."""
     import torch
     ctx, layer = full
     M = 16
@@ -276,6 +278,8 @@ def test_prefill_dropped_slots_skip_nonfinite_row0(gpu, orc, full):
     ids_h[0, 0] = 0
     ids_h[1, 4] = ids_h[1, 1]   # duplicate inside token 1
     ids_h[1, 6] = E + 5         # out of range
+    ids_h[2, :] = E + 7         # token 2: no valid slot at all (not even the shared one)
+    ids_h[3, 2] = E             # token 3 names the shared expert in a routed slot: slot 8 repeats it
     ids_bad = torch.from_numpy(ids_h.astype(np.uint16)).cuda()
     x[0] = float("inf")
     y = ctx.ffn(0, x, ids_bad, w).clone()
@@ -483,8 +487,10 @@ def test_kernel_timing_hook(gpu, full):
     ctx.ffn(0, xp, idp, wp)
     t = ctx.timing_read()
     assert t["router_topk"][0] == 2 and t["decode_gate_up"][0] == 1 and t["decode_down"][0] == 1
-    # the prefill chain: bucket fill and prep in one launch, then gate/up, down, combine
-    for k in ("bucket_fill", "prefill_gate_up", "prefill_down", "prefill_combine"):
+    # the prefill chain with ids given: the bucket count, the placement with the prep, then
+    # gate/up, down, combine
+    assert t["bucket_fill"][0] == 2 and t["bucket_fill"][1] > 0
+    for k in ("prefill_gate_up", "prefill_down", "prefill_combine"):
         assert t[k][0] == 1 and t[k][1] > 0
     assert ctx.timing_read() == {}
     ctx.timing_enable(0)
