@@ -260,7 +260,7 @@ enum {
     MOE_K_PREFILL_COMBINE = 6,
     MOE_K_DECODE_STACK = 7,    /* moe_decode_stack: its one persistent launch (routing included) */
     MOE_K_ROUTER_GEMV = 8,     /* moe_router_gemv_topk: the GEMV launch (its top-8 is ROUTER_TOPK) */
-    MOE_K_DECODE_PREP = 9,     /* moe_ffn / moe_ffn_route, 2 <= M <= 8: routing, plan, int8 activations */
+    MOE_K_DECODE_PREP = 9,     /* moe_ffn / moe_ffn_route, 5 <= M <= 8: routing, plan, int8 activations */
     MOE_K_COUNT = 10
 };
 moe_status moe_timing_enable(moe_ctx *ctx, int capacity);

@@ -4,9 +4,9 @@
 // w1_w3_fused_m1 GEMV and a w2_scatter_m1 GEMV (shaders/w1_w3_fused_m1.comp,
 // shaders/w2_scatter_m1.comp), 18 dispatches and 18 barriers per layer, with SiLU fused
 // into the down projection and the combine done as an f16 read-modify-write of the hidden
-// state.  Here one layer is two launches at M = 1 and three at 2 <= M <= 8, with no waits
+// state.  Here one layer is two launches at M <= 4 and three at 5 <= M <= 8, with no waits
 // between workgroups:
-//   prep (M >= 2) = one workgroup per token, once per call: its routing when the call passed
+//   prep (M >= 5) = one workgroup per token, once per call: its routing when the call passed
 //            logits (ids and w are published), its pair validity, its activations as int8
 //            planes (quant4) and its RMSNorm factor -- the token's row of a plan block in the
 //            scratch.
@@ -17,14 +17,15 @@
 //            and decoded once per call, whatever the number of tokens sharing it.  At M = 1
 //            every wave routes the token itself (the top-8 code of moe_router_topk, so all
 //            agree bit for bit) and quantizes x into registers: no plan, no barrier, and the
-//            shared expert first in slot order.  Beyond, each workgroup copies the tokens'
-//            plan rows into LDS, numbers the selected experts in slot order with the tokens
-//            each serves, and keeps two rounds of loads in flight.  h = silu(g) * u goes to a
+//            shared expert first in slot order.  Beyond, each workgroup routes the tokens
+//            and quantizes their activations into LDS itself (M <= 4: a wave per token) or
+//            copies their plan rows (M >= 5), numbers the selected experts in slot order with
+//            the tokens each serves, and keeps two rounds of loads in flight.  h = silu(g) * u goes to a
 //            [9M][I] f32 scratch.
 //   down    = at M = 1, 8 output rows per workgroup, wave s taking slot s; beyond, one
 //            workgroup per (token, 8 * MT output rows), the token's h rows quantized into
 //            int8 planes in LDS and its (slot, 8-row block) units dealt to eight waves, each
-//            requesting all its W2 rows at once.  Every pair's contribution c * w * (W2 h)
+//            requesting all its W2 rows at once (and computing each unit as its rows arrive).  Every pair's contribution c * w * (W2 h)
 //            goes to LDS and a token's 9 contributions are summed in slot order
 //            (deterministic, no atomics), the residual added in the same store.
 // A single launch with a device-side h exchange between the two roles was built and measured
@@ -354,33 +355,127 @@ __global__ __launch_bounds__(256) void k_dec_prep(DecodeArgs a) {
     }
 }
 
+// Maximum over each group of 8 consecutive lanes (non-negative values), in every lane.
+__device__ __forceinline__ float group_max8(float v) {
+    v = fmaxf(v, dpp_mov<0xB1>(v));  // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_mov<0x4E>(v));  // quad_perm [2,3,0,1]
+    return fmaxf(v, dpp_mov<0x141>(v)); // row_half_mirror
+}
+
 // Pairs before q (q < 128) set in the two-word mask m.
 __device__ __forceinline__ int rank2(uint64_t m0, uint64_t m1, int q) {
     return q < 64 ? __popcll(m0 & ((1ull << q) - 1ull)) : __popcll(m0) + __popcll(m1 & ((1ull << (q - 64)) - 1ull));
 }
 
 // ---------------------------------------------------------------- gate/up, 2 <= M <= 8
-// Each workgroup copies the tokens' rows of the plan block and the pairs' ids into LDS (one
-// round of loads), numbers the selected experts in slot order with the tokens each serves
-// (k_dec_prep left that to it, so no prep workgroup waits for another), then each wave runs
-// its steps with two rounds of G steps' loads in flight.
-template <int H, int I, int MT>
+// INL (M <= 4): each workgroup routes the tokens itself (the top-8 of moe_router_topk, one
+// wave per token; workgroup 0 publishes ids, w and the valid-slot masks for the down launch)
+// and quantizes their activations into LDS -- no prep launch.  Otherwise (5 <= M <= 8, where
+// every workgroup quantizing all the tokens would cost more than the prep launch) it copies
+// the tokens' rows of the plan block k_dec_prep wrote and the pairs' ids into LDS (one round
+// of loads).  Then it numbers the selected experts in slot order with the tokens each serves
+// (so no workgroup waits for another), and each wave runs its steps with two rounds of G
+// steps' loads in flight.
+template <int H, int I, int MT, bool INL>
 __global__ __launch_bounds__(256) void k_dec_gate_up_mt(DecodeArgs a) {
     using S = GuShape<H, I>;
     constexpr int LPR = S::LPR, RPS = S::RPS, SPE = S::SPE, NCH = S::NCH;
     constexpr int G = 4;
-    constexpr int XQR = NCH * XQS * 4, XSR = NCH * 4;
-    constexpr int PLB = 8 * MOE_DECODE_MAX_M + MT * (XQR + XSR); // plan bytes this launch copies
-    constexpr int CPT = (PLB / 16 + 255) / 256;                     // 16-byte pieces per thread
     __shared__ DecPlan<H, MT> L;
     __shared__ uint32_t owner[DEC_EMAX]; // first valid pair naming each expert (all ones: none)
     __shared__ uint16_t pid[DEC_MAXP];
+    __shared__ float s_ss[MT][4];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int gw = (int)blockIdx.x * 4 + wv, NW = (int)gridDim.x * 4;
     const int np = a.M * SLOTS;
     static_assert(DEC_MAXP <= 256, "one pair per thread");
-    {
+    constexpr int NQ = 8 * NCH, QPT = INL ? MT * NQ / 256 : 1; // quads of a token; per thread
+    constexpr int KPT = NQ >= 256 ? NQ / 256 : 1;               // consecutive k of one token
+    static_assert(!INL || (MT * NQ % 256 == 0 && NQ % 64 == 0 && QPT % KPT == 0), "a wave's quads are one token's");
+    if constexpr (INL) {
+        constexpr int TPW = (MT + 3) / 4; // tokens routed per wave
+        auto *P = reinterpret_cast<DecPlan<H, MOE_DECODE_MAX_M> *>(a.plan);
+        // Loads, all unconditional (so the compiler's counts of the in-order loads stay exact):
+        // the logits of this wave's tokens wv, wv + 4 (x stands in when there are none) and
+        // their ids (read when not routing), then quad tid + 256 k of the M x NQ activation
+        // quads (threads past the last re-read it): the routing waits for its own loads alone.
+        float raw[TPW][4];
+        int idr[TPW];
+        const float *lg = a.logits ? a.logits : a.x; // M x H >= M x E floats
+#pragma unroll
+        for (int r = 0; r < TPW; ++r) {
+            const int t = min(wv + 4 * r, a.M - 1);
+            load_logits<4>(lg + (size_t)t * a.E, a.E, lane, raw[r]);
+            idr[r] = (int)a.ids[t * SLOTS + min(lane, SLOTS - 1)];
+        }
+        f32x4 xv[QPT];
+#pragma unroll
+        for (int k = 0; k < QPT; ++k) xv[k] = ldg<f32x4>(a.x + 4 * min(tid + 256 * k, a.M * NQ - 1));
+        for (int e = tid; e < DEC_EMAX; e += 256) owner[e] = 0xFFFFFFFFu;
+        if (tid < DEC_MAXP) L.tmask[tid] = 0u;
+        // routing, the pair rule and the valid-slot masks of this wave's tokens; workgroup 0
+        // publishes them (the masks for the down launch) and raises the flags of invalid ids
+#pragma unroll
+        for (int r = 0; r < TPW; ++r) {
+            const int t = wv + 4 * r;
+            if (t >= a.M) break;
+            int id = lane < SLOTS ? idr[r] : 0;
+            float wt = 0.f;
+            if (a.logits) route_values<4>(raw[r], a.E, a.renorm, lane, id, wt);
+            uint32_t fl;
+            const bool ok = slot_kept(id, lane, a.E, fl);
+            const uint32_t vm = (uint32_t)__ballot(ok) & 0x1FFu;
+            if (lane < SLOTS) pid[t * SLOTS + lane] = (uint16_t)id;
+            if (lane == 0) L.vt[t] = vm;
+            if (blockIdx.x == 0) {
+                if (a.logits && lane < SLOTS) {
+                    a.ids[t * SLOTS + lane] = (uint16_t)id;
+                    a.w[t * SLOTS + lane] = wt;
+                }
+                if (lane == 0) {
+                    P->vt[t] = vm;
+                    if (fl) set_flag(a.flags, fl);
+                }
+            }
+        }
+        // The activations as int8 planes: quad q = tid + 256 k is elements 4 (q % 8) .. + 3 of
+        // chunk (q / 8) % NCH of token q / NQ (one token per wave and k), the chunk maximum
+        // over its 8 lanes; each wave's sum of squares of each token (0 for tokens it holds
+        // no quad of).
+        if (lane == 0)
+#pragma unroll
+            for (int t = 0; t < MT; ++t) s_ss[t][wv] = 0.f;
+#pragma unroll
+        for (int k0 = 0; k0 < QPT; k0 += KPT) {
+            float ss = 0.f;
+            const int t = __builtin_amdgcn_readfirstlane((tid + 256 * k0) / NQ);
+#pragma unroll
+            for (int k = k0; k < k0 + KPT; ++k) {
+                const int q = tid + 256 * k, c = (q / 8) % NCH, p = q % 8;
+                float am = 0.f;
+#pragma unroll
+                for (int e4 = 0; e4 < 4; ++e4) {
+                    const float f = fabsf(xv[k][e4]);
+                    am = fmaxf(am, f <= 3.4028234e38f ? f : INFINITY);
+                    ss = __builtin_fmaf(xv[k][e4], xv[k][e4], ss);
+                }
+                am = group_max8(am);
+                uint32_t xh, xl;
+                quant4(xv[k], quant_ratio(am), xh, xl);
+                if (t < a.M) {
+                    L.xq[t][c * XQS + p] = xh;
+                    L.xq[t][c * XQS + 8 + p] = xl;
+                    if (p == 0) L.xsc[t][c] = am <= 3.4028234e38f ? am * (1.0f / 127.0f) : __builtin_nanf("");
+                }
+            }
+            const float sw = wave_sum(ss);
+            if (lane == 0 && t < a.M) s_ss[t][wv] = sw;
+        }
+    } else {
+        constexpr int XQR = NCH * XQS * 4, XSR = NCH * 4;
+        constexpr int PLB = 8 * MOE_DECODE_MAX_M + MT * (XQR + XSR); // plan bytes this launch copies
+        constexpr int CPT = (PLB / 16 + 255) / 256;                     // 16-byte pieces per thread
         // the tokens' factors and valid-slot masks, the M rows of planes and the M rows of
         // scales (global rows are MOE_DECODE_MAX_M apart, local ones MT), and the pairs' ids:
         // all loads in flight, then the stores
@@ -417,6 +512,7 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_mt(DecodeArgs a) {
         if (tid < np) pid[tid] = (uint16_t)idq;
     }
     __syncthreads();
+    if (INL && tid < a.M) L.inv[tid] = rms_factor(a.rmsnorm, ((s_ss[tid][0] + s_ss[tid][1]) + s_ss[tid][2]) + s_ss[tid][3], H);
     // each expert's first valid pair, then wave 0 numbers the selected experts in slot order
     // with the tokens each serves and their pairs
     if (tid < np && ((L.vt[tid / SLOTS] >> (tid % SLOTS)) & 1u)) atomicMin(&owner[pid[tid]], (uint32_t)tid);
@@ -523,45 +619,45 @@ __global__ __launch_bounds__(512) void k_dec_down_mt(DecodeArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t = (int)blockIdx.x / NRB, n0 = ((int)blockIdx.x % NRB) * R;
-    // chunk tid of the token's 9 h rows (row s chunk c is chunk s * CPR + c), requested first
+    // The token's valid slots (bit s of vt): lane k < nvs takes the k-th one's slot ks, and its
+    // expert and weight are requested first, the h chunks next, the W2 rows last: the W2 loads
+    // wait for the ids alone, the quantization for h alone, and each unit below for its own
+    // rows.  Every load is unconditional (threads and units past the last one re-read a valid
+    // address), so the compiler's counts of the in-order loads stay exact at every wait.
+    const uint32_t vt = __builtin_amdgcn_readfirstlane(P->vt[t]);
+    const int nvs = __popc(vt), nun = nvs * MT;
+    uint32_t vm = vt;
+#pragma unroll
+    for (int i = 0; i < SLOTS - 1; ++i)
+        if (i < lane) vm &= vm - 1u;
+    const int ks = lane < nvs ? __builtin_ctz(vm) : 0;
+    const int ke = (int)a.ids[t * SLOTS + ks];
+    const float kw = a.w[t * SLOTS + ks];
+    // chunk tid of the token's 9 h rows (row s chunk c is chunk s * CPR + c)
     f32x4 hv[8];
-    if (tid < NCK) {
-        const float *src = a.hbuf + (size_t)t * SLOTS * I + 32 * tid;
+    {
+        const float *src = a.hbuf + (size_t)t * SLOTS * I + 32 * min(tid, NCK - 1);
 #pragma unroll
         for (int u = 0; u < 8; ++u) hv[u] = ldg<f32x4>(src + 4 * u);
     }
-    float yres = 0.f;
-    if (a.accumulate && tid < R) yres = a.y[(size_t)t * H + n0 + tid];
-    // the token's valid slots: lane k < nvs holds the k-th one's slot, expert and weight
-    const uint32_t vt = __builtin_amdgcn_readfirstlane(P->vt[t]);
-    const int nvs = __popc(vt), nun = nvs * MT;
-    int ks = 0, ke = 0;
-    float kw = 0.f;
-    if (lane < nvs) {
-        uint32_t m = vt;
-        for (int i = 0; i < lane; ++i) m &= m - 1u;
-        ks = __builtin_ctz(m);
-        ke = (int)a.ids[t * SLOTS + ks];
-        kw = a.w[t * SLOTS + ks];
-    }
+    const float yv = a.y[(size_t)t * H + n0 + min(tid, R - 1)];
+    const float yres = a.accumulate && tid < R ? yv : 0.f;
     const int nu = nun > wv ? (nun - wv + NWV - 1) / NWV : 0; // this wave's units wv, wv + 8, ...
     const int gsb = lane % LPR, rr = lane / LPR, sb = gsb >> 3, ib = gsb & 7;
-    // W2 rows of every unit (past the last one: a valid re-read); loads complete in order, so
-    // the quantization below waits for h only
+    // W2 rows of unit i of this wave (past the last unit, or with no valid slot, the shared
+    // expert's: a valid re-read)
     u32x4 qs[MAXU][STEPS];
     u32x2 hd[MAXU][STEPS];
-    if (nu > 0) {
 #pragma unroll
-        for (int i = 0; i < MAXU; ++i) {
-            const int j = min(wv + NWV * i, nun - 1);
-            const int e = __builtin_amdgcn_readlane(ke, j / MT);
-            const uint8_t *W2 = expert_w(a.L.w2, a.L.s2, a.L.sw2, e, a.E);
+    for (int i = 0; i < MAXU; ++i) {
+        const int j = max(min(wv + NWV * i, nun - 1), 0);
+        const int e = nun > 0 ? __builtin_amdgcn_readlane(ke, j / MT) : a.E;
+        const uint8_t *W2 = expert_w(a.L.w2, a.L.s2, a.L.sw2, e, a.E);
 #pragma unroll
-            for (int st = 0; st < STEPS; ++st) {
-                const int row = n0 + (j % MT) * DEC_ROWS + st * RPS + rr;
-                qs[i][st] = ldg<u32x4>(W2 + split_qs<SBR>(row, sb) + 16 * ib);
-                hd[i][st] = ldg<u32x2>(W2 + split_hdr<H, SBR>(row, sb));
-            }
+        for (int st = 0; st < STEPS; ++st) {
+            const int row = n0 + (j % MT) * DEC_ROWS + st * RPS + rr;
+            qs[i][st] = ldg<u32x4>(W2 + split_qs<SBR>(row, sb) + 16 * ib);
+            hd[i][st] = ldg<u32x2>(W2 + split_hdr<H, SBR>(row, sb));
         }
     }
     if (tid < NCK) {
@@ -679,7 +775,7 @@ static hipError_t launch_decode_t(const DecodeArgs &a, hipStream_t st, KernelTim
     // M >= 2: the prep launch routes (when given logits) and publishes ids/w, so the later
     // launches read the routing from ids/w and the plan block
     DecodeArgs b = a;
-    if (a.M >= 2) {
+    if (a.M > 4) {
         TimedLaunch tl(T, MOE_K_DECODE_PREP, st);
         hipLaunchKernelGGL((k_dec_prep<H>), dim3(a.M), dim3(256), 0, st, a);
         b.logits = nullptr;
@@ -688,9 +784,9 @@ static hipError_t launch_decode_t(const DecodeArgs &a, hipStream_t st, KernelTim
         TimedLaunch tl(T, MOE_K_DECODE_GATE_UP, st);
         const dim3 grid((unsigned)a.nwg), blk(256);
         if (a.M == 1) hipLaunchKernelGGL((k_dec_gate_up_m1<H, I>), grid, blk, 0, st, a);
-        else if (a.M == 2) hipLaunchKernelGGL((k_dec_gate_up_mt<H, I, 2>), grid, blk, 0, st, b);
-        else if (a.M <= 4) hipLaunchKernelGGL((k_dec_gate_up_mt<H, I, 4>), grid, blk, 0, st, b);
-        else hipLaunchKernelGGL((k_dec_gate_up_mt<H, I, 8>), grid, blk, 0, st, b);
+        else if (a.M == 2) hipLaunchKernelGGL((k_dec_gate_up_mt<H, I, 2, true>), grid, blk, 0, st, a);
+        else if (a.M <= 4) hipLaunchKernelGGL((k_dec_gate_up_mt<H, I, 4, true>), grid, blk, 0, st, a);
+        else hipLaunchKernelGGL((k_dec_gate_up_mt<H, I, 8, false>), grid, blk, 0, st, b);
     }
     // the down launch reads the routing from ids/w (published by the first launch when it
     // routed the tokens itself)
