@@ -64,6 +64,7 @@ __device__ __forceinline__ bool slot_kept(int id, int lane, int E, uint32_t &fl)
 
 // ---------------------------------------------------------------- down shape
 constexpr int DEC_ROWS = 8; // down: output rows per workgroup
+constexpr int DEC_DOWN_RING = 2; // down, 2 <= M <= 8: units of W2 rows in flight per wave
 // Down: a W2 row (I weights) on LPR2 lanes, one 32-weight sub-block per lane; RPS2 rows per
 // wave step, STEPS steps for the workgroup's DEC_ROWS rows.
 template <int H, int I>
@@ -375,12 +376,13 @@ __device__ __forceinline__ int rank2(uint64_t m0, uint64_t m1, int q) {
 // the tokens' rows of the plan block k_dec_prep wrote and the pairs' ids into LDS (one round
 // of loads).  Then it numbers the selected experts in slot order with the tokens each serves
 // (so no workgroup waits for another), and each wave runs its steps with two rounds of G
-// steps' loads in flight.
+// steps' loads in flight (G = 1: measured faster than 2 to 6 at every M -- with fewer rows in
+// flight per wave, each arrives sooner).
 template <int H, int I, int MT, bool INL>
 __global__ __launch_bounds__(256) void k_dec_gate_up_mt(DecodeArgs a) {
     using S = GuShape<H, I>;
     constexpr int LPR = S::LPR, RPS = S::RPS, SPE = S::SPE, NCH = S::NCH;
-    constexpr int G = 4;
+    constexpr int G = 1;
     __shared__ DecPlan<H, MT> L;
     __shared__ uint32_t owner[DEC_EMAX]; // first valid pair naming each expert (all ones: none)
     __shared__ uint16_t pid[DEC_MAXP];
@@ -645,21 +647,25 @@ __global__ __launch_bounds__(512) void k_dec_down_mt(DecodeArgs a) {
     const int nu = nun > wv ? (nun - wv + NWV - 1) / NWV : 0; // this wave's units wv, wv + 8, ...
     const int gsb = lane % LPR, rr = lane / LPR, sb = gsb >> 3, ib = gsb & 7;
     // W2 rows of unit i of this wave (past the last unit, or with no valid slot, the shared
-    // expert's: a valid re-read)
-    u32x4 qs[MAXU][STEPS];
-    u32x2 hd[MAXU][STEPS];
-#pragma unroll
-    for (int i = 0; i < MAXU; ++i) {
+    // expert's: a valid re-read), in a ring of DR units: unit i + DR is requested once unit i
+    // is done.  Fewer rows in flight per wave finish sooner each (measured: all nine units of
+    // M = 8 requested at once arrive together, late).
+    constexpr int DR = MAXU < DEC_DOWN_RING ? MAXU : DEC_DOWN_RING;
+    u32x4 qs[DR][STEPS];
+    u32x2 hd[DR][STEPS];
+    auto issue_unit = [&](int i) __attribute__((always_inline)) {
         const int j = max(min(wv + NWV * i, nun - 1), 0);
         const int e = nun > 0 ? __builtin_amdgcn_readlane(ke, j / MT) : a.E;
         const uint8_t *W2 = expert_w(a.L.w2, a.L.s2, a.L.sw2, e, a.E);
 #pragma unroll
         for (int st = 0; st < STEPS; ++st) {
             const int row = n0 + (j % MT) * DEC_ROWS + st * RPS + rr;
-            qs[i][st] = ldg<u32x4>(W2 + split_qs<SBR>(row, sb) + 16 * ib);
-            hd[i][st] = ldg<u32x2>(W2 + split_hdr<H, SBR>(row, sb));
+            qs[i % DR][st] = ldg<u32x4>(W2 + split_qs<SBR>(row, sb) + 16 * ib);
+            hd[i % DR][st] = ldg<u32x2>(W2 + split_hdr<H, SBR>(row, sb));
         }
-    }
+    };
+#pragma unroll
+    for (int i = 0; i < DR; ++i) issue_unit(i);
     if (tid < NCK) {
         uint32_t h8[8], l8[8];
         float sx, ss;
@@ -689,12 +695,13 @@ __global__ __launch_bounds__(512) void k_dec_down_mt(DecodeArgs a) {
             for (int st = 0; st < STEPS; ++st) {
                 uint32_t kv[8];
 #pragma unroll
-                for (int d = 0; d < 4; ++d) kv_signed8(qs[i][st][d], kv[2 * d], kv[2 * d + 1]);
-                float d = sub_scale(hd[i][st], ib) * sx * subblock_idot(kv, xh, xl);
+                for (int d = 0; d < 4; ++d) kv_signed8(qs[i % DR][st][d], kv[2 * d], kv[2 * d + 1]);
+                float d = sub_scale(hd[i % DR][st], ib) * sx * subblock_idot(kv, xh, xl);
                 d = group_sum<LPR>(d);
                 if (gsb == 0) part[s][(j % MT) * DEC_ROWS + st * RPS + rr] = cw * d;
             }
         }
+        if (i + DR < MAXU) issue_unit(i + DR);
     }
     __syncthreads();
     if (tid < R) {

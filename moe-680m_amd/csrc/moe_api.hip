@@ -416,8 +416,9 @@ static moe_status ffn_call(const char *fn, moe_ctx *ctx, int layer, const float 
         a.rmsnorm = (flags & MOE_FFN_RMSNORM) ? 1 : 0;
         a.renorm = renorm;
         a.c = c;
-        // gate/up: one workgroup per CU for M = 1 (every SIMD one wave), two beyond
-        a.nwg = ctx->ncu * (M == 1 ? 1 : 2);
+        // gate/up: one workgroup per CU for M = 1 (every SIMD one wave), two for M <= 4, three
+        // beyond (measured best at each M)
+        a.nwg = ctx->ncu * (M == 1 ? 1 : M <= 4 ? 2 : 3);
         he = launch_decode(H, I, a, st, T);
         if (he != hipSuccess) return fail(MOE_EHIP, "%s: decode launch: %s", fn, hipGetErrorString(he));
         return ok();
