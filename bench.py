@@ -215,8 +215,10 @@ def stack_timeline(torch, pkg, ctx, routers, n_tok, routed):
 
 # ---------------------------------------------------------------- legs
 
-def leg_decode(torch, pkg, ctx, K, W, eager):
-    """Config 2: one token through the 40 layers per moe_decode_stack launch."""
+def leg_decode(torch, pkg, ctx, K, W, eager, nl=LAYERS):
+    """Config 2: one token through the 40 layers per moe_decode_stack launch (nl < 40 layers
+    only in the eager runs profiled by rocprofv3, to split the traffic per launch into the
+    per-layer part and the fixed part)."""
     dev = torch.device("cuda:0")
     nsteps = W + K
     logits = pkg.gen_logits(nsteps * LAYERS, E, pkg.seed_for(2, 0, pkg.TAG_L)).view(nsteps, LAYERS, E)
@@ -225,11 +227,12 @@ def leg_decode(torch, pkg, ctx, K, W, eager):
     wts = torch.empty((LAYERS, 9), dtype=torch.float32, device=dev)
 
     def token(s):
-        ctx.decode_stack(0, x, logits[s], y=x, ids=ids, w=wts, rmsnorm=True)
+        ctx.decode_stack(0, x, logits[s][:nl], y=x, ids=ids, w=wts, rmsnorm=True)
 
     token(0)
     torch.cuda.synchronize()
     assert ctx.device_flags() == 0, "decode stack raised a device flag"
+    assert eager or nl == LAYERS, "the timed decode leg runs all 40 layers"
     if eager:
         for s in range(nsteps):
             token(s)
@@ -483,6 +486,9 @@ def main():
     ap.add_argument("--stack-timeline", type=int, default=0, metavar="TOKENS",
                     help="print the decode stack's per-phase timeline over this many tokens (seeded and "
                          "activation-routed) from the trace build libmoe680m_trace.so, and nothing else")
+    ap.add_argument("--stack-layers", type=int, default=LAYERS, metavar="N",
+                    help="with --only decode: layers per moe_decode_stack launch (1..40; the timed "
+                         "bench always runs 40)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="run a plain device copy of this size first (scales PMC byte counters)")
     args = ap.parse_args()
@@ -534,7 +540,7 @@ def main():
 
     if args.only:
         eager = True
-        {"decode": lambda: leg_decode(torch, pkg, ctx, K, W, eager),
+        {"decode": lambda: leg_decode(torch, pkg, ctx, K, W, eager, args.stack_layers),
          "decode_routed": lambda: leg_decode_routed(torch, pkg, ctx, routers, K, W, eager),
          "config0": lambda: leg_config0(torch, pkg, ctx, routers, eager),
          "prefill": lambda: leg_prefill(torch, pkg, ctx, args.prefill_steps, eager),

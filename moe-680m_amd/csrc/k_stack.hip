@@ -818,7 +818,9 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     // of its phase-B (W2) weights, issued at B1 of layer li: they stream during phase A and
     // the h exchange, which are compute- and L2-bound, and arrive before phase B.  The loads
     // are issued unconditionally -- past the last layer they re-read layer n-1, which is
-    // still cached -- because a conditional burst would make the compiler's load counter
+    // still in the L2 (FETCH_SIZE of a one-layer launch: 18.3 MB = the layer's 15.1 MB, its
+    // 2.8 MB of exchange reads and 0.4 MB, not the 10 MB a re-read from HBM would add) --
+    // because a conditional burst would make the compiler's load counter
     // path-dependent and turn the waits for the older burst into waits for everything.
     auto prefetch_a = [&](int li) __attribute__((always_inline)) {
         const uint8_t *W1 = rt_p[li % 3][0][0];
