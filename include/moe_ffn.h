@@ -251,8 +251,9 @@ const char *moe_last_error(void);
  * timed launches and their summed milliseconds, and starts a new window.  Events are
  * created here, never inside a hot call; capacity 0 disables and frees them. */
 enum {
-    MOE_K_ROUTER_TOPK = 0,     /* moe_router_topk, and moe_ffn_route's router launch for M > 8 */
-    MOE_K_BUCKET_FILL = 1,     /* moe_bucket_fill; moe_ffn's first prefill launch (bucket fill + prep) */
+    MOE_K_ROUTER_TOPK = 0,     /* moe_router_topk; moe_ffn_route's first prefill launch (routing + bucket counts) */
+    MOE_K_BUCKET_FILL = 1,     /* moe_bucket_fill; the prefill chain's count launch (moe_ffn, ids given) and its
+                                  placement + prep launch */
     MOE_K_DECODE_GATE_UP = 2,  /* moe_ffn / moe_ffn_route, M <= 8 */
     MOE_K_DECODE_DOWN = 3,
     MOE_K_PREFILL_GATE_UP = 4,
