@@ -138,56 +138,44 @@ __device__ __forceinline__ float max16(float v) {
 }
 
 // ---------------------------------------------------------------- prep
-// One wave per token; lane owns 32-blocks lane, lane+64, ... of the row.
+// One wave per token.  Lane l holds quads l, l + 64, ... (four consecutive elements each) of the
+// row, so every load instruction reads 1 KB of consecutive bytes; a quad's f16 values go
+// straight to their place in the 32-block's stored order (perm32_pos: quad j < 4 of the block
+// to positions 8j..8j+3, quad j >= 4 to 8(j-4)+4..+7), one 8-byte store each.
 template <int H>
 __device__ __forceinline__ void prep_token(const PrefillArgs &a, int t, int lane) {
-    constexpr int NB = H / 32 / 64 > 0 ? H / 32 / 64 : 1; // 32-blocks per lane
-    constexpr int NBK = H / 32;
-    float v[NB][32];
-    const bool own = lane < NBK;
+    constexpr int NQ = H / 4, QPL = NQ / 64; // quads of the row; per lane
+    static_assert(NQ % 64 == 0, "whole waves of quads");
+    f32x4 v[QPL];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        if (own) load32(a.x + (size_t)t * H + 32 * (lane + 64 * b), v[b]);
-        else
-#pragma unroll
-            for (int i = 0; i < 32; ++i) v[b][i] = 0.0f;
-    }
+    for (int u = 0; u < QPL; ++u) v[u] = ldg<f32x4>(a.x + (size_t)t * H + 4 * (lane + 64 * u));
     if (a.rmsnorm) {
         float ss = 0.f;
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
+        for (int u = 0; u < QPL; ++u)
 #pragma unroll
-            for (int i = 0; i < 32; ++i) ss = __builtin_fmaf(v[b][i], v[b][i], ss);
+            for (int i = 0; i < 4; ++i) ss = __builtin_fmaf(v[u][i], v[u][i], ss);
         ss = wave_sum(ss);
         const float inv = 1.0f / sqrtf(ss * (1.0f / (float)H) + 1e-6f);
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
+        for (int u = 0; u < QPL; ++u)
 #pragma unroll
-            for (int i = 0; i < 32; ++i) v[b][i] *= inv;
+            for (int i = 0; i < 4; ++i) v[u][i] *= inv;
     }
     float mx = 0.f;
 #pragma unroll
-    for (int b = 0; b < NB; ++b)
+    for (int u = 0; u < QPL; ++u)
 #pragma unroll
-        for (int i = 0; i < 32; ++i) mx = fmaxf(mx, fabsf(v[b][i]));
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, fabsf(v[u][i]));
     mx = __builtin_bit_cast(float, wave_max_u32(__builtin_bit_cast(uint32_t, mx))); // non-negative: int order
     float inv_s;
     const float s = pow2_scale(mx, &inv_s);
-    if (own) {
+    const int j = lane & 7, pos = j < 4 ? 8 * j : 8 * (j - 4) + 4; // the quad's place in its 32-block
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            u32x4 o[4];
-#pragma unroll
-            for (int p = 0; p < 16; ++p) {
-                // stored position 2p, 2p+1 <- natural k with perm32_pos(k) == 2p, 2p+1
-                const int g = (2 * p) >> 3, j = (2 * p) & 7;
-                const int k0 = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
-                o[p >> 2][p & 3] = pack_f16x2(v[b][k0] * s, v[b][k0 + 1] * s);
-            }
-            u32x4 *dst = reinterpret_cast<u32x4 *>(a.xh + (size_t)t * H + 32 * (lane + 64 * b));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) dst[i] = o[i];
-        }
+    for (int u = 0; u < QPL; ++u) {
+        const int q = lane + 64 * u;
+        const u32x2 o = {pack_f16x2(v[u][0] * s, v[u][1] * s), pack_f16x2(v[u][2] * s, v[u][3] * s)};
+        *reinterpret_cast<u32x2 *>(a.xh + (size_t)t * H + 32 * (q >> 3) + pos) = o;
     }
     if (lane == 0) a.xinv[t] = inv_s;
 }
