@@ -240,16 +240,19 @@ __global__ __launch_bounds__(64 * PF_COUNT_TOKENS) void k_pf_count(PfCountArgs c
     const bool routed = keep && id != c.E;
     uint32_t rank = routed ? atomicAdd(&hist[id], 1u) : 0u;
     __syncthreads();
+    // counter copy blockIdx % 8 (the workgroup's XCD): a hot bucket's adds are spread over
+    // eight addresses instead of queueing on one
+    const uint32_t cp = blockIdx.x % PF_CNT_COPIES;
     for (int e = threadIdx.x; e < E1; e += 64 * PF_COUNT_TOKENS) {
         const uint32_t n = hist[e];
-        base[e] = n ? __hip_atomic_fetch_add((MOE_GLOBAL uint32_t *)(c.cnt + e), n, __ATOMIC_RELAXED,
+        base[e] = n ? __hip_atomic_fetch_add((MOE_GLOBAL uint32_t *)(c.cnt + cp * E1 + e), n, __ATOMIC_RELAXED,
                                              __HIP_MEMORY_SCOPE_AGENT)
                     : 0u;
     }
     __syncthreads();
     if (tok && lane < SLOTS) {
         uint32_t info = 0xFFFFFFFFu;
-        if (routed) info = ((uint32_t)id << PF_SLOT_RANK_BITS) | (base[id] + rank);
+        if (routed) info = ((uint32_t)id << PF_SLOT_RANK_BITS) | (cp << PF_SLOT_COPY_SHIFT) | (base[id] + rank);
         else if (keep) info = ((uint32_t)c.E << PF_SLOT_RANK_BITS) | (uint32_t)t; // the shared slot
         else if (lane == SLOTS - 1 && !ns) info = PF_SLOT_HOLE;
         c.slot[(size_t)t * SLOTS + lane] = info;
@@ -276,7 +279,18 @@ __global__ __launch_bounds__(BF_THREADS) void k_pf_place(BucketArgs b, PfCountAr
     extern __shared__ uint32_t smem[];
     const int E1 = b.E1;
     const BucketScan S = bucket_scan_lds(smem, E1);
-    for (int e = tid; e < E1; e += BF_THREADS) S.tot[e] = e == E1 - 1 ? (uint32_t)b.M : ldg<uint32_t>(c.cnt + e);
+    // per bucket the copies' counts: their total, and each copy's start inside the bucket
+    uint32_t *cb = smem + 5 * (E1 + 1); // [PF_CNT_COPIES][E1]
+    for (int e = tid; e < E1; e += BF_THREADS) {
+        uint32_t tot = 0u;
+        if (e < E1 - 1)
+#pragma unroll
+            for (int k = 0; k < PF_CNT_COPIES; ++k) {
+                cb[k * E1 + e] = tot;
+                tot += ldg<uint32_t>(c.cnt + k * E1 + e);
+            }
+        S.tot[e] = e == E1 - 1 ? (uint32_t)b.M : tot;
+    }
     __syncthreads();
     bucket_lists(b, S, blk == 0);
     const int n = SLOTS * b.M, i0 = blk * PF_PLACE_SLOTS, i1 = min(i0 + PF_PLACE_SLOTS, n);
@@ -291,7 +305,8 @@ __global__ __launch_bounds__(BF_THREADS) void k_pf_place(BucketArgs b, PfCountAr
             b.sorted_tok[q] = (uint16_t)t;
             b.sorted_w[q] = 0.0f;
         } else if (info != 0xFFFFFFFFu) {
-            p = S.rg[info >> PF_SLOT_RANK_BITS] + (info & ((1u << PF_SLOT_RANK_BITS) - 1u));
+            const uint32_t e = info >> PF_SLOT_RANK_BITS, k = (info >> PF_SLOT_COPY_SHIFT) & (PF_CNT_COPIES - 1u);
+            p = S.rg[e] + (e < (uint32_t)E1 - 1u ? cb[k * E1 + e] : 0u) + (info & ((1u << PF_SLOT_COPY_SHIFT) - 1u));
             b.sorted_tok[p] = (uint16_t)t;
             b.sorted_w[p] = wv;
         }
@@ -810,7 +825,7 @@ __global__ __launch_bounds__(256) void k_pf_combine(PrefillArgs a) {
     const int t = blockIdx.x;
     // the chain's bucket counters, read by k_pf_place (an earlier launch), start over at zero
     if (t == 0 && a.cnt)
-        for (int e = threadIdx.x; e <= a.E; e += 256) a.cnt[e] = 0u;
+        for (int e = threadIdx.x; e < PF_CNT_COPIES * (a.E + 1); e += 256) a.cnt[e] = 0u;
     uint32_t ps[SLOTS];
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) ps[s] = a.pos[(size_t)t * SLOTS + s];
@@ -859,7 +874,7 @@ static hipError_t launch_prefill_t(const BucketArgs &b, const PfCountArgs &c, co
         const int nplace = (SLOTS * b.M + PF_PLACE_SLOTS - 1) / PF_PLACE_SLOTS;
         const int nprep = (a.M + PF_PREP_TOKENS - 1) / PF_PREP_TOKENS;
         hipLaunchKernelGGL((k_pf_place<H>), dim3((unsigned)(nplace + nprep)), dim3(BF_THREADS),
-                           5 * (size_t)(b.E1 + 1) * 4, st, b, c, a);
+                           (5 * (size_t)(b.E1 + 1) + (size_t)PF_CNT_COPIES * b.E1) * 4, st, b, c, a);
     }
     // one launch over the tile list (full and big remainder tiles, then small remainders, then
     // empty entries, which exit at once)

@@ -39,7 +39,7 @@ struct moe_ctx {
     float *sw = nullptr;         // [9 m_max]
     uint32_t *pos = nullptr;     // [m_max][9]
     uint32_t *chunk = nullptr;   // [ceil(m_max/64)][E+1]
-    uint32_t *pcnt = nullptr;    // [E+1] the prefill chain's bucket counters (zero between calls)
+    uint32_t *pcnt = nullptr;    // [PF_CNT_COPIES][E+1] the prefill chain's bucket counters (zero between calls)
     uint32_t *pslot = nullptr;   // [9 m_max] the prefill chain's slot bucket and rank
     Tile *tiles = nullptr;       // [tile_max(m_max)]
     LayerPtrs *dlayers = nullptr; // device layer table of the split copies (decode stack)
@@ -158,7 +158,7 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
         {(void **)&c->sw, SLOTS * mm * 4},
         {(void **)&c->pos, mm * SLOTS * 4},
         {(void **)&c->chunk, nchunk * E1 * 4},
-        {(void **)&c->pcnt, E1 * 4},
+        {(void **)&c->pcnt, (size_t)PF_CNT_COPIES * E1 * 4},
         {(void **)&c->pslot, SLOTS * mm * 4},
         {(void **)&c->tiles, tmax * sizeof(Tile)},
         {(void **)&c->dlayers, (size_t)cfg->n_layers * sizeof(LayerPtrs)},
@@ -195,7 +195,7 @@ moe_status moe_create(int device, const moe_config *cfg, moe_ctx **out) {
     he = hipMemset(c->flags, 0, 256);
     if (he == hipSuccess) he = hipMemset(c->dlayers, 0, (size_t)cfg->n_layers * sizeof(LayerPtrs));
     if (he == hipSuccess) he = hipMemset(c->drouters, 0, (size_t)cfg->n_layers * sizeof(StackRouter));
-    if (he == hipSuccess) he = hipMemset(c->pcnt, 0, E1 * 4);
+    if (he == hipSuccess) he = hipMemset(c->pcnt, 0, (size_t)PF_CNT_COPIES * E1 * 4);
     // the decode stack's control words and both exchange sets start zeroed
     if (he == hipSuccess) he = hipMemset(c->xtag, 0, c->xtag_words * 4);
     if (he == hipSuccess) he = hipDeviceSynchronize();

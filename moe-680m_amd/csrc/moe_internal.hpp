@@ -94,7 +94,9 @@ struct PfCountArgs {
     uint32_t *slot;      // [9M] (bucket << 23) | rank in the bucket, or ~0 for a dropped slot
     uint32_t *flags;
 };
-constexpr int PF_SLOT_RANK_BITS = 23; // ranks < 9 * 65535 < 2^23
+constexpr int PF_SLOT_RANK_BITS = 23; // a slot's expert above these bits
+constexpr int PF_CNT_COPIES = 8;      // striped bucket counters (one per XCD)
+constexpr int PF_SLOT_COPY_SHIFT = 20; // its counter copy at bits 20..22, its rank below: ranks < 9 * 65535 < 2^20
 
 // Prefill reads the split copy of a layer (k_repack_split), as the decode kernels do.
 struct PrefillArgs {
