@@ -404,7 +404,8 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_mt(DecodeArgs a) {
         // quads (threads past the last re-read it): the routing waits for its own loads alone.
         float raw[TPW][4];
         int idr[TPW];
-        const float *lg = a.logits ? a.logits : a.x; // M x H >= M x E floats
+        static_assert(H >= DEC_EMAX - 1, "x stands in for the logits: M x H >= M x E floats");
+        const float *lg = a.logits ? a.logits : a.x;
 #pragma unroll
         for (int r = 0; r < TPW; ++r) {
             const int t = min(wv + 4 * r, a.M - 1);

@@ -398,8 +398,8 @@ static moe_status ffn_call(const char *fn, moe_ctx *ctx, int layer, const float 
     KernelTimer *T = timer_for(ctx, st);
     hipError_t he;
     if (M <= MOE_DECODE_MAX_M) {
-        // the decode launches route the tokens themselves (M = 1: every gate/up wave; M >= 2:
-        // the prep launch) and publish ids/w
+        // the decode launches route the tokens themselves (M <= 4: every gate/up workgroup;
+        // M >= 5: the prep launch) and publish ids/w
         DecodeArgs a{};
         a.L = ctx->slayers[layer];
         a.x = x;
