@@ -58,7 +58,7 @@ def small(gpu, orc):
     ctx.close()
 
 
-@pytest.mark.parametrize("M", [1, 2, 5, 8, 9, 37, 200])
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 8, 9, 37, 200])
 @pytest.mark.parametrize("flags", [0, 1, 2, 3])
 def test_small_shape(gpu, orc, small, M, flags):
     ctx, layer = small
@@ -176,7 +176,7 @@ def test_renorm_flags(gpu, orc, full_renorm):
             assert err <= (TOL_DECODE if M <= 8 else TOL_PREFILL)
 
 
-@pytest.mark.parametrize("M", [1, 2, 5, 8, 9, 40, 512, 1000, 1025, 4096])
+@pytest.mark.parametrize("M", [1, 2, 4, 5, 8, 9, 40, 512, 1000, 1025, 4096])
 def test_ffn_route_equals_router_then_ffn(gpu, full, M):
     """moe_ffn_route (routing inside the decode launches for M <= 8, a router launch before the
     prefill launches beyond) gives the router's ids and weights and the FFN's output bit for
