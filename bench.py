@@ -69,13 +69,15 @@ def capture(torch, fn):
 
 def timed_graphs(torch, step, n, warm, per_graph):
     """Steps warm..n-1 replayed from graphs of per_graph steps after `warm` eager steps and
-    one warm replay; returns (wall us per step, event us per step)."""
+    one untimed replay of every graph (a graph's first launch pays its one-time upload, ~0.1 ms
+    here, which is not a cost of the steps); returns (wall us per step, event us per step)."""
     for s in range(warm):
         step(s)
     torch.cuda.synchronize()
     groups = [list(range(b, min(b + per_graph, n))) for b in range(warm, n, per_graph)]
     graphs = [capture(torch, lambda g=g: [step(s) for s in g]) for g in groups]
-    graphs[0].replay()
+    for g in graphs:
+        g.replay()
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()

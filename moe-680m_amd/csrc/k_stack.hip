@@ -602,20 +602,15 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 }
             }
             lds_barrier(); // B2: h_li in LDS
-            lds_barrier(); // B3: this workgroup's contributions in LDS
+            lds_barrier(); // B3: every compute wave past phase B (its partial rows published)
             // until B1 the compute waves only decode the next layer's weights, which is off
             // the critical path: let the exchange win every VALU issue slot on its SIMD
             __builtin_amdgcn_s_setprio(2);
             if (first) {
-                // publish this XCD's partial of rows [64j, 64j+64) ...
+                // this XCD's partial of rows [64j, 64j+64) was published by the compute waves;
+                // gather all eight (lane: quad lane&15 of XCDs lane>>4 and (lane>>4)+4) ...
                 uint32_t *pb = pbuf(li);
-                // (the workgroup's abort word read with the contributions: a wait that gave up in
-                // another wave of this workgroup left them invalid)
-                const float pv = part[0][lane] + part[1][lane];
-                const int ab = *abort_lds;
-                if (got && !ab) tag_store(pb + (size_t)k * H + ROWS * j + lane, pv);
                 STK_MARK(STK_EV_PUB, li);
-                // ... gather all eight (lane: quad lane&15 of XCDs lane>>4 and (lane>>4)+4) ...
                 const RemoteQuads ld{reinterpret_cast<const u32x4 *>(pb + ROWS * j)};
                 const int m = lane >> 4, qq = lane & 15;
                 int q[2] = {m * (H / 4) + qq, (m + 4) * (H / 4) + qq};
@@ -1117,7 +1112,19 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             if (lane % LPRB == 0 && lane < NSB) part[1][8 * w + rB] = wsh * ds;
         }
         if (w == 0) STK_MARK(STK_EV_B, li);
-        lds_barrier(); // B3: contributions in LDS
+        {
+            // this wave's 8 rows of the XCD's partial (slot k's contribution and its share of
+            // the shared expert's) published now, not after B3 by a poller: both parts of a row
+            // come from this wave (its own LDS writes, read back in order).  Valid unless a
+            // wait of this workgroup gave up (its flag is set before B2 by the waiting wave).
+            asm volatile("" ::: "memory");
+            if (lane < 8) {
+                const int r = 8 * w + lane;
+                const float pv = part[0][r] + part[1][r];
+                if (!*abort_lds) tag_store(pbuf(li) + (size_t)k * H + ROWS * j + r, pv);
+            }
+        }
+        lds_barrier(); // B3: every wave past phase B
         // the pollers now gather the partials and exchange x: decode layer li+1's phase-A
         // weights (requested at B2) meanwhile -- or, AR, request layer li+1's router rows
         if constexpr (AR) rg_prefetch(min(li + 1, n - 1));
