@@ -602,15 +602,23 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                 }
             }
             lds_barrier(); // B2: h_li in LDS
-            lds_barrier(); // B3: every compute wave past phase B (its partial rows published)
+            lds_barrier(); // B3: every compute wave past phase B (the contributions in LDS)
             // until B1 the compute waves only decode the next layer's weights, which is off
             // the critical path: let the exchange win every VALU issue slot on its SIMD
             __builtin_amdgcn_s_setprio(2);
             if (first) {
-                // this XCD's partial of rows [64j, 64j+64) was published by the compute waves;
-                // gather all eight (lane: quad lane&15 of XCDs lane>>4 and (lane>>4)+4) ...
+                // this XCD's partial of rows [64j, 64j+64): published by the compute waves, or
+                // (routed from the activations) here ...
                 uint32_t *pb = pbuf(li);
+                if constexpr (AR) {
+                    // (the workgroup's abort word read with the contributions: a wait that gave
+                    // up in another wave of this workgroup left them invalid)
+                    const float pv = part[0][lane] + part[1][lane];
+                    const int ab = *abort_lds;
+                    if (got && !ab) tag_store(pb + (size_t)k * H + ROWS * j + lane, pv);
+                }
                 STK_MARK(STK_EV_PUB, li);
+                // ... then gather all eight (lane: quad lane&15 of XCDs lane>>4 and (lane>>4)+4) ...
                 const RemoteQuads ld{reinterpret_cast<const u32x4 *>(pb + ROWS * j)};
                 const int m = lane >> 4, qq = lane & 15;
                 int q[2] = {m * (H / 4) + qq, (m + 4) * (H / 4) + qq};
@@ -1112,11 +1120,13 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             if (lane % LPRB == 0 && lane < NSB) part[1][8 * w + rB] = wsh * ds;
         }
         if (w == 0) STK_MARK(STK_EV_B, li);
-        {
+        if constexpr (!AR) {
             // this wave's 8 rows of the XCD's partial (slot k's contribution and its share of
             // the shared expert's) published now, not after B3 by a poller: both parts of a row
             // come from this wave (its own LDS writes, read back in order).  Valid unless a
             // wait of this workgroup gave up (its flag is set before B2 by the waiting wave).
+            // Seeded logits: 256.3 -> 255.0 us per token; routed from the activations the
+            // poller's publish stays (481 against 498 us with this one).
             asm volatile("" ::: "memory");
             if (lane < 8) {
                 const int r = 8 * w + lane;
