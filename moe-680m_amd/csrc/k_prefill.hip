@@ -28,9 +28,10 @@
 //            atomics, no f16 read-modify-write race (the reference's w2_scatter.comp:77-86).
 //
 // Operand precision: the weight dl*kv (exact in f32, up to 23 significant bits) is rounded
-// once to f16 (dl itself is rounded to f16 first: <= 2^-10 relative in all); activations
-// and h are f16 after an exact power-of-two scaling, so only their 11-bit rounding remains.
-// MFMA accumulates in f32.
+// once to f16 (dl itself is rounded to f16 first: <= 2^-10 relative in all), after an exact
+// power-of-two shift 2^-s_n per weight row (row_shift below, undone in the epilogue);
+// activations and h are f16 after an exact power-of-two scaling, so only their 11-bit
+// rounding remains.  MFMA accumulates in f32.
 //
 // Weight decode into a B fragment.  v_mfma_f32_16x16x32_f16 takes from lane (g, n) of the
 // B operand 8 K values of column n; the K order inside one 32-wide MFMA step is free as long
@@ -38,9 +39,11 @@
 // K = 4d..4d+3, high nibbles K = 16+4d..16+4d+3 of that sub-block, so one 32-bit qs word
 // gives the lane its 8 weights (which sub-block and dword each lane group takes in each
 // step: wstage_load).  The activations are stored in that order (perm32 below).
-// Codebook bytes come from the v_perm lookup (kv + 128, see moe_device.hpp); a second
-// v_perm places each byte under an 0x64 high byte, which is the f16 1024 + byte, exactly;
-// one packed f16 add of -1152 gives kv exactly and one packed multiply applies dl.
+// Codebook bytes b = kv + 128 come from the v_perm lookup (moe_device.hpp); a second v_perm
+// places each byte under a zero high byte, which is the f16 subnormal b * 2^-24, exactly; one
+// packed f16 FMA  b * 2^-24 * B + C  with B = dl * 2^(24 - s_n) and C = -128 * 2^-24 * B (both
+// exact f16) gives dl * kv * 2^-s_n with one rounding.  The row shift s_n (from the row's
+// largest |d|) keeps B <= 65504, so no scale overflows, and the row's large weights normal.
 #include "moe_internal.hpp"
 #include "bucket_fill.hpp"
 
@@ -62,30 +65,33 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
-// 8 weights of one qs dword (low nibbles then high nibbles) as 4 packed f16 pairs, * dl.
-__device__ __forceinline__ u32x4 dq8_f16(uint32_t q, uint32_t dl2) {
+// 8 weights of one qs dword (low nibbles then high nibbles) as 4 packed f16 pairs
+// dl * kv * 2^-s (b2, c2: the sub-block's B and C pairs, bc_pair).  v_perm selector 0x0c is a
+// zero byte.
+__device__ __forceinline__ u32x4 dq8_f16(uint32_t q, uint32_t b2, uint32_t c2) {
     uint32_t lo, hi;
     kv_biased8(q, lo, hi);
-    constexpr uint32_t MAGIC = 0x64646464u;
-    const f16x2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-    const f16x2 dl = __builtin_bit_cast(f16x2, dl2);
-    const uint32_t p[4] = {__builtin_amdgcn_perm(MAGIC, lo, 0x04010400u), __builtin_amdgcn_perm(MAGIC, lo, 0x04030402u),
-                           __builtin_amdgcn_perm(MAGIC, hi, 0x04010400u), __builtin_amdgcn_perm(MAGIC, hi, 0x04030402u)};
+    const f16x2 bv = __builtin_bit_cast(f16x2, b2), cv = __builtin_bit_cast(f16x2, c2);
+    const uint32_t p[4] = {__builtin_amdgcn_perm(lo, lo, 0x0c010c00u), __builtin_amdgcn_perm(lo, lo, 0x0c030c02u),
+                           __builtin_amdgcn_perm(hi, hi, 0x0c010c00u), __builtin_amdgcn_perm(hi, hi, 0x0c030c02u)};
     uint32_t o[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const f16x2 v = (__builtin_bit_cast(f16x2, p[i]) + bias) * dl;
-        o[i] = __builtin_bit_cast(uint32_t, v);
-    }
+    for (int i = 0; i < 4; ++i)
+        o[i] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2, p[i]), bv, cv));
     return u32x4{o[0], o[1], o[2], o[3]};
 }
 
-// dl = d * (ls - 32) of sub-block j from an 8-byte header, rounded once to f16, in both
-// halves of the returned word.
-__device__ __forceinline__ uint32_t dl_pair(u32x2 hdr, int j) {
-    const float dl = sub_scale(hdr, j);
-    const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)dl);
-    return h | (h << 16);
+// B = dl * F (F = 2^(24 - s), row_shift) of sub-block j from an 8-byte header, rounded once to
+// f16 (dl = d * (ls - 32) is exact in f32 and F a power of two, so B = f16(dl) * F wherever
+// both are normal), and C = -2^-17 * B = -128 * 2^-24 * B; each in both halves of a word.  C
+// is exact down to |B| = 8, and below that off by at most 2^-25, against weights of the row
+// up to 2^-1.
+__device__ __forceinline__ void bc_pair(u32x2 hdr, int j, float F, uint32_t &b2, uint32_t &c2) {
+    const _Float16 b = (_Float16)(sub_scale(hdr, j) * F);
+    const f16x2 bv = {b, b};
+    const f16x2 k = {(_Float16)-0x1p-17f, (_Float16)-0x1p-17f};
+    b2 = __builtin_bit_cast(uint32_t, bv);
+    c2 = __builtin_bit_cast(uint32_t, bv * k);
 }
 
 __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
@@ -362,11 +368,41 @@ __device__ __forceinline__ void wstage_load(WStage<NR> &s, const WRows (&groups)
     }
 }
 
-// dl pair of the lane's sub-block (4h + g of the stage's super-block) for each row group.
+// B and C pairs of the lane's sub-block (4h + g of the stage's super-block) for each row group.
 template <int NR>
-__device__ __forceinline__ void wstage_dl(const WStage<NR> &s, int ch, int g, uint32_t (&dl)[NR]) {
+__device__ __forceinline__ void wstage_bc(const WStage<NR> &s, int ch, int g, const float (&F)[NR],
+                                          uint32_t (&b2)[NR], uint32_t (&c2)[NR]) {
 #pragma unroll
-    for (int r = 0; r < NR; ++r) dl[r] = dl_pair(s.hdr[r], 4 * (ch & 1) + g);
+    for (int r = 0; r < NR; ++r) bc_pair(s.hdr[r], 4 * (ch & 1) + g, F[r], b2[r], c2[r]);
+}
+
+// Row shift s_n of weight row n (lane (g, n)): with the row's largest |d| < 2^e (over its SBR
+// super-blocks), s_n = e + 13, so every sub-block's |B| = |d (ls - 32)| 2^(24 - s_n) <
+// 32 * 2^e * 2^(11 - e) = 2^16, i.e. at most 65504 after rounding (a row's largest |d| times 32
+// is an f16 significand times a power of two).  Lane (g, n) requests the d words of a share of
+// the row's headers (row_dmax_load, issued with the first loads of the work item); row_shift
+// takes the maximum over the row's four lane groups and returns F = 2^(24 - s_n) for bc_pair
+// and P = 2^s_n for the epilogue.  A row whose d are all zero gets F = 2^127 (its B are 0).
+template <int SBR>
+__device__ __forceinline__ u32x2 row_dmax_load(const WRows &w, int n, int g) {
+    if constexpr (SBR == 1) {
+        return u32x2{ldg<uint32_t>(w.h + (uint32_t)n * 8u), 0u};
+    } else {
+        static_assert(SBR == 2 || SBR == 4 || SBR == 8, "one or two headers per lane group");
+        const u32x4 v = ldg<u32x4>(w.h + (uint32_t)n * (SBR * 8u) + 16u * (uint32_t)(g % (SBR / 2)));
+        return u32x2{v[0], v[2]};
+    }
+}
+__device__ __forceinline__ void row_shift(u32x2 d2, float &F, float &P) {
+    uint32_t m = (d2[0] & 0x7FFFu) > (d2[1] & 0x7FFFu) ? (d2[0] & 0x7FFFu) : (d2[1] & 0x7FFFu);
+    uint32_t o = (uint32_t)__shfl_xor((int)m, 16);
+    m = o > m ? o : m;
+    o = (uint32_t)__shfl_xor((int)m, 32);
+    m = o > m ? o : m;
+    const uint32_t eb = __builtin_bit_cast(uint32_t, f16_bits_to_f32(m)) >> 23; // max|d| < 2^(eb - 126)
+    const uint32_t fe = 264u - eb, pe = eb + 14u;                               // 127 + 11 - e, 127 + e + 13
+    F = __builtin_bit_cast(float, (fe < 254u ? fe : 254u) << 23);
+    P = __builtin_bit_cast(float, (pe < 254u ? pe : 254u) << 23);
 }
 
 // One stage of MFMAs: NR B fragments (dequantized here) against the MT M-tiles of the LDS
@@ -374,8 +410,8 @@ __device__ __forceinline__ void wstage_dl(const WStage<NR> &s, int ch, int g, ui
 // (which covers their LDS latency), then the MFMAs, reading the next A fragment two M-tiles
 // ahead (A fragments are held two at a time, not MT at a time: fewer live registers).
 template <int NR, int MT, int LK>
-__device__ __forceinline__ void stage_mfma(const WStage<NR> &s0, const uint32_t (&dl)[NR], const _Float16 *As,
-                                           int n, int g, f32x4 (&acc)[MT][NR]) {
+__device__ __forceinline__ void stage_mfma(const WStage<NR> &s0, const uint32_t (&b2)[NR], const uint32_t (&c2)[NR],
+                                           const _Float16 *As, int n, int g, f32x4 (&acc)[MT][NR]) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
         const _Float16 *ap = As + n * LK + 32 * g + 8 * ks;
@@ -384,7 +420,7 @@ __device__ __forceinline__ void stage_mfma(const WStage<NR> &s0, const uint32_t 
         for (int mt = 0; mt < (MT < 2 ? MT : 2); ++mt) av[mt] = *reinterpret_cast<const u32x4 *>(ap + 16 * mt * LK);
         u32x4 b[NR];
 #pragma unroll
-        for (int r = 0; r < NR; ++r) b[r] = dq8_f16(s0.q[r][ks], dl[r]);
+        for (int r = 0; r < NR; ++r) b[r] = dq8_f16(s0.q[r][ks], b2[r], c2[r]);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             const u32x4 cur = av[mt & 1];
@@ -437,7 +473,7 @@ __device__ __forceinline__ void wring_prologue(WStage<NR> (&ws)[RD], const WRows
 // stage_a(c) moves chunk c of A into LDS; chunk 0 is expected in LDS on entry (its loads were
 // issued before the weight ring's, so waiting for them did not wait for the weights).
 template <int NCH, int RD, int SBR, int NR, int MT, typename StageA>
-__device__ __forceinline__ void gemm_resident(WStage<NR> (&ws)[RD], const WRows (&rows)[NR],
+__device__ __forceinline__ void gemm_resident(WStage<NR> (&ws)[RD], const WRows (&rows)[NR], const float (&F)[NR],
                                               const _Float16 *As, int n, int g, f32x4 (&acc)[MT][NR],
                                               StageA stage_a) {
     constexpr int KCH = pf_kch<NCH, MT>();
@@ -450,9 +486,9 @@ __device__ __forceinline__ void gemm_resident(WStage<NR> (&ws)[RD], const WRows 
             stage_a(ch / KCH);
             lds_barrier();
         }
-        uint32_t dl[NR];
-        wstage_dl(ws[S], ch, g, dl);
-        stage_mfma<NR, MT, LK>(ws[S], dl, As + (ch % KCH) * PF_KC, n, g, acc);
+        uint32_t b2[NR], c2[NR];
+        wstage_bc(ws[S], ch, g, F, b2, c2);
+        stage_mfma<NR, MT, LK>(ws[S], b2, c2, As + (ch % KCH) * PF_KC, n, g, acc);
         // keep the scheduler from moving loads across stages: each stage's weights are
         // requested RD-1 stages ahead, in the order they are consumed
         __builtin_amdgcn_sched_barrier(0);
@@ -468,8 +504,8 @@ __device__ __forceinline__ void gemm_resident(WStage<NR> (&ws)[RD], const WRows 
 // length instead of two full ones (at M = 512, ~1140 items against ~570 of twice the length).
 template <int NCH, int RD, int SBR, int NR, int MT, typename StageA>
 __device__ __forceinline__ void gemm_resident_split(WStage<NR> (&ws)[RD], const WRows (&rows)[NR],
-                                                    const _Float16 *As, int n, int g, int p,
-                                                    f32x4 (&acc)[MT][NR], StageA stage_a) {
+                                                    const float (&F)[NR], const _Float16 *As, int n, int g,
+                                                    int p, f32x4 (&acc)[MT][NR], StageA stage_a) {
     constexpr int KCH = pf_kch<NCH, MT>();
     constexpr int LK = pf_ldsr<NCH, MT>();
     constexpr int NC2 = NCH / 2;
@@ -482,9 +518,9 @@ __device__ __forceinline__ void gemm_resident_split(WStage<NR> (&ws)[RD], const 
             lds_barrier();
         }
         const int ch = ch0 + p;
-        uint32_t dl[NR];
-        wstage_dl(ws[S], ch, g, dl);
-        stage_mfma<NR, MT, LK>(ws[S], dl, As + (ch0 % KCH + p) * PF_KC, n, g, acc);
+        uint32_t b2[NR], c2[NR];
+        wstage_bc(ws[S], ch, g, F, b2, c2);
+        stage_mfma<NR, MT, LK>(ws[S], b2, c2, As + (ch0 % KCH + p) * PF_KC, n, g, acc);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (c + RD - 1 < NC2) wstage_load<SBR>(ws[(c + RD - 1) % RD], rows, 2 * (c + RD - 1) + p, n + 16 * g);
         __builtin_amdgcn_sched_barrier(0);
@@ -565,6 +601,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
     // Weights: rows c0 + n of W1 (gate) and W3 (up).
     const WRows rows[2] = {split_rows<SBR>(expert_w(a.L.w1, a.L.s1, a.L.sw1, e, a.E), I, c0),
                            split_rows<SBR>(expert_w(a.L.w3, a.L.s3, a.L.sw3, e, a.E), I, c0)};
+    const u32x2 dq[2] = {row_dmax_load<SBR>(rows[0], n, g), row_dmax_load<SBR>(rows[1], n, g)};
 
     by_mtiles(nrows, [&](auto MTc) __attribute__((always_inline)) {
         constexpr int MT = decltype(MTc)::value;
@@ -606,6 +643,9 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
             wring_prologue<NCH, RD, SBR>(ws, rows, lane);
         }
         store_a(0, PER);
+        float F[2], P[2];
+        row_shift(dq[0], F[0], P[0]);
+        row_shift(dq[1], F[1], P[1]);
         lds_barrier();
         f32x4 acc[MT][2];
 #pragma unroll
@@ -627,7 +667,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
         constexpr int NE = 4 * MT, NOWN = SPLIT ? NE / 2 : NE;
         const int el0 = SPLIT && p ? NE / 2 : 0;
         if constexpr (SPLIT) {
-            gemm_resident_split<NCH, RD, SBR, 2, MT>(ws, rows, As, n, g, p, acc, stage_a);
+            gemm_resident_split<NCH, RD, SBR, 2, MT>(ws, rows, F, As, n, g, p, acc, stage_a);
             lds_barrier();
             float *red = reinterpret_cast<float *>(As);
             static_assert(4 * NE * 2 * 64 * 4 <= PF_AS_HALVES * 2, "the pair sums fit the A chunk");
@@ -643,11 +683,11 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
 #pragma unroll
                     for (int r = 0; r < 2; ++r) acc[el / 4][r][el % 4] += red[((cw * NE + el) * 2 + r) * 64 + lane];
         } else {
-            gemm_resident<NCH, RD, SBR, 2, MT>(ws, rows, As, n, g, acc, stage_a);
+            gemm_resident<NCH, RD, SBR, 2, MT>(ws, rows, F, As, n, g, acc, stage_a);
             lds_barrier(); // s_inv
         }
 
-        // epilogue: h = silu(g) * u with the token scale undone; per-row max|h| of the item's
+        // epilogue: h = silu(g) * u with the token scale and the row shifts undone; per-row max|h| of the item's
         // columns, then h as f16 scaled by the power of two that puts that max in [2^14, 2^15),
         // stored in the down kernel's K order (perm32_pos inside every 32-column block)
         float hv[NOWN];
@@ -661,7 +701,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
             hv[j] = 0.0f;
             if (m < nrows) {
                 const float inv = s_inv[m];
-                hv[j] = silu_rcp(gv * inv) * (uv * inv);
+                hv[j] = silu_rcp(gv * (P[0] * inv)) * (uv * (P[1] * inv));
             }
             const float rm = max16(fabsf(hv[j]));
             if (n == 0) atomicMax(&rowmax[m], __builtin_bit_cast(uint32_t, rm));
@@ -705,6 +745,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
     const int r0 = item * PF_ND + wv * 32; // this wave's output rows r0 .. r0+31
     const uint8_t *w2 = expert_w(a.L.w2, a.L.s2, a.L.sw2, e, a.E);
     const WRows rows[NTW] = {split_rows<SBR>(w2, H, r0), split_rows<SBR>(w2, H, r0 + 16)};
+    const u32x2 dq[NTW] = {row_dmax_load<SBR>(rows[0], n, g), row_dmax_load<SBR>(rows[1], n, g)};
 
     by_mtiles(nrows, [&](auto MTc) __attribute__((always_inline)) {
         constexpr int MT = decltype(MTc)::value;
@@ -765,15 +806,18 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
                 }
             }
         }
+        float F[NTW], P[NTW];
+#pragma unroll
+        for (int t = 0; t < NTW; ++t) row_shift(dq[t], F[t], P[t]);
         lds_barrier();
         f32x4 acc[MT][NTW];
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
             for (int t = 0; t < NTW; ++t) acc[i][t] = f32x4{0, 0, 0, 0};
-        gemm_resident<NCH, RD, SBR, NTW, MT>(ws, rows, As, n, g, acc, [](int) {});
+        gemm_resident<NCH, RD, SBR, NTW, MT>(ws, rows, F, As, n, g, acc, [](int) {});
 
-        // epilogue: v = c * w * 2^-s_row * acc per slot row; each row's 32 values of this
+        // epilogue: v = c * w * 2^-s_row * 2^s_n * acc per slot row (s_n: the weight row's shift); each row's 32 values of this
         // wave are stored as f16 times a power of two 2^sh that puts their max in
         // [2^14, 2^15), sh kept beside them (one byte per row and 32 columns), column n and
         // 16 + n of the block side by side (stored position 2n, 2n + 1).  Through LDS
@@ -792,7 +836,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
                 float v[NTW], mx = 0.0f;
 #pragma unroll
                 for (int t = 0; t < NTW; ++t) {
-                    v[t] = sc * acc[mt][t][i];
+                    v[t] = sc * (P[t] * acc[mt][t][i]);
                     mx = fmaxf(mx, fabsf(v[t]));
                 }
                 mx = max16(mx); // the row's 32 columns: 16 lanes x NTW
