@@ -62,6 +62,25 @@ __device__ __forceinline__ bool slot_kept(int id, int lane, int E, uint32_t &fl)
     return lane < SLOTS && id <= E && !dup;
 }
 
+// Kernel arguments a launch's chain needs, fetched at the kernel's first instructions: one asm
+// takes them all as inputs, so the compiler loads them there in one batch of scalar loads (and
+// keeps them in SGPRs; the values, and what the compiler knows of the pointers, are unchanged)
+// instead of at a first use deep in the kernel -- where it had placed the layer's pointers
+// (after the routing or the plan, in gate/up; after the ids, in down), one more scalar round trip
+// on the critical chain.
+__device__ __forceinline__ void fetch_gate_up_args(const DecodeArgs &a) {
+    asm volatile("" ::"s"(a.L.w1), "s"(a.L.w3), "s"(a.L.s1), "s"(a.L.s3), "s"(a.L.sw1), "s"(a.L.sw3), "s"(a.hbuf),
+                 "s"(a.ids), "s"(a.w), "s"(a.flags), "s"(a.plan), "s"(a.M), "s"(a.E), "s"(a.renorm), "s"(a.rmsnorm));
+}
+__device__ __forceinline__ void fetch_down_args(const DecodeArgs &a) {
+    asm volatile("" ::"s"(a.L.w2), "s"(a.L.s2), "s"(a.L.sw2), "s"(a.hbuf), "s"(a.y), "s"(a.ids), "s"(a.w), "s"(a.c),
+                 "s"(a.E), "s"(a.accumulate));
+}
+__device__ __forceinline__ void fetch_prep_args(const DecodeArgs &a) {
+    asm volatile("" ::"s"(a.x), "s"(a.logits), "s"(a.ids), "s"(a.w), "s"(a.flags), "s"(a.plan), "s"(a.E),
+                 "s"(a.renorm), "s"(a.rmsnorm));
+}
+
 // ---------------------------------------------------------------- down shape
 constexpr int DEC_ROWS = 8; // down: output rows per workgroup
 constexpr int DEC_DOWN_RING = 2; // down, 2 <= M <= 8: units of W2 rows in flight per wave
@@ -201,6 +220,7 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_m1(DecodeArgs a) {
     using S = GuShape<H, I>;
     constexpr int LPR = S::LPR, RPS = S::RPS, SPE = S::SPE, NCH = S::NCH;
     constexpr int G = 5; // steps per round of loads (one round with 256 CUs)
+    fetch_gate_up_args(a);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int gw = (int)blockIdx.x * 4 + wv, NW = (int)gridDim.x * 4;
@@ -243,9 +263,8 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_m1(DecodeArgs a) {
     };
     uint32_t xh[8], xl[8];
     float sx = 0.f, inv = 1.0f;
-    bool staged = false;
-    for (int k0 = 0; k0 < nk; k0 += G) {
-        GuLoad ld[G];
+    GuLoad ld[G];
+    auto issue = [&](int k0) __attribute__((always_inline)) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const int st = min(gw + (k0 + g) * NW, NS - 1); // past the last step: a valid re-read
@@ -254,13 +273,8 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_m1(DecodeArgs a) {
             ld[g] = gu_load<H, I>(expert_w(a.L.w1, a.L.s1, a.L.sw1, e, a.E),
                                   expert_w(a.L.w3, a.L.s3, a.L.sw3, e, a.E), rs * RPS + rr, sb, ib);
         }
-        if (!staged) {
-            // the activations as int8 planes while the weights are in flight
-            float ss;
-            quant_chunk(xv, xh, xl, sx, ss);
-            inv = rms_factor(a.rmsnorm, wave_sum(lane < NCH ? ss : 0.f), H);
-            staged = true;
-        }
+    };
+    auto compute = [&](int k0) __attribute__((always_inline)) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const int st = gw + (k0 + g) * NW;
@@ -269,6 +283,21 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_m1(DecodeArgs a) {
             GuDec d;
             gu_decode(ld[g], ib, d);
             gu_row<LPR>(d, xh, xl, sx, inv, a.hbuf + (size_t)slot_of(u) * I + rs * RPS + rr, gsb, lane);
+        }
+    };
+    if (nk > 0) {
+        issue(0);
+        // the activations as int8 planes while the weights are in flight.  The barrier keeps
+        // this ~500-instruction block (invariant over the rounds) behind the weight requests:
+        // the compiler had hoisted it between the routing and the first load (~1 us per call).
+        __builtin_amdgcn_sched_barrier(0);
+        float ss;
+        quant_chunk(xv, xh, xl, sx, ss);
+        inv = rms_factor(a.rmsnorm, wave_sum(lane < NCH ? ss : 0.f), H);
+        compute(0);
+        for (int k0 = G; k0 < nk; k0 += G) {
+            issue(k0);
+            compute(k0);
         }
     }
 }
@@ -288,6 +317,7 @@ __global__ __launch_bounds__(256) void k_dec_prep(DecodeArgs a) {
     static_assert(NCH * LPC <= 256 && (LPC & (LPC - 1)) == 0 && QPL >= 1 && QPL <= 2, "chunk lanes");
     __shared__ RouteLds R;
     __shared__ float s_ss[4];
+    fetch_prep_args(a);
     PL *P = reinterpret_cast<PL *>(a.plan);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -387,6 +417,7 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_mt(DecodeArgs a) {
     __shared__ uint32_t owner[DEC_EMAX]; // first valid pair naming each expert (all ones: none)
     __shared__ uint16_t pid[DEC_MAXP];
     __shared__ float s_ss[MT][4];
+    fetch_gate_up_args(a);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int gw = (int)blockIdx.x * 4 + wv, NW = (int)gridDim.x * 4;
@@ -727,15 +758,18 @@ __global__ __launch_bounds__(64 * SLOTS) void k_dec_down_m1(DecodeArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n0 = blockIdx.x * DEC_ROWS;
+    fetch_down_args(a);
     float yres = 0.f;
     if (a.accumulate && tid < DEC_ROWS) yres = a.y[n0 + tid];
     const int idl = lane < SLOTS ? (int)a.ids[lane] : 0;
+    // the slot's weight requested beside the ids (the weight rows wait for the ids, not for it)
+    const float wsl = ldg<float>(a.w + wv);
     const int e = __builtin_amdgcn_readlane(idl, wv);
     bool ok = e <= a.E;
     for (int s2 = 0; s2 < wv; ++s2) ok = ok && __builtin_amdgcn_readlane(idl, s2) != e;
     const int gsb = lane % LPR, rr = lane / LPR, sb = gsb >> 3, ib = gsb & 7;
     if (ok) {
-        const float wq = a.c * a.w[wv];
+        const float wq = a.c * wsl;
         const uint8_t *W2 = expert_w(a.L.w2, a.L.s2, a.L.sw2, e, a.E);
         u32x4 qs[STEPS];
         u32x2 hd[STEPS];
