@@ -577,6 +577,20 @@ __device__ __forceinline__ void xcd_tile_item(int &tile, int &item) {
 // ---------------------------------------------------------------- gate/up
 // SPLIT: PF_NGU columns per item, two waves per 16 columns on alternate stages; else
 // PF_NGU_WIDE columns, one wave per 16 columns on every stage.
+// Kernel arguments a work item's chain needs, fetched at the kernel's first instructions: one
+// asm takes them all as inputs, so the compiler loads them in one batch of scalar loads (the
+// values and the pointers' address space unchanged) instead of one at a time at each first use
+// -- the tile list, then the token ids, then the layer's pointers, then the A rows' base, each
+// with its own wait between the tile record and the first A load.
+__device__ __forceinline__ void fetch_gate_up_args(const PrefillArgs &a) {
+    asm volatile("" ::"s"(a.tiles), "s"(a.tile_max), "s"(a.sorted_tok), "s"(a.xinv), "s"(a.xh), "s"(a.L.w1),
+                 "s"(a.L.w3), "s"(a.L.s1), "s"(a.L.s3), "s"(a.L.sw1), "s"(a.L.sw3), "s"(a.E), "s"(a.hh), "s"(a.hmax));
+}
+__device__ __forceinline__ void fetch_down_args(const PrefillArgs &a) {
+    asm volatile("" ::"s"(a.tiles), "s"(a.tile_max), "s"(a.L.w2), "s"(a.L.s2), "s"(a.L.sw2), "s"(a.E), "s"(a.hh),
+                 "s"(a.hmax), "s"(a.sorted_w), "s"(a.c), "s"(a.part), "s"(a.pexp));
+}
+
 template <int H, int I, bool SPLIT>
 __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) {
     constexpr int NGU = SPLIT ? PF_NGU : PF_NGU_WIDE;
@@ -588,6 +602,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
     __shared__ uint32_t rowmax[PF_BM];
     __shared__ float s_inv[PF_BM];
     __shared__ int s_tok[PF_BM];
+    fetch_gate_up_args(a);
 
     int ti, item;
     xcd_tile_item<I / NGU, !SPLIT>(ti, item);
@@ -747,6 +762,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
     static_assert(pf_kch<NCH, 4>() == NCH, "all of K = inter resident in one chunk");
     __shared__ __attribute__((aligned(16))) _Float16 As[PF_AS_HALVES];
     __shared__ float s_sc[PF_BM];
+    fetch_down_args(a);
 
     int ti, item;
     xcd_tile_item<H / PF_ND, NGU == PF_NGU_WIDE>(ti, item);
