@@ -591,6 +591,13 @@ __device__ __forceinline__ void fetch_down_args(const PrefillArgs &a) {
                  "s"(a.hmax), "s"(a.sorted_w), "s"(a.c), "s"(a.part), "s"(a.pexp));
 }
 
+// A tile record in one 16-byte load (read field by field, the compiler fetched the expert, tested
+// it, and only then fetched row0 and nrows: one more round trip before the A rows).
+__device__ __forceinline__ Tile tile_record(const Tile *tiles, int ti) {
+    const u32x4 v = ldg<u32x4>(tiles + ti);
+    return Tile{(int32_t)v[0], (int32_t)v[1], (int32_t)v[2], 0};
+}
+
 template <int H, int I, bool SPLIT>
 __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) {
     constexpr int NGU = SPLIT ? PF_NGU : PF_NGU_WIDE;
@@ -607,7 +614,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
     int ti, item;
     xcd_tile_item<I / NGU, !SPLIT>(ti, item);
     if (ti >= a.tile_max) return;
-    const Tile tl = a.tiles[ti];
+    const Tile tl = tile_record(a.tiles, ti);
     if (tl.expert < 0) return;
     const int e = tl.expert, row0 = tl.row0, nrows = tl.nrows;
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform (SGPR)
@@ -628,7 +635,6 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
     // Weights: rows c0 + n of W1 (gate) and W3 (up).
     const WRows rows[2] = {split_rows<SBR>(expert_w(a.L.w1, a.L.s1, a.L.sw1, e, a.E), I, c0),
                            split_rows<SBR>(expert_w(a.L.w3, a.L.s3, a.L.sw3, e, a.E), I, c0)};
-    const u32x2 dq[2] = {row_dmax_load<SBR>(rows[0], n, g), row_dmax_load<SBR>(rows[1], n, g)};
 
     by_mtiles(nrows, [&](auto MTc) __attribute__((always_inline)) {
         constexpr int MT = decltype(MTc)::value;
@@ -660,6 +666,10 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_gate_up(PrefillArgs a) 
         constexpr int RD = 3; // weight ring depth: two stages ahead (register budget)
         WStage<2> ws[RD];
         load_a(0, 0, PER);
+        // the rows' headers for their shifts after A and before the first weights (requested
+        // ahead of A, their registers were reused by A's addressing and the A loads waited for
+        // them; requested after the weights, the first stage would wait for all of those)
+        const u32x2 dq[2] = {row_dmax_load<SBR>(rows[0], n, g), row_dmax_load<SBR>(rows[1], n, g)};
         if constexpr (SPLIT) {
 #pragma unroll
             for (int c = 0; c < RD - 1; ++c) {
@@ -767,7 +777,7 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
     int ti, item;
     xcd_tile_item<H / PF_ND, NGU == PF_NGU_WIDE>(ti, item);
     if (ti >= a.tile_max) return;
-    const Tile tl = a.tiles[ti];
+    const Tile tl = tile_record(a.tiles, ti);
     if (tl.expert < 0) return;
     const int e = tl.expert, row0 = tl.row0, nrows = tl.nrows;
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform (SGPR)
@@ -775,7 +785,6 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
     const int r0 = item * PF_ND + wv * 32; // this wave's output rows r0 .. r0+31
     const uint8_t *w2 = expert_w(a.L.w2, a.L.s2, a.L.sw2, e, a.E);
     const WRows rows[NTW] = {split_rows<SBR>(w2, H, r0), split_rows<SBR>(w2, H, r0 + 16)};
-    const u32x2 dq[NTW] = {row_dmax_load<SBR>(rows[0], n, g), row_dmax_load<SBR>(rows[1], n, g)};
 
     by_mtiles(nrows, [&](auto MTc) __attribute__((always_inline)) {
         constexpr int MT = decltype(MTc)::value;
@@ -804,6 +813,9 @@ __global__ __launch_bounds__(64 * PF_WAVES, 4) void k_pf_down(PrefillArgs a) {
                 sw[j] = ab == 0 ? a.sorted_w[slot] : 0.0f;
             }
         }
+        // the rows' headers for their shifts after the h rows, before the weights (requested
+        // first, their registers were reused by the h rows' addressing and the h loads waited)
+        const u32x2 dq[NTW] = {row_dmax_load<SBR>(rows[0], n, g), row_dmax_load<SBR>(rows[1], n, g)};
         constexpr int RD = 4; // weight ring depth: three stages ahead
         WStage<NTW> ws[RD];
         wring_prologue<NCH, RD, SBR>(ws, rows, lane);
