@@ -402,6 +402,51 @@ def test_prefill_zero_block_small_activations(gpu, orc):
         ctx.close()
 
 
+def test_prefill_row_scale_extremes(gpu, orc):
+    """Super-block scales d that stress the prefill decode's per-row shift (weights enter the
+    MFMA as dl * kv * 2^-s, s from the row's largest |d|): in rows 0..3 of every expert's W1,
+    W3 and W2 -- one large d among minimum-subnormal ones, all zero, all subnormal, and mixed
+    signs over five binades.  Prefill (M = 40) and decode (M = 3) against the oracle, which
+    decodes the same bytes."""
+    import torch
+    hidden, inter, nexp = H, I, E
+    ctx = gpu.Context(hidden, inter, nexp, 1, 64, gpu.W_REF)
+    try:
+        buf = gpu.gen_layer(hidden, inter, nexp, 3501)
+        mb = gpu.matrix_bytes(hidden, inter)
+        host = buf.cpu().numpy()
+        f16 = lambda v: np.frombuffer(np.float16(v).tobytes(), dtype=np.uint8)
+        for e in range(nexp + 1):
+            for mi, k in ((0, hidden), (1, hidden), (2, inter)):  # W1, W3 ([inter][hidden]), W2 ([hidden][inter])
+                nsb = k // 256
+                for row in range(4):
+                    base = e * 3 * mb + mi * mb + row * nsb * 136
+                    for sb in range(nsb):
+                        if row == 0:
+                            d = 0.25 if sb == 0 else float(np.float16(2.0 ** -24)) * (sb + 1)
+                        elif row == 1:
+                            d = 0.0
+                        elif row == 2:
+                            d = float(np.float16(3 * 2.0 ** -24)) * (1 if sb % 2 else -1)
+                        else:
+                            d = (-0.03 if sb % 2 else 0.001) * (2.0 ** -(sb % 5))
+                        host[base + sb * 136: base + sb * 136 + 2] = f16(d)
+        buf = torch.from_numpy(host).cuda()
+        ctx.bind_packed(0, buf)
+        layer = Layer(gpu, orc, None, hidden, inter, nexp, dev=buf)
+        for M, seed in ((40, 3502), (3, 3505)):
+            x = gpu.gen_normal(M * hidden, seed).view(M, hidden)
+            ids, w = ctx.router_topk(gpu.gen_logits(M, nexp, seed + 1))
+            y = ctx.ffn(0, x, ids, w)
+            torch.cuda.synchronize()
+            assert torch.isfinite(y).all()
+            ref = orc.moe_ffn(layer.host(), x.cpu().numpy(), ids.cpu().numpy(), w.cpu().numpy(), 1.0 / 9)
+            log(f"row scale extremes, M={M}")
+            check_errs(y.cpu().numpy(), ref, M <= 8)
+    finally:
+        ctx.close()
+
+
 def test_decode_graph_replays(gpu, full):
     """Graph replays of the decode path, with eager calls of another M in between, each equal
     the eager result bit for bit."""
