@@ -67,10 +67,17 @@ def capture(torch, fn):
     return g
 
 
-def timed_graphs(torch, step, n, warm, per_graph):
+# untimed replays before the timed replay of every leg but the headline (which honours --warmup)
+SETTLE_MS = 20.0
+
+
+def timed_graphs(torch, step, n, warm, per_graph, settle_ms=0.0):
     """Steps warm..n-1 replayed from graphs of per_graph steps after `warm` eager steps and
     one untimed replay of every graph (a graph's first launch pays its one-time upload, ~0.1 ms
-    here, which is not a cost of the steps); returns (wall us per step, event us per step)."""
+    here, which is not a cost of the steps); with settle_ms, the graphs are replayed, untimed,
+    for that long first (the shader clock ramps up under sustained load: config 3 at M = 8
+    went 41.9 -> 37.5 us per step over a dozen back-to-back timings).  Returns (wall us per
+    step, event us per step)."""
     for s in range(warm):
         step(s)
     torch.cuda.synchronize()
@@ -79,6 +86,11 @@ def timed_graphs(torch, step, n, warm, per_graph):
     for g in graphs:
         g.replay()
     torch.cuda.synchronize()
+    t_settle = time.perf_counter()
+    while (time.perf_counter() - t_settle) * 1e3 < settle_ms:
+        for g in graphs:
+            g.replay()
+        torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     ev0.record()
@@ -243,13 +255,13 @@ def leg_decode(torch, pkg, ctx, K, W, eager, nl=LAYERS):
     # Graphs of 8 consecutive tokens: in a serving loop the stack launch sits inside the
     # model's per-token graph, so the host-to-GPU gap between two separately launched graphs
     # is not a cost of this path.  The one-graph-per-token rate is logged beside it.
-    us, us_ev = timed_graphs(torch, token, nsteps, W, 8)
+    us, us_ev = timed_graphs(torch, token, nsteps, W, 8)  # the headline: W eager tokens only
     gbs = DECODE_BYTES_PER_TOKEN / (us * 1e-6) / 1e9
     log(f"decode: {us:.1f} us/token ({us_ev:.1f} us by events; graphs of 8 tokens), "
         f"{gbs:.1f} GB/s = {100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak")
     assert torch.isfinite(x).all(), "decode chain produced non-finite values"
     assert ctx.device_flags() == 0, "decode stack raised a device flag"
-    _, us_one = timed_graphs(torch, token, nsteps, W, 1)
+    _, us_one = timed_graphs(torch, token, nsteps, W, 1, SETTLE_MS)
     log(f"decode, one graph per token: {us_one:.1f} us/token")
     kern = kernel_times(ctx, lambda: [token(s) for s in range(W, min(nsteps, W + 8))], 64)
     log(f"decode kernels: {kern}")
@@ -278,7 +290,7 @@ def leg_decode_routed(torch, pkg, ctx, routers, K, W, eager):
             token(s)
         torch.cuda.synchronize()
         return None
-    us, us_ev = timed_graphs(torch, token, nsteps, W, 8)
+    us, us_ev = timed_graphs(torch, token, nsteps, W, 8, SETTLE_MS)
     gbs = DECODE_ROUTED_BYTES_PER_TOKEN / (us * 1e-6) / 1e9
     assert torch.isfinite(x).all() and ctx.device_flags() == 0
     kern = kernel_times(ctx, lambda: [token(s) for s in range(W, min(nsteps, W + 8))], 64)
@@ -323,9 +335,9 @@ def leg_config0(torch, pkg, ctx, routers, eager):
             step_gemv(s)
         torch.cuda.synchronize()
         return None
-    us, us_ev = timed_graphs(torch, step, n, warm, 8)
+    us, us_ev = timed_graphs(torch, step, n, warm, 8, SETTLE_MS)
     gbs = DECODE_BYTES_PER_LAYER / (us * 1e-6) / 1e9
-    us_g, _ = timed_graphs(torch, step_gemv, n, warm, 8)
+    us_g, _ = timed_graphs(torch, step_gemv, n, warm, 8, SETTLE_MS)
     gbs_g = (DECODE_BYTES_PER_LAYER + ROUTER_BYTES) / (us_g * 1e-6) / 1e9
     kern = kernel_times(ctx, lambda: [step(s) for s in range(warm, warm + 64)], 256)
     kern_g = kernel_times(ctx, lambda: [step_gemv(s) for s in range(warm, warm + 64)], 512)
@@ -371,7 +383,7 @@ def leg_prefill(torch, pkg, ctx, PK, eager):
             prefill(s)
         torch.cuda.synchronize()
         return None
-    us, _ = timed_graphs(torch, prefill, pn, pw, 5)
+    us, _ = timed_graphs(torch, prefill, pn, pw, 5, SETTLE_MS)
     p_ms = us * 1e-3
     tflops = PREFILL_FLOPS / (us * 1e-6) / 1e12
     active = [int(torch.unique(pids[s].view(-1).to(torch.int32)).numel()) for s in range(pw, pn)]
@@ -417,7 +429,7 @@ def leg_config3(torch, pkg, ctx, eager):
                 step3(s)
             torch.cuda.synchronize()
             continue
-        us3, _ = timed_graphs(torch, step3, n3, 3, 5)
+        us3, _ = timed_graphs(torch, step3, n3, 3, 5, SETTLE_MS)
         nexp = [int(torch.unique(i3[s].view(-1).to(torch.int32)).numel()) for s in range(3, n3)]
         b3 = sum(nexp) / len(nexp) * EXPERT_BYTES + Mv * TOKEN_IO_BYTES
         gbs3 = b3 / (us3 * 1e-6) / 1e9
@@ -459,7 +471,7 @@ def leg_config4(torch, pkg, layer0, eager):
         torch.cuda.synchronize()
         ctx4.close()
         return None
-    us4, _ = timed_graphs(torch, step4, n4, 2, 1)
+    us4, _ = timed_graphs(torch, step4, n4, 2, 1, SETTLE_MS)
     kern4 = kernel_times(ctx4, lambda: [step4(s) for s in range(2, n4)], 256)
     ctx4.close()
     fl4 = 2 * (9 * M4) * 3 * I * H
@@ -476,7 +488,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=40)  # ~10 ms of eager tokens: the clock ramps up
     ap.add_argument("--prefill-steps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
