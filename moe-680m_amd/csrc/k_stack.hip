@@ -1018,9 +1018,12 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             if (w == 0) STK_MARK(STK_EV_ROUTED, li);
             prefetch_a(li);
             __builtin_amdgcn_s_setprio(1);
-            prefetch_b(li);
             __builtin_amdgcn_sched_barrier(0);
             decode_a();
+            // this layer's W2 rows only once its W1/W3 rows are in: the 9.4 MB of phase A no
+            // longer share the HBM queue with them (phase B needs them only after the h exchange)
+            prefetch_b(li);
+            __builtin_amdgcn_sched_barrier(0);
         } else {
             // phase A ahead of the other compute wave's decode on this SIMD
             __builtin_amdgcn_s_setprio(1);
