@@ -828,13 +828,8 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     auto prefetch_a = [&](int li) __attribute__((always_inline)) {
         const uint8_t *W1 = rt_p[li % 3][0][0];
         const uint8_t *W3 = rt_p[li % 3][0][1];
-#pragma unroll
-        for (int st = 0; st < STA; ++st) {
-            aq1[st] = ldg<u32x4>(W1 + offA[st]);
-            aq3[st] = ldg<u32x4>(W3 + offA[st]);
-        }
-        saq = ldg<u32x2>(rt_p[li % 3][1][mA] + offSA);
-        // every header of the layer (phase B's too: used before the next such load)
+        // every header of the layer (phase B's too: used before the next such load) -- AR:
+        // requested first, so that each step of phase A waits only for its own rows
         const uint64_t b2 = (uint64_t)rt_p[li % 3][1][0], b3 = (uint64_t)rt_p[li % 3][1][1];
         const uint64_t b4 = (uint64_t)rt_p[li % 3][0][2], b5 = (uint64_t)rt_p[li % 3][1][2];
         uint64_t hb = (uint64_t)W1;
@@ -843,7 +838,15 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         hb = hsel == 3 ? b3 : hb;
         hb = hsel == 4 ? b4 : hb;
         hb = hsel == 5 ? b5 : hb;
-        const u32x2 hd = ldg<u32x2>((const uint8_t *)hb + hoff);
+        u32x2 hd;
+        if constexpr (AR) hd = ldg<u32x2>((const uint8_t *)hb + hoff);
+#pragma unroll
+        for (int st = 0; st < STA; ++st) {
+            aq1[st] = ldg<u32x4>(W1 + offA[st]);
+            aq3[st] = ldg<u32x4>(W3 + offA[st]);
+        }
+        saq = ldg<u32x2>(rt_p[li % 3][1][mA] + offSA);
+        if constexpr (!AR) hd = ldg<u32x2>((const uint8_t *)hb + hoff);
         hd0 = hd.x;
         hd1 = hd.y;
     };
@@ -887,6 +890,25 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(ak1[st][e]), "+v"(ak3[st][e]));
         asm volatile("" : "+v"(sak[0]), "+v"(sak[1]), "+v"(sak[2]), "+v"(sak[3]));
         asm volatile("" : "+v"(as1), "+v"(as3), "+v"(sas));
+    };
+
+    // AR: decode_a in pieces, each waiting only for its own loads (the headers, requested
+    // first, with the first): step st of the slot rows, then the shared rows
+    auto decode_a_step = [&](int st) __attribute__((always_inline)) {
+        asm volatile("" : "+v"(aq1[st]), "+v"(aq3[st]), "+v"(hd0), "+v"(hd1));
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            kv_signed8(aq1[st][d], ak1[st][2 * d], ak1[st][2 * d + 1]);
+            kv_signed8(aq3[st][d], ak3[st][2 * d], ak3[st][2 * d + 1]);
+        }
+        as1[st] = sub_scale(header(hA1[st]), ib1);
+        as3[st] = sub_scale(header(hA3[st]), ib1);
+    };
+    auto decode_a_shared = [&]() __attribute__((always_inline)) {
+        asm volatile("" : "+v"(saq));
+        kv_signed8(saq[0], sak[0], sak[1]);
+        kv_signed8(saq[1], sak[2], sak[3]);
+        sas = sub_scale(header(hSA), sbg & 7);
     };
 
     auto decode_b = [&]() __attribute__((always_inline)) {
@@ -1019,11 +1041,9 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             prefetch_a(li);
             __builtin_amdgcn_s_setprio(1);
             __builtin_amdgcn_sched_barrier(0);
-            decode_a();
-            // this layer's W2 rows only once its W1/W3 rows are in: the 9.4 MB of phase A no
-            // longer share the HBM queue with them (phase B needs them only after the h exchange)
-            prefetch_b(li);
-            __builtin_amdgcn_sched_barrier(0);
+            // phase A below decodes and computes step by step as the rows arrive; this layer's
+            // W2 rows are requested once its W1/W3 rows are in (the 9.4 MB of phase A then do
+            // not share the HBM queue with them; phase B needs them after the h exchange)
         } else {
             // phase A ahead of the other compute wave's decode on this SIMD
             __builtin_amdgcn_s_setprio(1);
@@ -1066,12 +1086,17 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             uint32_t *hb = hbuf(li);
 #pragma unroll
             for (int st = 0; st < STA; ++st) {
+                if constexpr (AR) {
+                    decode_a_step(st);
+                    if (st == STA - 1) prefetch_b(li);
+                }
                 float g = (as1[st] * sx) * subblock_idot(ak1[st], xh, xl);
                 float u = (as3[st] * sx) * subblock_idot(ak3[st], xh, xl);
                 g = inv * row_total<LPR1>(g);
                 u = inv * row_total<LPR1>(u);
                 if (g1 == LPR1_LAST && !ab) tag_store_local(hb + rowA + st * RPS1 + rr1, silu_rcp(g) * u);
             }
+            if constexpr (AR) decode_a_shared();
             int sah_i = 0, sal_i = 0;
             dword_idot(sak[0], sak[1], sxh0[0], sxh1[0], sxl0[0], sxl1[0], sah_i, sal_i);
             dword_idot(sak[2], sak[3], sxh0[1], sxh1[1], sxl0[1], sxl1[1], sah_i, sal_i);
