@@ -961,6 +961,21 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             asm volatile("" : "+v"(rq[0].x));
         }
     };
+    // AR, IQ4_XS: the row's codebook bytes and scale, looked up while x is exchanged (after the
+    // row's loads, before B1): router_dot then runs only the dot products
+    uint32_t rkv[8];
+    float rsc = 0.f;
+    auto rg_decode = [&]() __attribute__((always_inline)) {
+        if (rg_type == MOE_WG_IQ4_XS) {
+            asm volatile("" : "+v"(rq[0]), "+v"(rgh));
+#pragma unroll
+            for (int d = 0; d < 4; ++d) kv_signed8(rq[0][d], rkv[2 * d], rkv[2 * d + 1]);
+            rsc = sub_scale(rgh, g1 & 7);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(rkv[e]));
+            asm volatile("" : "+v"(rsc));
+        }
+    };
     // AR: the logit of row rG against x_li (xin = RMSNorm(x) when asked, as phase A), published
     // in this XCD's logit block of layer li
     auto router_dot = [&](int li) __attribute__((always_inline)) {
@@ -990,10 +1005,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) rq[i] = ldg<u32x4>(rg_row + 16 * i);
         if (rg_type == MOE_WG_IQ4_XS) {
-            uint32_t kv[8];
-#pragma unroll
-            for (int d = 0; d < 4; ++d) kv_signed8(rq[0][d], kv[2 * d], kv[2 * d + 1]);
-            part = (sub_scale(rgh, g1 & 7) * sx) * subblock_idot(kv, xh, xl);
+            part = (rsc * sx) * subblock_idot(rkv, xh, xl);
         } else {
             // element 4i + b of the chunk: weight word i, byte / half b; planes dword i, byte
             // b, read biased (xh + 128, by v_cvt_f32_ubyte) with the bias removed once:
@@ -1025,6 +1037,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
 
     if constexpr (AR) {
         rg_prefetch(0);
+        rg_decode();
     } else {
         prefetch_a(0);
         decode_a();
@@ -1042,8 +1055,9 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             __builtin_amdgcn_s_setprio(1);
             __builtin_amdgcn_sched_barrier(0);
             // phase A below decodes and computes step by step as the rows arrive; this layer's
-            // W2 rows are requested once its W1/W3 rows are in (the 9.4 MB of phase A then do
-            // not share the HBM queue with them; phase B needs them after the h exchange)
+            // W2 rows are requested once the first step's W1/W3 rows are in, not with them (the
+            // 9.4 MB of phase A would share the HBM queue with them; phase B needs them only
+            // after the h exchange)
         } else {
             // phase A ahead of the other compute wave's decode on this SIMD
             __builtin_amdgcn_s_setprio(1);
@@ -1088,7 +1102,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             for (int st = 0; st < STA; ++st) {
                 if constexpr (AR) {
                     decode_a_step(st);
-                    if (st == STA - 1) prefetch_b(li);
+                    if (st == 0) prefetch_b(li);
                 }
                 float g = (as1[st] * sx) * subblock_idot(ak1[st], xh, xl);
                 float u = (as3[st] * sx) * subblock_idot(ak3[st], xh, xl);
@@ -1165,7 +1179,10 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         lds_barrier(); // B3: every wave past phase B
         // the pollers now gather the partials and exchange x: decode layer li+1's phase-A
         // weights (requested at B2) meanwhile -- or, AR, request layer li+1's router rows
-        if constexpr (AR) rg_prefetch(min(li + 1, n - 1));
+        if constexpr (AR) {
+            rg_prefetch(min(li + 1, n - 1));
+            rg_decode();
+        }
         else decode_a();
     }
 }
