@@ -80,7 +80,10 @@ enum StackTraceEvent {
     STK_EV_GATHER = 8,  // first poller: the eight partials gathered
     STK_EV_XPUB = 9,    // first poller: x_{l+1} published (or y stored, last layer)
     STK_EV_XPOLL = 10,  // second poller: its x_{l+1} wait satisfied
-    STK_TRACE_EV_USED = 11
+    STK_EV_LGPOLL = 11, // router wave (activation routing only): the XCD's logits gathered
+    STK_EV_TOP8 = 12,   // router wave (activation routing only): top-8 computed
+    STK_EV_RING = 13,   // router wave (activation routing only): ring slot written
+    STK_TRACE_EV_USED = 14
 };
 static_assert(STK_TRACE_EV_USED <= STK_TRACE_EV, "trace record");
 #ifdef MOE_STACK_TRACE
@@ -450,6 +453,7 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                     // a wait that gives up leaves the abort flag set: stale logits then still
                     // route to valid expert ids, and nothing computed from them is published
                     (void)poll_until_tagged<1>(v, q, ld, a.flags, atag, a.spin_max, abort_lds);
+                    STK_MARK(STK_EV_LGPOLL, li);
                     if (lane < nq) *reinterpret_cast<f32x4 *>(s_lg + 4 * lane) = __builtin_bit_cast(f32x4, v[0]);
                     // lanes read what other lanes of this wave wrote: LDS keeps a wave's
                     // accesses in order, the compiler must too
@@ -461,8 +465,10 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
                     float wt;
                     __builtin_amdgcn_s_setprio(3);
                     route_values<4>(raw, a.E, a.renorm, lane, id, wt);
+                    STK_MARK(STK_EV_TOP8, li);
                     __builtin_amdgcn_s_setprio(0);
                     ring_write(li, id, wt, L);
+                    STK_MARK(STK_EV_RING, li);
                 }
                 lds_barrier(); // BR: routing of li in LDS
                 lds_barrier(); // B2

@@ -378,8 +378,8 @@ __device__ __forceinline__ void load_logits(const float *__restrict__ l, int E, 
 // the top-8 sum over ranks 0..7 -- which route_wg4 keeps too, so every routing site agrees bit
 // for bit.
 template <int NV>
-__device__ __forceinline__ void route_values(const float (&raw)[NV], int E, int renorm, int lane, int &id,
-                                             float &wt) {
+__device__ __forceinline__ void route_values_exact(const float (&raw)[NV], int E, int renorm, int lane, int &id,
+                                                   float &wt) {
     float kf[NV], ex[NV];
     uint32_t ord[NV];
 #pragma unroll
@@ -422,6 +422,95 @@ __device__ __forceinline__ void route_values(const float (&raw)[NV], int E, int 
         s8 += e;
         if (lane == r) {
             my_id = w + 64 * jw;
+            my_e = e;
+        }
+    }
+    float Z = wave_sum(ex[0]);
+#pragma unroll
+    for (int j = 1; j < NV; ++j) Z += wave_sum(ex[j]);
+    id = my_id;
+    wt = (lane < TOPK) ? my_e / (renorm ? s8 : Z) : 1.0f;
+}
+
+// The same routing, faster where no two of the winning keys tie (the common case), and
+// bit for bit equal to route_values_exact: each lane sorts its NV keys once (key desc, j asc), a
+// round is then the wave max of the lanes' first keys and a shift on the lanes holding it, with
+// nothing else on the rounds' dependency chain -- the round's ballot, the winner's index and
+// softmax term are kept and read after the rounds.  A round whose key several lanes hold (a
+// tie, where the exact rule picks the lowest index among them) sends the call to
+// route_values_exact, from the start.
+template <int NV>
+__device__ __forceinline__ void route_values(const float (&raw)[NV], int E, int renorm, int lane, int &id,
+                                             float &wt) {
+    float kf[NV], ex[NV], es[NV];
+    uint32_t key[NV], js[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int i = lane + 64 * j;
+        kf[j] = (i < E) ? router_key(raw[j]) : -INFINITY;
+        key[j] = (i < E) ? ord32(kf[j]) : 0u; // 0 sorts below every real key (-inf is 0x007FFFFF)
+        js[j] = (uint32_t)j;
+    }
+    uint32_t k0 = key[0];
+#pragma unroll
+    for (int j = 1; j < NV; ++j) k0 = max(k0, key[j]);
+    const uint32_t K0 = wave_max_last_u32(k0);
+    const float m = unord32(K0);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        ex[j] = (lane + 64 * j < E) ? ((kf[j] == m) ? 1.0f : expf(kf[j] - m)) : 0.0f;
+        es[j] = ex[j];
+    }
+    // insertion sort: strictly greater keys move up, so equal keys keep ascending j
+#pragma unroll
+    for (int a = 1; a < NV; ++a)
+#pragma unroll
+        for (int b = a; b > 0; --b) {
+            const bool sw = key[b] > key[b - 1];
+            const uint32_t ka = key[b - 1], kb = key[b], ja = js[b - 1], jb = js[b];
+            const float ea = es[b - 1], eb = es[b];
+            key[b - 1] = sw ? kb : ka;
+            key[b] = sw ? ka : kb;
+            js[b - 1] = sw ? jb : ja;
+            js[b] = sw ? ja : jb;
+            es[b - 1] = sw ? eb : ea;
+            es[b] = sw ? ea : eb;
+        }
+    uint64_t hit[TOPK];
+    uint32_t ri[TOPK];
+    float re[TOPK];
+#pragma unroll
+    for (int r = 0; r < TOPK; ++r) {
+        const uint32_t K = r == 0 ? K0 : wave_max_last_u32(key[0]);
+        const bool eq = key[0] == K;
+        hit[r] = __ballot(eq);
+        ri[r] = eq ? (uint32_t)(lane + 64 * (int)js[0]) : 0u;
+        re[r] = eq ? es[0] : 0.0f;
+#pragma unroll
+        for (int p = 0; p < NV - 1; ++p) {
+            key[p] = eq ? key[p + 1] : key[p];
+            js[p] = eq ? js[p + 1] : js[p];
+            es[p] = eq ? es[p + 1] : es[p];
+        }
+        key[NV - 1] = eq ? 0u : key[NV - 1];
+    }
+    bool tie = false;
+#pragma unroll
+    for (int r = 0; r < TOPK; ++r) tie = tie || __builtin_popcountll(hit[r]) != 1;
+    if (tie) {
+        route_values_exact<NV>(raw, E, renorm, lane, id, wt);
+        return;
+    }
+    float s8 = 0.f, my_e = 1.0f;
+    int my_id = E;
+#pragma unroll
+    for (int r = 0; r < TOPK; ++r) {
+        const int w = (int)__builtin_ctzll(hit[r]);
+        const int ir = __builtin_amdgcn_readlane((int)ri[r], w);
+        const float e = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, re[r]), w));
+        s8 += e;
+        if (lane == r) {
+            my_id = ir;
             my_e = e;
         }
     }
