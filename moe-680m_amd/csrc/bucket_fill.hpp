@@ -185,7 +185,8 @@ __device__ __forceinline__ void bucket_lists(const BucketArgs &a, BucketScan S, 
 
 // Phases 2a/2b and the lists: exclusive scan of each bucket's chunk counts in place, bucket
 // totals, ranges, and the tile lists.  Every thread of the workgroup; ends with a barrier.
-// 2a loads B counts at a time as independent loads before any is overwritten.
+// 2a loads B counts at a time as independent loads before any is overwritten (B = 16: with 64
+// the chunks' uniform offsets took 128 SGPRs, 112 of them spilled).
 template <int B>
 __device__ __forceinline__ void bucket_scan_and_lists(const BucketArgs &a, CntLayout CL, int nch, BucketScan S) {
     const int E1 = a.E1;
@@ -277,7 +278,7 @@ __device__ __forceinline__ void bucket_count_chunk(const BucketArgs &a, int c) {
 
 __device__ __forceinline__ void bucket_scan_wg(const BucketArgs &a) {
     extern __shared__ uint32_t smem[];
-    bucket_scan_and_lists<64>(a, bucket_global_cnt(a), (a.M + 63) / 64, bucket_scan_lds(smem, a.E1));
+    bucket_scan_and_lists<16>(a, bucket_global_cnt(a), (a.M + 63) / 64, bucket_scan_lds(smem, a.E1));
 }
 
 __device__ __forceinline__ void bucket_scatter_chunk(const BucketArgs &a, int c) {
