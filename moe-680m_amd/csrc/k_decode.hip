@@ -789,7 +789,7 @@ __global__ __launch_bounds__(64 * SLOTS) void k_dec_down_m1(DecodeArgs a) {
             uint32_t kv[8];
 #pragma unroll
             for (int d = 0; d < 4; ++d) kv_biased8(qs[st][d], kv[2 * d], kv[2 * d + 1]);
-            float d = sub_scale(hd[st], ib) * subblock_dot(kv, hv, hs);
+            float d = sub_scale(hd[st], ib) * subblock_dot_mix(kv, hv, hs);
             d = group_sum<LPR>(d);
             if (gsb == 0) part[wv][st * RPS + rr] = wq * d;
         }

@@ -190,6 +190,49 @@ __device__ __forceinline__ float subblock_dot(const uint32_t (&kv)[8], const flo
     return ((a0 + a1) + (a2 + a3)) - 128.f * xs;
 }
 
+// Biased codebook bytes b = kv + 128 (a kv_biased8 word, 4 weights) as two words of f16
+// pairs 1024 + b: exponent byte 0x64 over each byte (exact; b < 1024).
+__device__ __forceinline__ void kv_magic_f16(uint32_t bytes, uint32_t &p01, uint32_t &p23) {
+    p01 = __builtin_amdgcn_perm(0x64646464u, bytes, 0x04010400u);
+    p23 = __builtin_amdgcn_perm(0x64646464u, bytes, 0x04030402u);
+}
+
+// acc + w * x, w the low or high f16 half of a word, x and acc f32: one v_fma_mix_f32 (the
+// f16 widened exactly, one rounding) -- what fmaf((float)w, x, acc) computes, in one
+// instruction where the compiler emits a conversion and an FMA.
+__device__ __forceinline__ float fma_mix_lo(uint32_t w, float x, float acc) {
+    float d;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(w), "v"(x), "v"(acc));
+    return d;
+}
+__device__ __forceinline__ float fma_mix_hi(uint32_t w, float x, float acc) {
+    float d;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(w), "v"(x), "v"(acc));
+    return d;
+}
+
+// subblock_dot from the same kv_biased8 words, each as f16 pairs 1024 + b: one
+// v_fma_mix_f32 per weight instead of a byte conversion and an FMA; the offset 1024 + 128
+// comes off once, with the activations' sum xs.  Unscaled.
+__device__ __forceinline__ float subblock_dot_mix(const uint32_t (&kv)[8], const float (&xv)[32], float xs) {
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        uint32_t l01, l23, h01, h23;
+        kv_magic_f16(kv[2 * d], l01, l23);
+        kv_magic_f16(kv[2 * d + 1], h01, h23);
+        a0 = fma_mix_lo(l01, xv[4 * d + 0], a0);
+        a1 = fma_mix_hi(l01, xv[4 * d + 1], a1);
+        a2 = fma_mix_lo(l23, xv[4 * d + 2], a2);
+        a3 = fma_mix_hi(l23, xv[4 * d + 3], a3);
+        a0 = fma_mix_lo(h01, xv[16 + 4 * d + 0], a0);
+        a1 = fma_mix_hi(h01, xv[16 + 4 * d + 1], a1);
+        a2 = fma_mix_lo(h23, xv[16 + 4 * d + 2], a2);
+        a3 = fma_mix_hi(h23, xv[16 + 4 * d + 3], a3);
+    }
+    return ((a0 + a1) + (a2 + a3)) - 1152.f * xs;
+}
+
 // ---------------------------------------------------------------- split weight layout
 // The library's one resident copy of every bound matrix (k_repack_split): for a matrix of
 // `rows` rows of SBR super-blocks each,
