@@ -227,16 +227,16 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_m1(DecodeArgs a) {
     const int gsb = lane % LPR, rr = lane / LPR, sb = gsb >> 3, ib = gsb & 7;
     // the token's logit of this lane, then this lane's chunk of x (loads complete in order:
     // the routing waits for the logit only)
-    const float raw = a.logits ? ldg<float>(a.logits + min(64 * wv + lane, a.E - 1)) : 0.f;
+    float raw[4] = {0.f, 0.f, 0.f, 0.f};
+    if (a.logits) load_logits<4>(a.logits, a.E, lane, raw);
     f32x4 xv[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) xv[u] = ldg<f32x4>(a.x + 32 * gsb + 4 * u);
-    // routing of the token: lane p < 9 holds slot p
+    // routing of the token, by every wave alone (no barrier): lane p < 9 holds slot p
     int id;
     float wt = 1.0f;
     if (a.logits) {
-        __shared__ RouteLds R;
-        route_wg4v(raw, a.E, a.renorm, lane, wv, R, id, wt);
+        route_values<4>(raw, a.E, a.renorm, lane, id, wt);
     } else {
         id = lane < SLOTS ? (int)a.ids[lane] : 0;
     }
