@@ -326,7 +326,6 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
     __shared__ int s_abort;
     __shared__ int s_j;
     __shared__ uint32_t s_ep;
-    __shared__ RouteLds s_route[2]; // layers 0 and 1, routed by four waves each
     __shared__ __attribute__((aligned(16))) float s_lg[STK_LG_WORDS]; // AR: a layer's logits
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -355,29 +354,28 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
         }
     };
 
-    // Start: compute waves 0-3 route layer 0 and waves 4-7 layer 1 (route_wg4: two LDS
-    // barriers, which every wave of the workgroup passes); the router wave takes this
+    // Start: compute wave 0 routes layer 0 and wave 4 layer 1 (the one-wave top-8, no barrier);
+    // the router wave takes this
     // workgroup's rank j among the workgroups that started on XCD k -- a per-XCD ticket, not
     // blockIdx, so no assumption on the dispatch order -- and the launch epoch meanwhile.  An
     // XCD that receives more than NJ workgroups leaves another XCD short: the surplus ones
     // raise the timeout and leave, and the others' bounded waits end the launch with y
     // untouched.
     if (wv < NCW) {
-        if constexpr (AR) {
-            // nothing to route yet: the two barriers of route_wg4 only
-            lds_barrier();
-            lds_barrier();
-        } else {
+        if constexpr (!AR) {
             const int grp = wv >> 2, r = grp < n ? grp : 0;
-            const LayerPtrs L = load_layer(a.layers + a.layer0 + r);
-            int id;
-            float wt;
-            route_wg4(a.logits + (size_t)r * a.E, a.E, a.renorm, lane, wv & 3, s_route[grp], id, wt);
-            if ((wv & 3) == 0 && grp < n) ring_write(grp, id, wt, L);
+            if ((wv & 3) == 0) {
+                const LayerPtrs L = load_layer(a.layers + a.layer0 + r);
+                float raw[4];
+                load_logits<4>(a.logits + (size_t)r * a.E, a.E, lane, raw);
+                int id;
+                float wt;
+                route_values<4>(raw, a.E, a.renorm, lane, id, wt);
+                if (grp < n) ring_write(grp, id, wt, L);
+            }
         }
     } else {
-        // the ticket and the epoch are requested first and waited for only after the routing
-        // waves' two barriers
+        // the ticket and the epoch, waited for after the routing (B0 follows)
         const bool tk = wv == NCW && lane == 0;
         uint32_t t = 0u, e0 = 0u;
         if (tk) {
@@ -385,8 +383,6 @@ __global__ __launch_bounds__(64 * STK_WAVES) void k_decode_stack(StackArgs a) {
             e0 = __hip_atomic_load((const MOE_GLOBAL uint32_t *)ctl(STK_CTL_EPOCH), __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
         }
-        lds_barrier();
-        lds_barrier();
         if (tk) {
             s_j = t < (uint32_t)NJ ? (int)t : -1;
             s_ep = e0;
