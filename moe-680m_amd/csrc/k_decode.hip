@@ -208,8 +208,8 @@ __device__ __forceinline__ float rms_factor(int rmsnorm, float ss_wave, int H) {
 }
 
 // ---------------------------------------------------------------- gate/up, M = 1
-// No plan: the four waves of each workgroup route the token together (route_wg4, which agrees
-// with moe_router_topk bit for bit; two LDS-only barriers) or every wave reads the 9 ids; each
+// No plan: every wave routes the token alone (route_values, the one-wave top-8: the same ids
+// and weights as moe_router_topk bit for bit, no LDS, no barrier) or reads the 9 ids; each
 // wave checks them by the pair rule, quantizes the lane's chunk of x into registers, and runs
 // its steps.  Slot order
 // puts the shared expert first: u = 0 is slot 8, u = 1.. the valid routed slots ascending.
