@@ -61,6 +61,15 @@ __device__ __forceinline__ bool slot_kept(int id, int lane, int E, uint32_t &fl)
          (__ballot(lane < SLOTS && id <= E && dup) ? MOE_DEVFLAG_DUP_ID : 0u);
     return lane < SLOTS && id <= E && !dup;
 }
+// The same where the ids may come from the routing inside the launch (routed: wave-uniform):
+// routed ids are distinct indices below E and the shared id E, so every slot is kept.
+__device__ __forceinline__ bool slot_kept(bool routed, int id, int lane, int E, uint32_t &fl) {
+    if (routed) {
+        fl = 0u;
+        return lane < SLOTS;
+    }
+    return slot_kept(id, lane, E, fl);
+}
 
 // Kernel arguments a launch's chain needs, fetched at the kernel's first instructions: one asm
 // takes them all as inputs, so the compiler loads them there in one batch of scalar loads (and
@@ -241,7 +250,7 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_m1(DecodeArgs a) {
         id = lane < SLOTS ? (int)a.ids[lane] : 0;
     }
     uint32_t fl;
-    const bool ok = slot_kept(id, lane, a.E, fl);
+    const bool ok = slot_kept(a.logits != nullptr, id, lane, a.E, fl);
     const uint32_t vm = (uint32_t)__ballot(ok) & 0x1FFu;
     if (blockIdx.x == 0 && wv == 0) {
         if (a.logits && lane < SLOTS) {
@@ -342,7 +351,7 @@ __global__ __launch_bounds__(256) void k_dec_prep(DecodeArgs a) {
     }
     if (wv == 0) {
         uint32_t fl;
-        const bool ok = slot_kept(id, lane, a.E, fl);
+        const bool ok = slot_kept(a.logits != nullptr, id, lane, a.E, fl);
         const uint32_t vm = (uint32_t)__ballot(ok) & 0x1FFu;
         if (lane == 0) {
             P->vt[t] = vm;
@@ -458,7 +467,7 @@ __global__ __launch_bounds__(256) void k_dec_gate_up_mt(DecodeArgs a) {
             float wt = 0.f;
             if (a.logits) route_values<4>(raw[r], a.E, a.renorm, lane, id, wt);
             uint32_t fl;
-            const bool ok = slot_kept(id, lane, a.E, fl);
+            const bool ok = slot_kept(a.logits != nullptr, id, lane, a.E, fl);
             const uint32_t vm = (uint32_t)__ballot(ok) & 0x1FFu;
             if (lane < SLOTS) pid[t * SLOTS + lane] = (uint16_t)id;
             if (lane == 0) L.vt[t] = vm;

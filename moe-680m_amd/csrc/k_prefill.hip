@@ -232,12 +232,16 @@ __global__ __launch_bounds__(64 * PF_COUNT_TOKENS) void k_pf_count(PfCountArgs c
             id = lane < SLOTS ? (int)c.ids[(size_t)t * SLOTS + lane] : 0;
         }
     }
-    const bool bad = tok && lane < SLOTS && id > c.E;
+    // the pair rule for given ids; routed ids are E distinct indices and the shared id, so no
+    // slot of theirs is dropped (ROUTE skips the check)
+    const bool bad = !ROUTE && tok && lane < SLOTS && id > c.E;
     bool dup = false;
+    if constexpr (!ROUTE) {
 #pragma unroll
-    for (int s = 0; s < SLOTS - 1; ++s) {
-        const int o = __builtin_amdgcn_readlane(id, s);
-        dup = dup || (tok && s < lane && lane < SLOTS && !bad && o == id);
+        for (int s = 0; s < SLOTS - 1; ++s) {
+            const int o = __builtin_amdgcn_readlane(id, s);
+            dup = dup || (tok && s < lane && lane < SLOTS && !bad && o == id);
+        }
     }
     const bool keep = tok && lane < SLOTS && !bad && !dup;
     const uint64_t nb = __ballot(bad), nd = __ballot(dup), ns = __ballot(keep && id == c.E);
