@@ -203,7 +203,7 @@ __device__ __forceinline__ void prep_token(const PrefillArgs &a, int t, int lane
 //       position -- with the prep of PF_PREP_TOKENS tokens per workgroup in the others.
 // The counters start at zero and k_pf_combine, the chain's last launch, zeroes them again.
 // The shared expert's bucket has no counter: token t's shared row is row t of it.
-constexpr int PF_COUNT_TOKENS = 16; // tokens per counting workgroup (one wave each; 4 measured slower at M = 4096)
+constexpr int PF_COUNT_TOKENS = 8; // tokens per counting workgroup, one wave each (16: 6.3 against 5.1 us at M = 512; 4: 10.3 against 8.7 us at M = 4096)
 constexpr uint32_t PF_SLOT_HOLE = 0xFFFFFFFEu; // slot 8 of a token with no kept shared slot
 
 template <bool ROUTE>
