@@ -274,8 +274,8 @@ __global__ __launch_bounds__(64 * PF_COUNT_TOKENS) void k_pf_count(PfCountArgs c
 // 2- and 4-byte stores, and per wave 64 cache lines touched by each of a token's 8 loads and 4
 // stores -- so they are spread over many CUs (measured, M = 512: 9.1 us for the launch with
 // 4096 slots and 16 tokens per workgroup).
-constexpr int PF_PLACE_SLOTS = 1024;
-constexpr int PF_PREP_TOKENS = 4;
+constexpr int PF_PLACE_SLOTS = 512; // slots per placing workgroup (1024: 12.8 against 12.3 us at M = 4096)
+constexpr int PF_PREP_TOKENS = 4; // tokens per prep workgroup, one wave each (16: 14.0 against 12.8 us at M = 4096)
 
 template <int H>
 __global__ __launch_bounds__(BF_THREADS) void k_pf_place(BucketArgs b, PfCountArgs c, PrefillArgs a) {
